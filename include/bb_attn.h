@@ -1,0 +1,116 @@
+/*
+ * bb_attn -- C ABI of the MI355X-native Bigger Bird v3 sparse prefill path (gfx950 HIP kernels).
+ *
+ * Conventions
+ *   - Every tensor argument is a device pointer plus element strides (int64); the innermost (head_dim) stride is 1.
+ *     bf16 tensors are passed as raw 16-bit storage.
+ *   - All launches are asynchronous on `stream` (a hipStream_t; NULL = the null stream). Nothing synchronises the
+ *     host, nothing allocates or frees device memory: callers pass any workspace the *_workspace() query asks for.
+ *   - Return value: 0 on success; BB_EINVAL (-1) for an argument error, whose message (bb_last_error()) matches the
+ *     reference's ValueError text where the reference raises one; BB_EHIP (-2) when a HIP launch fails.
+ *   - Functions are re-entrant; bb_last_error() is per host thread.
+ */
+#ifndef BB_ATTN_H
+#define BB_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BB_OK 0
+#define BB_EINVAL (-1)
+#define BB_EHIP (-2)
+
+/* Library version (major * 10000 + minor * 100 + patch). */
+int bb_version(void);
+
+/* Message of the last failed call on this host thread ("" if none). */
+const char* bb_last_error(void);
+
+/*
+ * Sparse flash attention: one joint softmax over front anchors | causal local window | routed keys.
+ * Replaces bigger_bird_flash(q, k, v, indices, front=, window=, token_mask=, num_heads=, route_chunk=, kv_groups=,
+ * scale=) of kernels/bigger_bird_flash.py:99-138 (and its dispatch at modal_rd/attention.py:41-45).
+ *   q    [BH, T, D]   strides sq[3]          k, v [BH / kv_groups, N, D]   strides sk[3], sv[3]
+ *   idx  [BH, n_groups, route_k] int32 (-1 = empty), strides si[3]; may be NULL when route_k == 0
+ *   key_mask [B, N] uint8 (B = BH / num_heads, row stride smb) or NULL        (token_mask)
+ *   out  [BH, T, D]   strides so[3]          (e.g. a permuted view of a [T, BH, D] buffer)
+ *   Query row t sits at absolute position t + N - T. Rows >= row_end are not written (row_end = T for all rows).
+ *   D in {32, 64, 128}; bf16 only; scale > 0.
+ *   vt   optional V^T from bb_transpose_v (NULL: transposed into the workspace).
+ *   ws/ws_bytes: workspace of at least bb_sparse_flash_workspace(...) bytes (V^T unless given, plus the (O, m, l)
+ *   partials of the split-key schedule used for long windows without routes).
+ */
+int bb_sparse_flash(const void* q, const int64_t* sq, const void* k, const int64_t* sk, const void* v,
+                    const int64_t* sv, const void* vt, const int32_t* idx, const int64_t* si, int n_groups,
+                    int route_k, const uint8_t* key_mask, int64_t smb, void* out, const int64_t* so, int BH, int64_t T,
+                    int64_t N, int D, int num_heads, int kv_groups, int64_t front, int64_t window,
+                    int64_t route_chunk, float scale, int64_t row_end, void* ws, size_t ws_bytes, void* stream);
+
+/* Workspace bytes for bb_sparse_flash; have_vt != 0 when the caller passes a precomputed V^T. */
+size_t bb_sparse_flash_workspace(int BH, int64_t T, int64_t N, int D, int num_heads, int kv_groups, int64_t front,
+                                 int64_t window, int route_k, int64_t row_end, int have_vt);
+
+/*
+ * V [n_kvbh, N, D] (strides sv[3]) -> V^T [n_kvbh, D, bb_transpose_v_cols(N)] with zero columns past N: the layout
+ * the window tiles stream from. A caller making several bb_sparse_flash calls over the same V (prefill main pass
+ * and exact tail) transposes once and passes the result as `vt`. No reference counterpart (the reference's Triton
+ * kernel reads V in place).
+ */
+int bb_transpose_v(const void* v, const int64_t* sv, int n_kvbh, int64_t N, int D, void* vt, void* stream);
+int64_t bb_transpose_v_cols(int64_t N);
+
+/*
+ * Routing: per query head, the `budget` key columns with the largest mean (pool_max = 0) or max (pool_max = 1)
+ * softmax probability over the r route queries at positions qpos, among columns [sink, n - window); returned
+ * ascending as int32 in idx_out [B*H, budget]. Replaces RDAttention.routes (modal_rd/attention.py:143-174).
+ *   q [B*H, n, D] (strides sq[2]: head, token), k [B*Hkv, n, D] (strides sk[2]); qpos [r] int64 on the device.
+ *   pooled_out: optional [B*H, n] uint64 copy of the pooled scores in units of 2^-40 (NULL to skip).
+ *   Arithmetic is deterministic (exact bf16 scores, fixed-point sums); results are identical on every run.
+ */
+int bb_routes(const void* q, const int64_t* sq, const void* k, const int64_t* sk, const int64_t* qpos, int r,
+              int B, int H, int Hkv, int64_t n, int D, int64_t sink, int64_t window, int budget, float scaling,
+              int pool_max, int32_t* idx_out, uint64_t* pooled_out, void* ws, size_t ws_bytes, void* stream);
+
+size_t bb_routes_workspace(int64_t n, int H, int Hkv, int B, int r);
+
+/*
+ * Per-row symmetric int8 quantisation of rows (outer, inner) at x + outer*row_stride + inner*inner_stride,
+ * D contiguous elements each, written token-major: q [outer*inner, D], scale [outer*inner] (fp16 or fp32).
+ * Replaces modal_rd/kv_int8.py:19-22 / kernels/kv_int8_triton.py:36-51.
+ */
+int bb_int8_quantize(const void* x, int x_is_f32, int64_t outer, int64_t row_stride, int inner, int64_t inner_stride,
+                     int D, float min_scale, int8_t* q, void* scale, int scale_is_f16, void* stream);
+
+/* q [rows, D] int8 * scale [rows] -> out [rows, D] (bf16 or fp32). Replaces modal_rd/kv_int8.py:25-26. */
+int bb_int8_dequantize(const int8_t* q, const void* scale, int scale_is_f16, int64_t rows, int D, void* out,
+                       int out_is_f32, void* stream);
+
+/*
+ * Exact attention of one decode token over the first n rows of a KV cache: out [H, D] bf16 from q [H, D] bf16.
+ * int8 cache: k8/v8 [cap, Hkv, D] token-major with scales ks/vs [cap, Hkv] (fp16 if scale_is_f16 else fp32).
+ * bf16 cache (k8 == NULL): kb/vb [Hkv, cap, D] with strides skb[2], svb[2] (head, token).
+ * Replaces RDAttention.exact_attention (modal_rd/attention.py:137-141) over Int8KVLayer's dequantised cache.
+ */
+int bb_decode(const void* q, int64_t sq, const int8_t* k8, const void* ks, const int8_t* v8, const void* vs,
+              int scale_is_f16, const void* kb, const int64_t* skb, const void* vb, const int64_t* svb, int64_t n,
+              int H, int Hkv, int D, float scale, void* out, int64_t so, void* ws, size_t ws_bytes, void* stream);
+
+size_t bb_decode_workspace(int64_t n, int H, int Hkv, int D);
+
+/*
+ * In-place RoPE on x [B, Hh, T, D] (strides sx[3]) with cos/sin [B, T, D] (strides sc[2]; 0 to broadcast), with
+ * the arithmetic of HF apply_rotary_pos_emb on bf16 tensors (bit-identical). Replaces rope_inplace
+ * (modal_rd/attention.py:51-60).
+ */
+int bb_rope_inplace(void* x, const int64_t* sx, int B, int Hh, int64_t T, int D, const void* cos, const void* sin,
+                    const int64_t* sc, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BB_ATTN_H */

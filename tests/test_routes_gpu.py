@@ -1,0 +1,69 @@
+"""bb_routes (HIP) against the CPU oracle: the deterministic contract makes them bit-identical, so route indices
+are compared set-exactly (sorted int32 equality) and the pooled fixed-point scores value-exactly."""
+import pytest
+import torch
+
+import oracle
+from bigger_bird_amd.attention import routes as hip_routes
+from bigger_bird_amd.synth import make_inputs
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    # name, T, H, Hkv, d, sink, window, budget, n_route, pool, queries, planted
+    ("small_d64", 1024, 8, 2, 64, 16, 256, 64, 64, "mean", "last", 0),
+    ("odd_len_d128", 3001, 8, 2, 128, 64, 512, 100, 64, "mean", "last", 8),
+    ("max_pool", 2048, 16, 4, 128, 64, 512, 128, 64, "max", "last", 0),
+    ("spread", 2048, 16, 4, 128, 64, 512, 128, 64, "mean", "spread", 0),
+    ("mha_d32", 777, 4, 4, 32, 8, 96, 24, 16, "mean", "last", 0),
+    ("config1", 8192, 32, 8, 128, 64, 2048, 128, 64, "mean", "last", 64),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_routes_bit_exact(case, dev):
+    name, T, H, Hkv, d, sink, window, budget, nr, pool, qmode, planted = case
+    print(f"case {name}", flush=True)
+    inp = make_inputs(T, H, Hkv, d, seed=3, window=window, sink=sink, planted=planted)
+    q, k = inp["q"], inp["k"]
+    idx, pooled = hip_routes(q.to(dev), k.to(dev), num_heads=H, num_kv_heads=Hkv, sink=sink, window=window,
+                             budget=budget, n_route=nr, route_pool=pool, route_queries=qmode, scaling=d ** -0.5,
+                             return_pooled=True)
+    torch.cuda.synchronize()
+    r = min(nr, T)
+    qpos = (torch.linspace(sink + window, T - 1, r).long() if qmode == "spread" else torch.arange(T - r, T))
+    want, want_pooled = oracle.routes(q[0], k[0], sink=sink, window=window, budget=budget, scaling=d ** -0.5,
+                                      n_route=nr, route_pool=pool, qpos=qpos, return_pooled=True)
+    got = idx.cpu()
+    assert torch.equal(got, want), f"{name}: route indices differ"
+    scale = 2.0 ** -40 / (r if pool == "mean" else 1)
+    prob = (want_pooled.double() * scale).float()
+    lo, hi = sink, T - window  # pooled scores are defined on the eligible columns
+    assert torch.equal(pooled.cpu()[:, lo:hi], prob[:, lo:hi]), f"{name}: pooled scores differ"
+    if planted:
+        for h in range(H):
+            assert set(inp["planted_pos"][0, h // (H // Hkv)].tolist()) <= set(got[h].tolist()), "planted key missed"
+
+
+def test_ties_go_to_lower_index(dev):
+    """Identical keys give identical pooled probabilities; the lower index must win (the contract's tie-break)."""
+    print("case ties", flush=True)
+    T, H, Hkv, d, sink, window, budget = 512, 4, 1, 64, 8, 64, 10
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(1, H, T, d, generator=g).to(torch.bfloat16)
+    k = torch.randn(1, Hkv, T, d, generator=g).to(torch.bfloat16)
+    k[0, 0, sink:T - window] = k[0, 0, 100]  # every eligible key identical -> all pooled values tie
+    idx = hip_routes(q.to(dev), k.to(dev), num_heads=H, num_kv_heads=Hkv, sink=sink, window=window, budget=budget,
+                     scaling=d ** -0.5).cpu()
+    want = torch.arange(sink, sink + budget, dtype=torch.int32).expand(H, -1)
+    assert torch.equal(idx, want)
+
+
+def test_budget_covers_all_eligible(dev):
+    """budget == n - sink - window -> every eligible column (modal_rd/selfcheck.py:38)."""
+    print("case full_budget_routes", flush=True)
+    T, H, Hkv, d, sink, window = 700, 8, 2, 128, 16, 128
+    inp = make_inputs(T, H, Hkv, d, seed=9, window=window)
+    idx = hip_routes(inp["q"].to(dev), inp["k"].to(dev), num_heads=H, num_kv_heads=Hkv, sink=sink, window=window,
+                     budget=T - sink - window, scaling=d ** -0.5).cpu()
+    assert torch.equal(idx, torch.arange(sink, T - window, dtype=torch.int32).expand(H, -1))

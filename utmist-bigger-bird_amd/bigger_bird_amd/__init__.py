@@ -1,0 +1,13 @@
+"""bigger_bird_amd -- MI355X-native Bigger Bird v3 sparse prefill attention (gfx950 HIP kernels behind a C ABI).
+
+Public surface (mirrors the reference's modal_rd.attention / kernels.bigger_bird_flash / modal_rd.kv_int8):
+  RDAttention, install, rope_inplace, vertical_budget, routes        -- attention module and routing
+  bigger_bird_flash, transpose_v                                      -- the sparse attention operator
+  quantize, dequantize, Int8KVLayer, make_int8_cache, decode_int8     -- INT8 KV cache and exact decode
+"""
+from .attention import RDAttention, install, rope_inplace, routes, vertical_budget
+from .flash import bigger_bird_flash, transpose_v
+from .kv_int8 import Int8KVLayer, decode_bf16, decode_int8, dequantize, make_int8_cache, quantize
+
+__all__ = ["RDAttention", "install", "rope_inplace", "routes", "vertical_budget", "bigger_bird_flash", "transpose_v",
+           "Int8KVLayer", "decode_bf16", "decode_int8", "dequantize", "make_int8_cache", "quantize"]

@@ -1,0 +1,341 @@
+// C ABI of libbb_attn: argument validation (reference error texts), schedule selection, kernel launches.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+
+#include "../../include/bb_attn.h"
+#include "bb_internal.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return BB_EINVAL;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return BB_OK;
+  snprintf(g_err, sizeof(g_err), "%s: %s", what, hipGetErrorString(e));
+  return BB_EHIP;
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Work schedule of the sparse flash kernel.
+struct FlashSchedule {
+  int hpw, head_splits, row_tiles, n_chunks;
+  int64_t key_chunk;
+  bool split;
+};
+
+constexpr int kCUs = 256;
+
+// Waves per flash workgroup: 8 (32 query rows per wave, two waves per SIMD) or 4 (64 rows, one per SIMD).
+// BB_FLASH_WAVES=4 selects the latter for measurement.
+int flash_waves() {
+  static int w = [] {
+    const char* e = getenv("BB_FLASH_WAVES");
+    int v = e ? atoi(e) : 8;
+    return v == 4 ? 4 : 8;
+  }();
+  return w;
+}
+
+FlashSchedule flash_schedule(int BH, int64_t T, int64_t N, int num_heads, int kv_groups, int64_t front, int64_t window,
+                             int route_k, int64_t row_end) {
+  FlashSchedule s;
+  const int G = kv_groups;
+  s.hpw = (G % 4 == 0) ? 4 : (G % 2 == 0) ? 2 : 1;
+  s.head_splits = G / s.hpw;
+  const int64_t R = 64 * (4 / s.hpw);
+  const int64_t rows = row_end < T ? row_end : T;
+  s.row_tiles = (int)cdiv(rows > 0 ? rows : 0, R);
+  const int64_t n_kvbh = BH / G;
+  const int64_t items = n_kvbh * s.head_splits * s.row_tiles;
+  int64_t span = (window < N ? window : N) + R;  // keys per item (window part)
+  s.split = false;
+  s.n_chunks = 1;
+  s.key_chunk = N;
+  (void)front;
+  (void)num_heads;
+  if (route_k == 0 && items > 0 && items < 2 * kCUs && span / 64 > 32) {
+    int64_t want = cdiv(2 * kCUs, items);
+    int64_t max_chunks = cdiv(N, 4096);
+    int64_t nc = want < max_chunks ? want : max_chunks;
+    if (nc > 1) {
+      s.key_chunk = cdiv(cdiv(N, nc), 64) * 64;
+      s.n_chunks = (int)cdiv(N, s.key_chunk);
+      s.split = s.n_chunks > 1;
+      if (!s.split) {
+        s.n_chunks = 1;
+        s.key_chunk = N;
+      }
+    }
+  }
+  return s;
+}
+
+}  // namespace
+
+extern "C" {
+
+int bb_version(void) { return 100; }
+
+const char* bb_last_error(void) { return g_err; }
+
+int64_t bb_transpose_v_cols(int64_t N) { return cdiv(N > 0 ? N : 1, 64) * 64; }
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+size_t bb_sparse_flash_workspace(int BH, int64_t T, int64_t N, int D, int num_heads, int kv_groups, int64_t front,
+                                 int64_t window, int route_k, int64_t row_end, int have_vt) {
+  if (BH <= 0 || T <= 0 || N <= 0 || kv_groups <= 0 || BH % kv_groups) return 0;
+  if (row_end <= 0 || row_end > T) row_end = T;
+  FlashSchedule s = flash_schedule(BH, T, N, num_heads, kv_groups, front, window, route_k, row_end);
+  size_t bytes = 0;
+  if (!have_vt) bytes += align256((size_t)(BH / kv_groups) * D * bb_transpose_v_cols(N) * 2);
+  if (s.split) bytes += (size_t)s.n_chunks * BH * T * (size_t)(D + 2) * sizeof(float);
+  return bytes;
+}
+
+int bb_transpose_v(const void* v, const int64_t* sv, int n_kvbh, int64_t N, int D, void* vt, void* stream) {
+  g_err[0] = 0;
+  if (!v || !sv || !vt) return fail("transpose_v: null argument");
+  if (D != 32 && D != 64 && D != 128) return fail("head_dim %d unsupported (32, 64 or 128)", D);
+  if (!aligned(v, 16) || !aligned(vt, 16) || sv[0] % 8 || sv[1] % 8 || sv[2] != 1)
+    return fail("q/k/v need a contiguous head_dim and 16-byte aligned rows");
+  return hip_status(bb::launch_transpose_v(static_cast<const uint16_t*>(v), sv[0], sv[1], n_kvbh, N,
+                                           bb_transpose_v_cols(N), D, static_cast<uint16_t*>(vt),
+                                           static_cast<hipStream_t>(stream)),
+                    "bb_transpose_v");
+}
+
+int bb_sparse_flash(const void* q, const int64_t* sq, const void* k, const int64_t* sk, const void* v,
+                    const int64_t* sv, const void* vt, const int32_t* idx, const int64_t* si, int n_groups,
+                    int route_k, const uint8_t* key_mask, int64_t smb, void* out, const int64_t* so, int BH, int64_t T,
+                    int64_t N, int D, int num_heads, int kv_groups, int64_t front, int64_t window,
+                    int64_t route_chunk, float scale, int64_t row_end, void* ws, size_t ws_bytes, void* stream) {
+  g_err[0] = 0;
+  if (!q || !k || !v || !out || !sq || !sk || !sv || !so)
+    return fail("Q [BH,T,D] and K/V [BH/kv_groups,N,D] must have matching heads and dimensions");
+  if (kv_groups <= 0 || num_heads <= 0 || BH <= 0 || BH % kv_groups || num_heads % kv_groups || BH % num_heads)
+    return fail("Q [BH,T,D] and K/V [BH/kv_groups,N,D] must have matching heads and dimensions");
+  if (D != 32 && D != 64 && D != 128) return fail("head_dim %d unsupported (32, 64 or 128)", D);
+  if (front < 0 || window < 1) return fail("front >= 0 and window >= 1 required");
+  if (T > N) return fail("Key sequence must be at least as long as query sequence");
+  if (T <= 0) return BB_OK;
+  if (route_k < 0 || (route_k > 0 && (!idx || !si || n_groups <= 0)))
+    return fail("Routing groups must cover the sequence and align with query tiles");
+  if (route_chunk <= 0 || (route_k > 0 && n_groups != cdiv(N, route_chunk)))
+    return fail("Routing groups must cover the sequence and align with query tiles");
+  if (!(scale > 0.0f)) return fail("scale must be positive");
+  // 16-byte operand loads, 8-byte output stores
+  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || sq[0] % 8 || sq[1] % 8 || sk[0] % 8 || sk[1] % 8 ||
+      sv[0] % 8 || sv[1] % 8 || sq[2] != 1 || sk[2] != 1 || sv[2] != 1)
+    return fail("q/k/v need a contiguous head_dim and 16-byte aligned rows");
+  if (!aligned(out, 8) || so[0] % 4 || so[1] % 4 || so[2] != 1)
+    return fail("out needs a contiguous head_dim and 8-byte aligned rows");
+  if (front > N) front = N;
+  if (row_end <= 0 || row_end > T) row_end = T;
+
+  FlashSchedule s = flash_schedule(BH, T, N, num_heads, kv_groups, front, window, route_k, row_end);
+  bb::FlashParams p;
+  memset(&p, 0, sizeof(p));
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.idx = idx;
+  p.key_mask = key_mask;
+  p.out = static_cast<uint16_t*>(out);
+  p.sq0 = sq[0]; p.sq1 = sq[1];
+  p.sk0 = sk[0]; p.sk1 = sk[1];
+  p.sv0 = sv[0]; p.sv1 = sv[1];
+  if (si) { p.si0 = si[0]; p.si1 = si[1]; p.si2 = si[2]; }
+  p.smb = smb;
+  p.so0 = so[0]; p.so1 = so[1];
+  p.N = N; p.T = T; p.offset = N - T; p.row_end = row_end;
+  p.route_chunk = route_chunk;
+  p.key_chunk = s.key_chunk;
+  p.BH = BH; p.H = num_heads; p.G = kv_groups; p.Hkv_pb = num_heads / kv_groups; p.n_kvbh = BH / kv_groups;
+  p.front = (int)front;
+  p.window = (int)(window > N + 1 ? N + 1 : window);
+  p.route_k = route_k;
+  p.n_groups = n_groups > 0 ? n_groups : 1;
+  p.row_tiles = s.row_tiles;
+  p.head_splits = s.head_splits;
+  p.n_chunks = s.n_chunks;
+  p.remap = ((int64_t)p.n_kvbh * s.head_splits) % 8 == 0;
+  p.waves = flash_waves();
+  p.np = bb_transpose_v_cols(N);
+  p.c = (float)((double)scale * 1.4426950408889634);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const size_t need = bb_sparse_flash_workspace(BH, T, N, D, num_heads, kv_groups, front, window, route_k, row_end,
+                                                vt != nullptr);
+  if (need && (!ws || ws_bytes < need)) return fail("workspace of %zu bytes required", need);
+  char* wsp = static_cast<char*>(ws);
+  if (vt) {
+    if (!aligned(vt, 16)) return fail("vt must be 16-byte aligned");
+    p.vt = static_cast<const uint16_t*>(vt);
+  } else {
+    uint16_t* vt_ws = reinterpret_cast<uint16_t*>(wsp);
+    wsp += align256((size_t)p.n_kvbh * D * p.np * 2);
+    hipError_t e = bb::launch_transpose_v(p.v, p.sv0, p.sv1, p.n_kvbh, N, p.np, D, vt_ws, st);
+    if (e != hipSuccess) return hip_status(e, "bb_sparse_flash transpose");
+    p.vt = vt_ws;
+  }
+  if (s.split) {
+    p.part_o = reinterpret_cast<float*>(wsp);
+    p.part_ml = p.part_o + (size_t)s.n_chunks * BH * T * D;
+    hipError_t e = bb::launch_flash(p, D, s.hpw, true, st);
+    if (e != hipSuccess) return hip_status(e, "bb_sparse_flash split kernel");
+    return hip_status(bb::launch_flash_merge(p, D, st), "bb_sparse_flash merge kernel");
+  }
+  return hip_status(bb::launch_flash(p, D, s.hpw, false, st), "bb_sparse_flash kernel");
+}
+
+size_t bb_routes_workspace(int64_t n, int H, int Hkv, int B, int r) {
+  if (n <= 0 || H <= 0 || Hkv <= 0 || H % Hkv || B <= 0 || r <= 0) return 0;
+  return bb::routes_workspace_bytes(n, H, Hkv, B, r);
+}
+
+int bb_routes(const void* q, const int64_t* sq, const void* k, const int64_t* sk, const int64_t* qpos, int r, int B,
+              int H, int Hkv, int64_t n, int D, int64_t sink, int64_t window, int budget, float scaling, int pool_max,
+              int32_t* idx_out, uint64_t* pooled_out, void* ws, size_t ws_bytes, void* stream) {
+  g_err[0] = 0;
+  if (!q || !k || !qpos || !sq || !sk) return fail("routes: null argument");
+  if (H <= 0 || Hkv <= 0 || H % Hkv || B <= 0 || n <= 0 || r <= 0) return fail("routes: bad head/sequence sizes");
+  if (D != 32 && D != 64 && D != 128) return fail("head_dim %d unsupported (32, 64 or 128)", D);
+  if (H / Hkv * r > 4096) return fail("routes: groups * n_route must be <= 4096");
+  if (!aligned(q, 16) || !aligned(k, 16) || sq[0] % 8 || sq[1] % 8 || sk[0] % 8 || sk[1] % 8)
+    return fail("q/k need a contiguous head_dim and 16-byte aligned rows");
+  int64_t lo = sink < n ? (sink > 0 ? sink : 0) : n;
+  int64_t hi = n - window;
+  if (hi > n) hi = n;
+  const int64_t eligible = hi > lo ? hi - lo : 0;
+  if (budget < 0 || budget > eligible) return fail("routes: budget %d exceeds %lld eligible columns", budget, (long long)eligible);
+  if (budget > 0 && !idx_out) return fail("routes: idx_out required");
+  if (!(scaling > 0.0f)) return fail("scaling must be positive");
+  const size_t need = bb::routes_workspace_bytes(n, H, Hkv, B, r);
+  if (!ws || ws_bytes < need) return fail("workspace of %zu bytes required", need);
+  bb::RoutesParams p;
+  memset(&p, 0, sizeof(p));
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.qpos = qpos;
+  p.sq0 = sq[0]; p.sq1 = sq[1]; p.sk0 = sk[0]; p.sk1 = sk[1];
+  p.n = n; p.H = H; p.Hkv = Hkv; p.B = B; p.D = D; p.r = r;
+  p.sink = (int)(sink < n ? sink : n);
+  p.window = (int)(window < n ? window : n);
+  p.budget = budget; p.pool_max = pool_max; p.scaling = scaling;
+  p.out_idx = idx_out;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e = bb::launch_routes(p, ws, ws_bytes, st);
+  if (e != hipSuccess) return hip_status(e, "bb_routes");
+  if (pooled_out) {
+    e = hipMemcpyAsync(pooled_out, p.pooled, (size_t)B * H * n * sizeof(uint64_t), hipMemcpyDeviceToDevice, st);
+    if (e != hipSuccess) return hip_status(e, "bb_routes pooled copy");
+  }
+  return BB_OK;
+}
+
+int bb_int8_quantize(const void* x, int x_is_f32, int64_t outer, int64_t row_stride, int inner, int64_t inner_stride,
+                     int D, float min_scale, int8_t* q, void* scale, int scale_is_f16, void* stream) {
+  g_err[0] = 0;
+  if (!x || !q || !scale) return fail("quantize: null argument");
+  if (D != 32 && D != 64 && D != 128 && D != 256) return fail("quantize: head_dim %d unsupported", D);
+  const int64_t el = x_is_f32 ? 4 : 2;
+  if (!aligned(x, 16) || (row_stride * el) % 16 || (inner_stride * el) % 16 || !aligned(q, 8))
+    return fail("quantize: rows must be 16-byte aligned");
+  return hip_status(bb::launch_int8_quantize(x, x_is_f32, outer, row_stride, inner, inner_stride, D, min_scale, q, scale,
+                                             scale_is_f16, static_cast<hipStream_t>(stream)),
+                    "bb_int8_quantize");
+}
+
+int bb_int8_dequantize(const int8_t* q, const void* scale, int scale_is_f16, int64_t rows, int D, void* out,
+                       int out_is_f32, void* stream) {
+  g_err[0] = 0;
+  if (!q || !scale || !out) return fail("dequantize: null argument");
+  if (D != 32 && D != 64 && D != 128 && D != 256) return fail("dequantize: head_dim %d unsupported", D);
+  if (!aligned(q, 8) || !aligned(out, 16)) return fail("dequantize: misaligned buffers");
+  return hip_status(bb::launch_int8_dequantize(q, scale, scale_is_f16, rows, D, out, out_is_f32,
+                                               static_cast<hipStream_t>(stream)),
+                    "bb_int8_dequantize");
+}
+
+static int decode_splits(int64_t n, int Hkv) {
+  int64_t want = cdiv(4 * kCUs, Hkv);
+  int64_t by_len = cdiv(n, 256);
+  int64_t s = want < by_len ? want : by_len;
+  return (int)(s < 1 ? 1 : s);
+}
+
+size_t bb_decode_workspace(int64_t n, int H, int Hkv, int D) {
+  if (n <= 0 || Hkv <= 0) return 0;
+  return bb::decode_workspace_bytes(H, D, decode_splits(n, Hkv));
+}
+
+int bb_decode(const void* q, int64_t sq, const int8_t* k8, const void* ks, const int8_t* v8, const void* vs,
+              int scale_is_f16, const void* kb, const int64_t* skb, const void* vb, const int64_t* svb, int64_t n,
+              int H, int Hkv, int D, float scale, void* out, int64_t so, void* ws, size_t ws_bytes, void* stream) {
+  g_err[0] = 0;
+  if (!q || !out) return fail("decode: null argument");
+  if (n <= 0) return fail("decode: empty cache");
+  if (H <= 0 || Hkv <= 0 || H % Hkv) return fail("q [H,D] and k/v [Hkv,N,D] must match");
+  const int G = H / Hkv;
+  if (G != 1 && G != 2 && G != 4 && G != 8) return fail("decode: groups %d unsupported", G);
+  if (D != 64 && D != 128) return fail("decode: head_dim %d unsupported (64 or 128)", D);
+  const bool int8 = k8 != nullptr;
+  if (int8 && (!v8 || !ks || !vs)) return fail("decode: int8 cache needs k8, v8 and scales");
+  if (!int8 && (!kb || !vb || !skb || !svb)) return fail("decode: bf16 cache needs kb, vb and strides");
+  if (int8 && (!aligned(k8, 16) || !aligned(v8, 16))) return fail("decode: misaligned cache");
+  if (!int8 && (!aligned(kb, 16) || !aligned(vb, 16) || skb[0] % 8 || skb[1] % 8 || svb[0] % 8 || svb[1] % 8))
+    return fail("decode: misaligned cache");
+  if (!(scale > 0.0f)) return fail("scale must be positive");
+  bb::DecodeParams p;
+  memset(&p, 0, sizeof(p));
+  p.q = static_cast<const uint16_t*>(q);
+  p.sq = sq;
+  p.k8 = k8; p.v8 = v8; p.ks = ks; p.vs = vs;
+  p.kb = static_cast<const uint16_t*>(kb);
+  p.vb = static_cast<const uint16_t*>(vb);
+  if (skb) { p.skb0 = skb[0]; p.skb1 = skb[1]; }
+  if (svb) { p.svb0 = svb[0]; p.svb1 = svb[1]; }
+  p.n = n; p.H = H; p.Hkv = Hkv; p.D = D; p.scale_is_f16 = scale_is_f16;
+  p.n_splits = decode_splits(n, Hkv);
+  p.split_len = cdiv(n, p.n_splits);
+  p.n_splits = (int)cdiv(n, p.split_len);
+  p.c = (float)((double)scale * 1.4426950408889634);
+  p.out = static_cast<uint16_t*>(out);
+  p.so = so;
+  const size_t need = bb::decode_workspace_bytes(H, D, decode_splits(n, Hkv));
+  if (!ws || ws_bytes < need) return fail("workspace of %zu bytes required", need);
+  p.part = static_cast<float*>(ws);
+  (void)G;
+  return hip_status(bb::launch_decode(p, static_cast<hipStream_t>(stream)), "bb_decode");
+}
+
+int bb_rope_inplace(void* x, const int64_t* sx, int B, int Hh, int64_t T, int D, const void* cos, const void* sin,
+                    const int64_t* sc, void* stream) {
+  g_err[0] = 0;
+  if (!x || !cos || !sin || !sx || !sc) return fail("rope: null argument");
+  if (D % 16) return fail("rope: head_dim must be a multiple of 16");
+  if (!aligned(x, 16) || !aligned(cos, 16) || !aligned(sin, 16) || sx[0] % 8 || sx[1] % 8 || sx[2] % 8 || sc[0] % 8 ||
+      sc[1] % 8)
+    return fail("rope: rows must be 16-byte aligned");
+  return hip_status(bb::launch_rope(static_cast<uint16_t*>(x), sx[0], sx[1], sx[2], B, Hh, T, D,
+                                    static_cast<const uint16_t*>(cos), static_cast<const uint16_t*>(sin), sc[0], sc[1],
+                                    static_cast<hipStream_t>(stream)),
+                    "bb_rope_inplace");
+}
+
+}  // extern "C"

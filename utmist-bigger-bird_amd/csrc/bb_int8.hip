@@ -1,0 +1,367 @@
+// INT8 KV cache kernels (modal_rd/kv_int8.py:15-26 and kernels/kv_int8_triton.py:14-33 of the reference) and the
+// fused exact decode over the int8 cache (modal_rd/attention.py:137-141 run on the dequantised cache there).
+//
+//   quantize    scale = max(absmax(row) / 127, min_scale) in fp32 (correctly rounded divide), q = rint(x / scale)
+//               clamped to [-127, 127]; the scale is stored as fp16 (RNE, the reference's format) or fp32.
+//   dequantize  q * float(scale) -> bf16 (RNE) or fp32.
+//   decode      one query token per head against n cached rows, K/V read as int8 straight from the token-major
+//               cache [cap, Hkv, D] (no dequantised copy): flash-decoding split over keys, each workgroup owns one
+//               KV head and a key range and serves all G query heads of that group, so every K/V byte is read once.
+#include <hip/hip_fp16.h>
+
+#include "bb_common.h"
+#include "bb_internal.h"
+
+namespace bb {
+namespace {
+
+BB_DEV float load_scale(const void* s, int64_t i, int is_f16) {
+  if (is_f16) return __half2float(reinterpret_cast<const __half*>(s)[i]);
+  return reinterpret_cast<const float*>(s)[i];
+}
+
+// One group of D/8 lanes per row, 8 elements per lane.
+template <int D>
+__global__ __launch_bounds__(256) void quantize_kernel(const void* __restrict__ x, int x_is_f32, int64_t rows,
+                                                       int64_t row_stride, int inner, int64_t inner_stride,
+                                                       float min_scale, int8_t* __restrict__ qo, void* __restrict__ so,
+                                                       int scale_is_f16) {
+  constexpr int LPR = D / 8;
+  constexpr int RPB = 256 / LPR;
+  const int lane_in_row = threadIdx.x % LPR;
+  const int64_t r = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR;  // flat row = outer * inner + inner_idx
+  const int64_t total = rows * inner;
+  const bool valid = r < total;
+  float v[8];
+  if (valid) {
+    const int64_t outer = r / inner, in = r % inner;
+    const int64_t off = outer * row_stride + in * inner_stride + 8 * lane_in_row;
+    if (x_is_f32) {
+      const float* xp = reinterpret_cast<const float*>(x) + off;
+      const f32x4_t a = *reinterpret_cast<const f32x4_t*>(xp), b = *reinterpret_cast<const f32x4_t*>(xp + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) { v[i] = a[i]; v[4 + i] = b[i]; }
+    } else {
+      const u32x4_t a = ld16(reinterpret_cast<const uint16_t*>(x) + off);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[2 * i] = bf16_to_f32((uint16_t)(a[i] & 0xffffu));
+        v[2 * i + 1] = bf16_to_f32((uint16_t)(a[i] >> 16));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+#pragma unroll
+  for (int off = LPR / 2; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+  float scale = amax / 127.0f;
+  scale = scale < min_scale ? min_scale : scale;
+  if (!valid) return;
+  uint32_t packed[2] = {0, 0};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float qv = rintf(v[i] / scale);
+    qv = fminf(fmaxf(qv, -127.0f), 127.0f);
+    packed[i >> 2] |= ((uint32_t)(uint8_t)(int8_t)qv) << (8 * (i & 3));
+  }
+  *reinterpret_cast<u32x2_t*>(qo + r * D + 8 * lane_in_row) = u32x2_t{packed[0], packed[1]};
+  if (lane_in_row == 0) {
+    if (scale_is_f16) reinterpret_cast<__half*>(so)[r] = __float2half_rn(scale);
+    else reinterpret_cast<float*>(so)[r] = scale;
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void dequantize_kernel(const int8_t* __restrict__ q, const void* __restrict__ s,
+                                                         int scale_is_f16, int64_t rows, void* __restrict__ out,
+                                                         int out_is_f32) {
+  constexpr int LPR = D / 8;
+  constexpr int RPB = 256 / LPR;
+  const int lane_in_row = threadIdx.x % LPR;
+  const int64_t r = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR;
+  if (r >= rows) return;
+  const float sc = load_scale(s, r, scale_is_f16);
+  const u32x2_t w = *reinterpret_cast<const u32x2_t*>(q + r * D + 8 * lane_in_row);
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = (float)(int8_t)((w[i >> 2] >> (8 * (i & 3))) & 0xffu) * sc;
+  if (out_is_f32) {
+    float* o = reinterpret_cast<float*>(out) + r * D + 8 * lane_in_row;
+    *reinterpret_cast<f32x4_t*>(o) = f32x4_t{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4_t*>(o + 4) = f32x4_t{v[4], v[5], v[6], v[7]};
+  } else {
+    uint16_t* o = reinterpret_cast<uint16_t*>(out) + r * D + 8 * lane_in_row;
+    st16(o, u32x4_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])});
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Decode. Workgroup (split s, KV head g): 4 waves; a wave walks keys 8 at a time, 8 lanes per key row (16 d each).
+constexpr int kDecThreads = 256;
+constexpr float kDecRescale = 8.0f;
+
+template <int D, int G, bool INT8>
+__global__ __launch_bounds__(kDecThreads) void decode_kernel(DecodeParams p) {
+  constexpr int LPK = 8;             // lanes per key
+  constexpr int DPL = D / LPK;       // d values per lane
+  constexpr int KPW = 64 / LPK;      // keys per wave step
+  constexpr int SLOTS = kDecThreads / LPK;  // key slots per workgroup (32)
+  __shared__ float part_m[SLOTS][G];
+  __shared__ float part_l[SLOTS][G];
+  __shared__ float part_o[SLOTS][G][D];
+
+  const int split = blockIdx.x, g = blockIdx.y;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int kslot = lane / LPK, sub = lane % LPK;
+  const int slot = wave * KPW + kslot;
+  const int64_t j_begin = (int64_t)split * p.split_len;
+  int64_t j_end = j_begin + p.split_len;
+  if (j_end > p.n) j_end = p.n;
+
+  float qv[G][DPL];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    const uint16_t* qr = p.q + (int64_t)(g * G + h) * p.sq + DPL * sub;
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) qv[h][e] = bf16_to_f32(qr[e]);
+  }
+  float m[G], l[G], acc[G][DPL];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    m[h] = -1.0e20f;
+    l[h] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) acc[h][e] = 0.0f;
+  }
+
+  for (int64_t j = j_begin + slot; j < j_end; j += SLOTS) {
+    float kf[DPL], vf[DPL];
+    float ks = 1.0f, vs = 1.0f;
+    if constexpr (INT8) {
+      const int64_t row = j * p.Hkv + g;
+      const int8_t* kr = p.k8 + row * D + DPL * sub;
+      const int8_t* vr = p.v8 + row * D + DPL * sub;
+      ks = load_scale(p.ks, row, p.scale_is_f16);
+      vs = load_scale(p.vs, row, p.scale_is_f16);
+#pragma unroll
+      for (int e0 = 0; e0 < DPL; e0 += 16) {
+        const u32x4_t kw = ld16(kr + e0), vw = ld16(vr + e0);
+#pragma unroll
+        for (int e = 0; e < 16 && e0 + e < DPL; ++e) {
+          kf[e0 + e] = (float)(int8_t)((kw[e >> 2] >> (8 * (e & 3))) & 0xffu);
+          vf[e0 + e] = (float)(int8_t)((vw[e >> 2] >> (8 * (e & 3))) & 0xffu);
+        }
+      }
+    } else {
+      const uint16_t* kr = p.kb + (int64_t)g * p.skb0 + j * p.skb1 + DPL * sub;
+      const uint16_t* vr = p.vb + (int64_t)g * p.svb0 + j * p.svb1 + DPL * sub;
+#pragma unroll
+      for (int e0 = 0; e0 < DPL; e0 += 8) {
+        const u32x4_t kw = ld16(kr + e0), vw = ld16(vr + e0);
+#pragma unroll
+        for (int e = 0; e < 8 && e0 + e < DPL; ++e) {
+          kf[e0 + e] = bf16_to_f32((uint16_t)(kw[e >> 1] >> (16 * (e & 1))));
+          vf[e0 + e] = bf16_to_f32((uint16_t)(vw[e >> 1] >> (16 * (e & 1))));
+        }
+      }
+    }
+    float s[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float t = 0.0f;
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) t = fmaf(qv[h][e], kf[e], t);
+      s[h] = t;
+    }
+#pragma unroll
+    for (int off = 1; off < LPK; off <<= 1)
+#pragma unroll
+      for (int h = 0; h < G; ++h) s[h] += __shfl_xor(s[h], off);
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float x = s[h] * ks * p.c;
+      if (x > m[h] + kDecRescale) {
+        const float alpha = fast_exp2(m[h] - x);
+        m[h] = x;
+        l[h] *= alpha;
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) acc[h][e] *= alpha;
+      }
+      const float pr = fast_exp2(x - m[h]);
+      l[h] += pr;
+      const float pv = pr * vs;
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) acc[h][e] = fmaf(pv, vf[e], acc[h][e]);
+    }
+  }
+  // workgroup combine of the SLOTS partial states per head
+  if (sub == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) { part_m[slot][h] = m[h]; part_l[slot][h] = l[h]; }
+  }
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) part_o[slot][h][DPL * sub + e] = acc[h][e];
+  __syncthreads();
+  for (int t = tid; t < G * D; t += kDecThreads) {
+    const int h = t / D, d = t % D;
+    float M = -1.0e30f;
+    for (int s2 = 0; s2 < SLOTS; ++s2) M = fmaxf(M, part_m[s2][h]);
+    float L = 0.0f, O = 0.0f;
+    for (int s2 = 0; s2 < SLOTS; ++s2) {
+      const float w = fast_exp2(part_m[s2][h] - M);
+      L += w * part_l[s2][h];
+      O += w * part_o[s2][h][d];
+    }
+    float* dst = p.part + ((int64_t)(g * G + h) * p.n_splits + split) * (D + 2);
+    dst[d] = O;
+    if (d == 0) { dst[D] = M; dst[D + 1] = L; }
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
+  const int h = blockIdx.x;
+  for (int d = threadIdx.x; d < D; d += 256) {
+    const float* base = p.part + (int64_t)h * p.n_splits * (D + 2);
+    float M = -1.0e30f;
+    for (int s = 0; s < p.n_splits; ++s) M = fmaxf(M, base[s * (D + 2) + D]);
+    float L = 0.0f, O = 0.0f;
+    for (int s = 0; s < p.n_splits; ++s) {
+      const float w = fast_exp2(base[s * (D + 2) + D] - M);
+      L += w * base[s * (D + 2) + D + 1];
+      O += w * base[s * (D + 2) + d];
+    }
+    p.out[(int64_t)h * p.so + d] = f32_to_bf16(O / fmaxf(L, 1.0e-20f));
+  }
+}
+
+template <int D, int G>
+hipError_t launch_decode_dg(const DecodeParams& p, hipStream_t stream) {
+  if (p.k8)
+    hipLaunchKernelGGL((decode_kernel<D, G, true>), dim3(p.n_splits, p.Hkv), dim3(kDecThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((decode_kernel<D, G, false>), dim3(p.n_splits, p.Hkv), dim3(kDecThreads), 0, stream, p);
+  hipLaunchKernelGGL(decode_merge_kernel<D>, dim3(p.H), dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_decode_d(const DecodeParams& p, hipStream_t stream) {
+  switch (p.H / p.Hkv) {
+    case 1: return launch_decode_dg<D, 1>(p, stream);
+    case 2: return launch_decode_dg<D, 2>(p, stream);
+    case 4: return launch_decode_dg<D, 4>(p, stream);
+    case 8: return launch_decode_dg<D, 8>(p, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// RoPE: x' = bf16(bf16(x * cos) + bf16(rotate_half(x) * sin)), rotate_half(x) = cat(-x2, x1): the arithmetic of
+// HF apply_rotary_pos_emb on bf16 tensors (each torch op rounds to bf16), so results are bit-identical.
+__global__ __launch_bounds__(256) void rope_kernel(uint16_t* __restrict__ x, int64_t sx0, int64_t sx1, int64_t sx2,
+                                                   int B, int Hh, int64_t T, int D, const uint16_t* __restrict__ cs,
+                                                   const uint16_t* __restrict__ sn, int64_t sc0, int64_t sc1) {
+  const int half = D / 2;
+  const int cpr = half / 8;  // 8-element chunks per half row
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)B * Hh * T * cpr;
+  if (t >= total) return;
+  const int c = (int)(t % cpr);
+  const int64_t row = t / cpr;
+  const int64_t pos = row % T;
+  const int64_t bh = row / T;
+  const int64_t b = bh / Hh, hh = bh % Hh;
+  uint16_t* xr = x + b * sx0 + hh * sx1 + pos * sx2;
+  const uint16_t* cr = cs + b * sc0 + pos * sc1;
+  const uint16_t* sr = sn + b * sc0 + pos * sc1;
+  const int d1 = 8 * c, d2 = half + 8 * c;
+  const u32x4_t x1 = ld16(xr + d1), x2 = ld16(xr + d2);
+  const u32x4_t c1 = ld16(cr + d1), c2 = ld16(cr + d2);
+  const u32x4_t s1 = ld16(sr + d1), s2 = ld16(sr + d2);
+  u32x4_t o1, o2;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    uint32_t r1 = 0, r2 = 0;
+#pragma unroll
+    for (int hw = 0; hw < 2; ++hw) {
+      const int sh = 16 * hw;
+      const float a1 = bf16_to_f32((uint16_t)(x1[w] >> sh)), a2 = bf16_to_f32((uint16_t)(x2[w] >> sh));
+      const float fc1 = bf16_to_f32((uint16_t)(c1[w] >> sh)), fc2 = bf16_to_f32((uint16_t)(c2[w] >> sh));
+      const float fs1 = bf16_to_f32((uint16_t)(s1[w] >> sh)), fs2 = bf16_to_f32((uint16_t)(s2[w] >> sh));
+      // first half: x1*cos1 + (-x2)*sin1 ; second half: x2*cos2 + x1*sin2
+      const float p1 = bf16_to_f32(f32_to_bf16(a1 * fc1));
+      const float q1 = bf16_to_f32(f32_to_bf16(-a2 * fs1));
+      const float p2 = bf16_to_f32(f32_to_bf16(a2 * fc2));
+      const float q2 = bf16_to_f32(f32_to_bf16(a1 * fs2));
+      r1 |= (uint32_t)f32_to_bf16(p1 + q1) << sh;
+      r2 |= (uint32_t)f32_to_bf16(p2 + q2) << sh;
+    }
+    o1[w] = r1;
+    o2[w] = r2;
+  }
+  st16(xr + d1, o1);
+  st16(xr + d2, o2);
+}
+
+}  // namespace
+
+hipError_t launch_int8_quantize(const void* x, int x_is_f32, int64_t rows, int64_t row_stride, int inner,
+                                int64_t inner_stride, int D, float min_scale, int8_t* q, void* scale, int scale_is_f16,
+                                hipStream_t stream) {
+  const int64_t total = rows * inner;
+  if (total <= 0) return hipSuccess;
+  const int rpb = 256 / (D / 8);
+  const unsigned blocks = (unsigned)((total + rpb - 1) / rpb);
+  switch (D) {
+    case 32: hipLaunchKernelGGL(quantize_kernel<32>, dim3(blocks), dim3(256), 0, stream, x, x_is_f32, rows, row_stride, inner, inner_stride, min_scale, q, scale, scale_is_f16); break;
+    case 64: hipLaunchKernelGGL(quantize_kernel<64>, dim3(blocks), dim3(256), 0, stream, x, x_is_f32, rows, row_stride, inner, inner_stride, min_scale, q, scale, scale_is_f16); break;
+    case 128: hipLaunchKernelGGL(quantize_kernel<128>, dim3(blocks), dim3(256), 0, stream, x, x_is_f32, rows, row_stride, inner, inner_stride, min_scale, q, scale, scale_is_f16); break;
+    case 256: hipLaunchKernelGGL(quantize_kernel<256>, dim3(blocks), dim3(256), 0, stream, x, x_is_f32, rows, row_stride, inner, inner_stride, min_scale, q, scale, scale_is_f16); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_int8_dequantize(const int8_t* q, const void* scale, int scale_is_f16, int64_t rows, int D, void* out,
+                                  int out_is_f32, hipStream_t stream) {
+  if (rows <= 0) return hipSuccess;
+  const int rpb = 256 / (D / 8);
+  const unsigned blocks = (unsigned)((rows + rpb - 1) / rpb);
+  switch (D) {
+    case 32: hipLaunchKernelGGL(dequantize_kernel<32>, dim3(blocks), dim3(256), 0, stream, q, scale, scale_is_f16, rows, out, out_is_f32); break;
+    case 64: hipLaunchKernelGGL(dequantize_kernel<64>, dim3(blocks), dim3(256), 0, stream, q, scale, scale_is_f16, rows, out, out_is_f32); break;
+    case 128: hipLaunchKernelGGL(dequantize_kernel<128>, dim3(blocks), dim3(256), 0, stream, q, scale, scale_is_f16, rows, out, out_is_f32); break;
+    case 256: hipLaunchKernelGGL(dequantize_kernel<256>, dim3(blocks), dim3(256), 0, stream, q, scale, scale_is_f16, rows, out, out_is_f32); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+size_t decode_workspace_bytes(int H, int D, int n_splits) { return (size_t)H * n_splits * (D + 2) * sizeof(float); }
+
+hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
+  if (p.n <= 0) return hipErrorInvalidValue;
+  switch (p.D) {
+    case 64: return launch_decode_d<64>(p, stream);
+    case 128: return launch_decode_d<128>(p, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_rope(uint16_t* x, int64_t sx0, int64_t sx1, int64_t sx2, int B, int Hh, int64_t T, int D,
+                       const uint16_t* cos, const uint16_t* sin, int64_t sc0, int64_t sc1, hipStream_t stream) {
+  const int64_t total = (int64_t)B * Hh * T * (D / 16);
+  if (total <= 0) return hipSuccess;
+  hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, x, sx0, sx1, sx2, B, Hh,
+                     T, D, cos, sin, sc0, sc1);
+  return hipGetLastError();
+}
+
+}  // namespace bb

@@ -1,0 +1,80 @@
+// Host-side launch descriptors shared between the kernels and the C-ABI layer.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bb {
+
+// Sparse flash attention (one joint softmax over front | causal window | routed keys).
+struct FlashParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint16_t* vt;       // V^T [n_kvbh][D][np] (keys >= N zero)
+  const int32_t* idx;       // [BH, n_groups, route_k] (strided), -1 = empty slot
+  const uint8_t* key_mask;  // [B, N] bool (strided by smb), or null
+  uint16_t* out;            // [BH, T, D] view (strided)
+  float* part_o;            // split mode: [n_chunks][BH][T][D]
+  float* part_ml;           // split mode: [n_chunks][BH][T][2] (running max in log2 units, denominator)
+  int64_t sq0, sq1, sk0, sk1, sv0, sv1, si0, si1, si2, smb, so0, so1;
+  int64_t N, T, offset, row_end, route_chunk, key_chunk, np;
+  int BH, H, G, Hkv_pb, n_kvbh, front, window, route_k, n_groups;
+  int row_tiles, head_splits, n_chunks, remap, waves;
+  float c;  // scale * log2(e)
+};
+
+hipError_t launch_flash(const FlashParams& p, int D, int hpw, bool split, hipStream_t stream);
+hipError_t launch_flash_merge(const FlashParams& p, int D, hipStream_t stream);
+hipError_t launch_transpose_v(const uint16_t* v, int64_t sv0, int64_t sv1, int n_kvbh, int64_t N, int64_t np, int D,
+                              uint16_t* vt, hipStream_t stream);
+
+// Routing (pooled softmax of the route queries, then per-head top-k).
+struct RoutesParams {
+  const uint16_t* q;  // [BH, n, D] strided (sq0 head, sq1 token)
+  const uint16_t* k;  // [BKV, n, D] strided
+  const int64_t* qpos;  // [r]
+  int64_t sq0, sq1, sk0, sk1;
+  int64_t n;
+  int H, Hkv, B, D, r, sink, window, budget, pool_max;
+  float scaling;
+  uint16_t* scores;     // [B*Hkv][G*r][n] bf16 workspace
+  uint32_t* rowmax;     // [B*H*r] ordered-float keys
+  uint64_t* rowsum;     // [B*H*r] fixed point 2^40
+  uint64_t* pooled;     // [B*H][n] fixed point 2^40
+  int32_t* out_idx;     // [B*H][budget]
+};
+
+size_t routes_workspace_bytes(int64_t n, int H, int Hkv, int B, int r);
+hipError_t launch_routes(RoutesParams& p, void* ws, size_t ws_bytes, hipStream_t stream);
+
+// INT8 KV cache.
+hipError_t launch_int8_quantize(const void* x, int x_is_f32, int64_t rows, int64_t row_stride, int inner, int64_t inner_stride,
+                                int D, float min_scale, int8_t* q, void* scale, int scale_is_f16, hipStream_t stream);
+hipError_t launch_int8_dequantize(const int8_t* q, const void* scale, int scale_is_f16, int64_t rows, int D,
+                                  void* out, int out_is_f32, hipStream_t stream);
+
+struct DecodeParams {
+  const uint16_t* q;   // [B*H, D] (row stride sq)
+  const int8_t* k8;    // [cap, Hkv, D] token-major
+  const int8_t* v8;
+  const void* ks;      // [cap, Hkv] fp16 or fp32
+  const void* vs;
+  const uint16_t* kb;  // bf16 cache variant: [Hkv, cap, D] (strided) -- used when k8 == null
+  const uint16_t* vb;
+  int64_t sq, skb0, skb1, svb0, svb1;
+  int64_t n;
+  int H, Hkv, D, scale_is_f16, n_splits;
+  int64_t split_len;
+  float c;             // scale * log2(e)
+  uint16_t* out;       // [H, D]
+  int64_t so;
+  float* part;         // [H][n_splits][D + 2]
+};
+size_t decode_workspace_bytes(int H, int D, int n_splits);
+hipError_t launch_decode(const DecodeParams& p, hipStream_t stream);
+
+// RoPE in place (HF apply_rotary_pos_emb arithmetic in bf16).
+hipError_t launch_rope(uint16_t* x, int64_t sx0, int64_t sx1, int64_t sx2, int B, int Hh, int64_t T, int D,
+                       const uint16_t* cos, const uint16_t* sin, int64_t sc0, int64_t sc1, hipStream_t stream);
+
+}  // namespace bb

@@ -1,0 +1,412 @@
+// Routing for Bigger Bird v3 prefill (modal_rd/attention.py:143-174 of the reference): for every query head, the
+// mean (or max) softmax probability that its r route queries give to each key, then the `budget` best keys in
+// [sink, n - window), returned ascending as int32.
+//
+// The arithmetic is fixed so that results are reproducible bit for bit on any device and by the CPU oracle:
+//   s    = bf16_rne(exact q.k)             float64 FMA chain from bf16 operands (exact), one RNE step to bf16
+//   x    = fp32(s * scaling); M = row max over causal keys j <= qpos
+//   e    = det_exp2(fp32(fp32(x - M) * log2e))
+//   Z    = sum floor(e * 2^40) (uint64)    p = fp32(e * fp32(2^40 / double(Z)))
+//   P_j  = sum_i floor(p_ij * 2^40)  (or max_i for max pooling); top-budget by (P desc, index asc).
+// Integer sums make every reduction order-independent; there are no floating-point atomics.
+//
+// Kernels (all on the caller's stream, no host synchronisation):
+//   scores_kernel   exact scores of G*r route rows against a 64-key block, bf16 to the workspace, partial row max
+//   rowmax_kernel   partial maxima -> row max
+//   rowsum_kernel   fixed-point partial row sums over 1024-key blocks
+//   invz_kernel     partial sums -> fp32 scale 2^40 / Z per row
+//   pooled_kernel   per (head, key): pooled fixed-point probability over the r rows
+//   topk_kernel     one 1024-thread workgroup per head: MSD radix select on the 64-bit pooled values, then an
+//                   ordered compaction that emits the selected indices ascending (ties -> lower index)
+#include "bb_common.h"
+#include "bb_internal.h"
+
+// Every rounding step above is part of the contract: no fused multiply-add contraction in this file.
+#pragma clang fp contract(off)
+
+namespace bb {
+namespace {
+
+constexpr int kScoreKeys = 64;    // keys per scores_kernel workgroup
+constexpr int kSumKeys = 1024;    // keys per rowsum_kernel workgroup
+constexpr int kPoolKeys = 256;    // keys per pooled_kernel workgroup
+constexpr int kMaxRows = 256;     // G * r handled by one scores workgroup (rows beyond this use more row blocks)
+constexpr float kFixOne = 1099511627776.0f;  // 2^40
+
+BB_DEV uint64_t fix40(float v) { return (uint64_t)(v * kFixOne); }
+
+struct RouteGeom {
+  int G, rows, n_kb1, n_kb2, row_blocks;
+  int64_t ns;  // score row stride: n rounded up to 8 (16-byte aligned rows)
+};
+
+// Exact scores: one workgroup = up to 256 route rows x 64 keys of one KV head.
+// Thread t computes rows 8*(t/8)..+7 against keys 8*(t%8)..+7 with a float64 FMA chain over d in ascending order.
+template <int D>
+__global__ __launch_bounds__(256) void scores_kernel(RoutesParams p, RouteGeom g, float* __restrict__ pmax) {
+  __shared__ __attribute__((aligned(16))) uint16_t qs[D][kMaxRows];  // Q^T (bf16)
+  __shared__ __attribute__((aligned(16))) double ks[D][kScoreKeys];  // K^T (float64)
+  __shared__ float rmax_part[kMaxRows][8];
+  const int tid = threadIdx.x;
+  const int kb = blockIdx.x, rblk = blockIdx.y, bkv = blockIdx.z;
+  const int batch = bkv / p.Hkv, kvh = bkv % p.Hkv;
+  const int64_t j0 = (int64_t)kb * kScoreKeys;
+  const int row0 = rblk * kMaxRows;
+  const int nrows = g.rows - row0 < kMaxRows ? g.rows - row0 : kMaxRows;
+
+  // stage Q^T: row -> (head slot, query i)
+  for (int e = tid; e < kMaxRows * (D / 8); e += 256) {
+    const int row = e / (D / 8), c8 = e % (D / 8);
+    u32x4_t v = {0, 0, 0, 0};
+    if (row < nrows) {
+      const int rr = row0 + row, hs = rr / p.r, i = rr % p.r;
+      const int head = batch * p.H + kvh * g.G + hs;
+      v = ld16(p.q + (int64_t)head * p.sq0 + p.qpos[i] * p.sq1 + 8 * c8);
+    }
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      qs[8 * c8 + 2 * w][row] = (uint16_t)(v[w] & 0xffffu);
+      qs[8 * c8 + 2 * w + 1][row] = (uint16_t)(v[w] >> 16);
+    }
+  }
+  // stage K^T as float64
+  const uint16_t* kbase = p.k + (int64_t)bkv * p.sk0;
+  for (int e = tid; e < kScoreKeys * (D / 8); e += 256) {
+    const int key = e / (D / 8), c8 = e % (D / 8);
+    const int64_t j = j0 + key;
+    u32x4_t v = j < p.n ? ld16(kbase + j * p.sk1 + 8 * c8) : u32x4_t{0, 0, 0, 0};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      ks[8 * c8 + 2 * w][key] = (double)bf16_to_f32((uint16_t)(v[w] & 0xffffu));
+      ks[8 * c8 + 2 * w + 1][key] = (double)bf16_to_f32((uint16_t)(v[w] >> 16));
+    }
+  }
+  __syncthreads();
+
+  const int rb = tid >> 3, kq = tid & 7;
+  double acc[8][8];
+#pragma unroll
+  for (int a = 0; a < 8; ++a)
+#pragma unroll
+    for (int b = 0; b < 8; ++b) acc[a][b] = 0.0;
+  for (int d = 0; d < D; ++d) {
+    const u32x4_t qv = *reinterpret_cast<const u32x4_t*>(&qs[d][8 * rb]);
+    double qd[8];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      qd[2 * w] = (double)bf16_to_f32((uint16_t)(qv[w] & 0xffffu));
+      qd[2 * w + 1] = (double)bf16_to_f32((uint16_t)(qv[w] >> 16));
+    }
+    double kd[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) kd[b] = ks[d][8 * kq + b];
+#pragma unroll
+    for (int a = 0; a < 8; ++a)
+#pragma unroll
+      for (int b = 0; b < 8; ++b) acc[a][b] = fma(qd[a], kd[b], acc[a][b]);
+  }
+
+  // round, mask, store bf16, partial max of x = s * scaling
+  uint16_t* srow_base = p.scores + (int64_t)bkv * g.rows * g.ns;
+#pragma unroll
+  for (int a = 0; a < 8; ++a) {
+    const int row = 8 * rb + a;
+    const int rr = row0 + row;
+    float mx = -__builtin_huge_valf();
+    uint32_t packed[4];
+    const int64_t qp = row < nrows ? p.qpos[rr % p.r] : -1;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const int64_t j = j0 + 8 * kq + b;
+      uint16_t sb = 0xff80u;  // -inf
+      if (row < nrows && j < p.n && j <= qp) {
+        sb = bf16_from_f64(acc[a][b]);
+        mx = fmaxf(mx, bf16_to_f32(sb) * p.scaling);
+      }
+      if (b & 1) packed[b >> 1] |= (uint32_t)sb << 16;
+      else packed[b >> 1] = sb;
+    }
+    if (row < nrows) {
+      const int64_t jj = j0 + 8 * kq;
+      uint16_t* dst = srow_base + (int64_t)rr * g.ns + jj;
+      if (jj + 8 <= p.n) {
+        st16(dst, u32x4_t{packed[0], packed[1], packed[2], packed[3]});
+      } else {
+        for (int b = 0; b < 8 && jj + b < p.n; ++b) dst[b] = (uint16_t)(packed[b >> 1] >> (16 * (b & 1)));
+      }
+    }
+    rmax_part[row][kq] = mx;
+  }
+  __syncthreads();
+  if (tid < nrows) {
+    float mx = rmax_part[tid][0];
+#pragma unroll
+    for (int b = 1; b < 8; ++b) mx = fmaxf(mx, rmax_part[tid][b]);
+    pmax[((int64_t)bkv * g.n_kb1 + kb) * g.rows + row0 + tid] = mx;
+  }
+}
+
+__global__ void rowmax_kernel(RoutesParams p, RouteGeom g, const float* __restrict__ pmax) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)p.B * p.Hkv * g.rows;
+  if (t >= total) return;
+  const int64_t bkv = t / g.rows, row = t % g.rows;
+  float mx = -__builtin_huge_valf();
+  for (int kb = 0; kb < g.n_kb1; ++kb) mx = fmaxf(mx, pmax[(bkv * g.n_kb1 + kb) * g.rows + row]);
+  p.rowmax[t] = __float_as_uint(mx);
+}
+
+// Fixed-point partial row sums: one wave per row (4 rows in flight per workgroup), 16 keys per lane.
+__global__ __launch_bounds__(256) void rowsum_kernel(RoutesParams p, RouteGeom g, uint64_t* __restrict__ psum) {
+  const int kb = blockIdx.x, bkv = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t j0 = (int64_t)kb * kSumKeys + 16 * lane;
+  for (int row = wave; row < g.rows; row += 4) {
+    const float M = __uint_as_float(p.rowmax[(int64_t)bkv * g.rows + row]);
+    const uint16_t* src = p.scores + ((int64_t)bkv * g.rows + row) * g.ns + j0;
+    uint64_t acc = 0;
+    if (j0 + 16 <= p.n) {
+      const u32x4_t a = ld16(src), b = ld16(src + 8);
+      uint32_t w[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const uint16_t sb = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+        const float x = bf16_to_f32(sb) * p.scaling;
+        acc += fix40(det_exp2((x - M) * kLog2e));
+      }
+    } else {
+      for (int e = 0; e < 16 && j0 + e < p.n; ++e) {
+        const float x = bf16_to_f32(src[e]) * p.scaling;
+        acc += fix40(det_exp2((x - M) * kLog2e));
+      }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
+    if (lane == 0) psum[((int64_t)bkv * g.n_kb2 + kb) * g.rows + row] = acc;
+  }
+}
+
+__global__ void invz_kernel(RoutesParams p, RouteGeom g, const uint64_t* __restrict__ psum, float* __restrict__ invz) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)p.B * p.Hkv * g.rows;
+  if (t >= total) return;
+  const int64_t bkv = t / g.rows, row = t % g.rows;
+  uint64_t z = 0;
+  for (int kb = 0; kb < g.n_kb2; ++kb) z += psum[(bkv * g.n_kb2 + kb) * g.rows + row];
+  p.rowsum[t] = z;
+  invz[t] = (float)(1099511627776.0 / (double)z);
+}
+
+// Pooled fixed-point probability per (query head, key): thread per key, loop over the head's r rows.
+__global__ __launch_bounds__(256) void pooled_kernel(RoutesParams p, RouteGeom g, const float* __restrict__ invz) {
+  const int64_t j = (int64_t)blockIdx.x * kPoolKeys + threadIdx.x;
+  const int head = blockIdx.y;  // over B * H
+  if (j >= p.n) return;
+  const int batch = head / p.H, hh = head % p.H;
+  const int kvh = hh / g.G, hs = hh % g.G;
+  const int64_t bkv = (int64_t)batch * p.Hkv + kvh;
+  uint64_t P = 0;
+  const bool eligible = j >= p.sink && j < p.n - p.window;
+  if (eligible) {
+    for (int i = 0; i < p.r; ++i) {
+      const int64_t row = (int64_t)hs * p.r + i;
+      const int64_t ridx = bkv * g.rows + row;
+      const float M = __uint_as_float(p.rowmax[ridx]);
+      const uint16_t sb = p.scores[ridx * g.ns + j];
+      const float x = bf16_to_f32(sb) * p.scaling;
+      const float e = det_exp2((x - M) * kLog2e);
+      const uint64_t pf = fix40(e * invz[ridx]);
+      if (p.pool_max) P = pf > P ? pf : P;
+      else P += pf;
+    }
+  }
+  p.pooled[(int64_t)head * p.n + j] = P;
+}
+
+// Top-budget selection per head: MSD radix select over 8-bit digits, then ordered compaction.
+constexpr int kTopThreads = 1024;
+__global__ __launch_bounds__(kTopThreads) void topk_kernel(RoutesParams p) {
+  __shared__ uint32_t hist[256];
+  __shared__ uint64_t red[kTopThreads / 64];
+  __shared__ uint32_t scan_sel[kTopThreads];
+  __shared__ uint32_t scan_tie[kTopThreads];
+  __shared__ uint64_t s_prefix, s_mask;
+  __shared__ int64_t s_need;
+  __shared__ int s_exact;
+
+  const int head = blockIdx.x, tid = threadIdx.x;
+  const int64_t lo = p.sink < p.n ? (p.sink > 0 ? p.sink : 0) : p.n;
+  int64_t hi = p.n - p.window;
+  if (hi > p.n) hi = p.n;
+  const int64_t cnt = hi > lo ? hi - lo : 0;
+  const uint64_t* P = p.pooled + (int64_t)head * p.n + lo;
+  int32_t* out = p.out_idx + (int64_t)head * p.budget;
+  if (p.budget <= 0 || cnt <= 0) return;
+
+  // global max -> first digit
+  uint64_t mx = 0;
+  for (int64_t t = tid; t < cnt; t += kTopThreads) mx = P[t] > mx ? P[t] : mx;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    uint64_t o = __shfl_xor(mx, off);
+    mx = o > mx ? o : mx;
+  }
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t m = 0;
+    for (int w = 0; w < kTopThreads / 64; ++w) m = red[w] > m ? red[w] : m;
+    red[0] = m;
+    s_prefix = 0;
+    s_mask = 0;
+    s_need = p.budget;
+    s_exact = 0;
+  }
+  __syncthreads();
+  const uint64_t gmax = red[0];
+  int top_digit = 0;
+  if (gmax) top_digit = (63 - __clzll((long long)gmax)) / 8;
+  // the most significant digits above top_digit are zero for every value: fixed prefix 0
+  uint64_t prefix = 0, mask = top_digit < 7 ? ~((1ull << (8 * (top_digit + 1))) - 1ull) : 0ull;
+  if (tid == 0) s_mask = mask;
+  __syncthreads();
+  for (int digit = top_digit; digit >= 0; --digit) {
+    const int shift = 8 * digit;
+    for (int b = tid; b < 256; b += kTopThreads) hist[b] = 0;
+    __syncthreads();
+    prefix = s_prefix;
+    mask = s_mask;
+    for (int64_t t = tid; t < cnt; t += kTopThreads) {
+      const uint64_t v = P[t];
+      if ((v & mask) == prefix) atomicAdd(&hist[(v >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      int64_t need = s_need, cum = 0;
+      int bsel = 0;
+      for (int b = 255; b >= 0; --b) {
+        if (cum + (int64_t)hist[b] >= need) { bsel = b; break; }
+        cum += hist[b];
+      }
+      need -= cum;  // still needed from bin bsel
+      s_prefix = prefix | ((uint64_t)bsel << shift);
+      s_mask = mask | (255ull << shift);
+      s_need = need;
+      if ((int64_t)hist[bsel] == need) s_exact = 1;  // whole bin selected: no ties to break
+    }
+    __syncthreads();
+    if (s_exact) break;
+  }
+  // Final threshold: values matching prefix under mask form the boundary set; `need` of them are taken
+  // (all of them when s_exact), lowest indices first.
+  prefix = s_prefix;
+  mask = s_mask;
+  const int64_t need = s_need;
+  const int64_t seg = (cnt + kTopThreads - 1) / kTopThreads;
+  const int64_t t0 = (int64_t)tid * seg, t1 = t0 + seg < cnt ? t0 + seg : cnt;
+  uint32_t nsel = 0, ntie = 0;
+  for (int64_t t = t0; t < t1; ++t) {
+    const uint64_t v = P[t];
+    const uint64_t vm = v & mask;
+    if (vm > prefix) ++nsel;
+    else if (vm == prefix) ++ntie;
+  }
+  scan_sel[tid] = nsel;
+  scan_tie[tid] = ntie;
+  __syncthreads();
+  // exclusive scans (Hillis-Steele in place, 1024 entries)
+  for (int off = 1; off < kTopThreads; off <<= 1) {
+    uint32_t a = tid >= off ? scan_sel[tid - off] : 0u;
+    uint32_t b = tid >= off ? scan_tie[tid - off] : 0u;
+    __syncthreads();
+    scan_sel[tid] += a;
+    scan_tie[tid] += b;
+    __syncthreads();
+  }
+  const int64_t sel_before = (int64_t)scan_sel[tid] - nsel;
+  const int64_t tie_before = (int64_t)scan_tie[tid] - ntie;
+  // position of an element = selected-above before it + ties taken before it
+  int64_t taken_ties = tie_before < need ? tie_before : need;
+  int64_t pos = sel_before + taken_ties;
+  int64_t ties_seen = tie_before;
+  for (int64_t t = t0; t < t1; ++t) {
+    const uint64_t vm = P[t] & mask;
+    bool take = false;
+    if (vm > prefix) take = true;
+    else if (vm == prefix) {
+      take = ties_seen < need;
+      ++ties_seen;
+    }
+    if (take) {
+      if (pos < p.budget) out[pos] = (int32_t)(lo + t);
+      ++pos;
+    }
+  }
+}
+
+template <int D>
+hipError_t launch_routes_d(RoutesParams& p, const RouteGeom& g, float* pmax, uint64_t* psum, float* invz,
+                           hipStream_t stream) {
+  const int nbkv = p.B * p.Hkv;
+  hipLaunchKernelGGL(scores_kernel<D>, dim3(g.n_kb1, g.row_blocks, nbkv), dim3(256), 0, stream, p, g, pmax);
+  const int64_t rows_total = (int64_t)nbkv * g.rows;
+  hipLaunchKernelGGL(rowmax_kernel, dim3((unsigned)((rows_total + 255) / 256)), dim3(256), 0, stream, p, g, pmax);
+  hipLaunchKernelGGL(rowsum_kernel, dim3(g.n_kb2, nbkv), dim3(256), 0, stream, p, g, psum);
+  hipLaunchKernelGGL(invz_kernel, dim3((unsigned)((rows_total + 255) / 256)), dim3(256), 0, stream, p, g, psum, invz);
+  hipLaunchKernelGGL(pooled_kernel, dim3((unsigned)((p.n + kPoolKeys - 1) / kPoolKeys), p.B * p.H), dim3(kPoolKeys), 0,
+                     stream, p, g, invz);
+  if (p.budget > 0)
+    hipLaunchKernelGGL(topk_kernel, dim3(p.B * p.H), dim3(kTopThreads), 0, stream, p);
+  return hipGetLastError();
+}
+
+RouteGeom geom(int64_t n, int H, int Hkv, int r) {
+  RouteGeom g;
+  g.G = H / Hkv;
+  g.rows = g.G * r;
+  g.n_kb1 = (int)((n + kScoreKeys - 1) / kScoreKeys);
+  g.n_kb2 = (int)((n + kSumKeys - 1) / kSumKeys);
+  g.row_blocks = (g.rows + kMaxRows - 1) / kMaxRows;
+  g.ns = (n + 7) & ~(int64_t)7;
+  return g;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+}  // namespace
+
+size_t routes_workspace_bytes(int64_t n, int H, int Hkv, int B, int r) {
+  RouteGeom g = geom(n, H, Hkv, r);
+  const size_t nbkv = (size_t)B * Hkv;
+  size_t s = 0;
+  s += align256(nbkv * g.rows * (size_t)g.ns * 2);        // scores
+  s += align256(nbkv * g.n_kb1 * g.rows * 4);             // partial max
+  s += align256(nbkv * g.rows * 4);                       // row max
+  s += align256(nbkv * g.n_kb2 * g.rows * 8);             // partial sums
+  s += align256(nbkv * g.rows * 8);                       // row sums
+  s += align256(nbkv * g.rows * 4);                       // 2^40 / Z
+  s += align256((size_t)B * H * (size_t)n * 8);           // pooled
+  return s;
+}
+
+hipError_t launch_routes(RoutesParams& p, void* ws, size_t ws_bytes, hipStream_t stream) {
+  if (ws_bytes < routes_workspace_bytes(p.n, p.H, p.Hkv, p.B, p.r)) return hipErrorInvalidValue;
+  RouteGeom g = geom(p.n, p.H, p.Hkv, p.r);
+  const size_t nbkv = (size_t)p.B * p.Hkv;
+  char* w = static_cast<char*>(ws);
+  p.scores = reinterpret_cast<uint16_t*>(w); w += align256(nbkv * g.rows * (size_t)g.ns * 2);
+  float* pmax = reinterpret_cast<float*>(w); w += align256(nbkv * g.n_kb1 * g.rows * 4);
+  p.rowmax = reinterpret_cast<uint32_t*>(w); w += align256(nbkv * g.rows * 4);
+  uint64_t* psum = reinterpret_cast<uint64_t*>(w); w += align256(nbkv * g.n_kb2 * g.rows * 8);
+  p.rowsum = reinterpret_cast<uint64_t*>(w); w += align256(nbkv * g.rows * 8);
+  float* invz = reinterpret_cast<float*>(w); w += align256(nbkv * g.rows * 4);
+  p.pooled = reinterpret_cast<uint64_t*>(w);
+  switch (p.D) {
+    case 32: return launch_routes_d<32>(p, g, pmax, psum, invz, stream);
+    case 64: return launch_routes_d<64>(p, g, pmax, psum, invz, stream);
+    case 128: return launch_routes_d<128>(p, g, pmax, psum, invz, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace bb
