@@ -25,15 +25,25 @@ def rope_host(x, cos, sin):
 
 
 def make_inputs(T, H=32, Hkv=8, d=128, *, batch=1, seed=0, theta=500000.0, rope=True, planted=0, sink=64,
-                window=16384, device="cpu", rope_on_device=True):
+                window=16384, device="cpu", rope_on_device=True, rng="host"):
     """Returns dict(q, k, v, planted_pos) with q [B,H,T,d], k/v [B,Hkv,T,d] bf16 on `device`.
 
-    RoPE runs on the device through the HIP kernel when `device` is a GPU and `rope_on_device` (bit-identical to
-    the host formula), otherwise on the host."""
+    rng="host" draws Q/K/V from a CPU generator (identical bytes on every machine); rng="device" draws them with the
+    device's generator (fast at 128K tokens, reproducible on one torch build and GPU model). Planted positions always
+    come from the host generator. RoPE runs on the device through the HIP kernel when `device` is a GPU and
+    `rope_on_device` (bit-identical to the host formula), otherwise on the host."""
     g = torch.Generator().manual_seed(seed)
-    q = torch.randn(batch, H, T, d, generator=g).to(torch.bfloat16)
-    k = torch.randn(batch, Hkv, T, d, generator=g).to(torch.bfloat16)
-    v = torch.randn(batch, Hkv, T, d, generator=g).to(torch.bfloat16)
+    if rng == "device":
+        gd = torch.Generator(device=device).manual_seed(seed)
+        q = torch.randn(batch, H, T, d, generator=gd, device=device).to(torch.bfloat16)
+        k = torch.randn(batch, Hkv, T, d, generator=gd, device=device).to(torch.bfloat16)
+        v = torch.randn(batch, Hkv, T, d, generator=gd, device=device).to(torch.bfloat16)
+    elif rng == "host":
+        q = torch.randn(batch, H, T, d, generator=g).to(torch.bfloat16)
+        k = torch.randn(batch, Hkv, T, d, generator=g).to(torch.bfloat16)
+        v = torch.randn(batch, Hkv, T, d, generator=g).to(torch.bfloat16)
+    else:
+        raise ValueError("rng must be 'host' or 'device'")
     pos = None
     if planted:
         span = T - window - sink
