@@ -69,7 +69,9 @@ int64_t bb_transpose_v_cols(int64_t N);
  * ascending as int32 in idx_out [B*H, budget]. Replaces RDAttention.routes (modal_rd/attention.py:143-174).
  *   q [B*H, n, D] (strides sq[2]: head, token), k [B*Hkv, n, D] (strides sk[2]); qpos [r] int64 on the device.
  *   pooled_out: optional [B*H, n] uint64 copy of the pooled scores in units of 2^-40 (NULL to skip).
- *   Arithmetic is deterministic (exact bf16 scores, fixed-point sums); results are identical on every run.
+ *   Arithmetic is deterministic: bf16 scores rounded from fp32 sums in the accumulation order of the reference's
+ *   CPU matmul (oneDNN AMX-BF16: per 32-element block of d, even and odd fp32 chains), fixed-point softmax sums;
+ *   results are identical on every run.
  */
 int bb_routes(const void* q, const int64_t* sq, const void* k, const int64_t* sk, const int64_t* qpos, int r,
               int B, int H, int Hkv, int64_t n, int D, int64_t sink, int64_t window, int budget, float scaling,

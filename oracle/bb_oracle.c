@@ -14,11 +14,10 @@
  *   orc_dequantize  modal_rd/kv_int8.py:25-26.
  *   orc_decode      modal_rd/attention.py:137-141 over the dequantised cache (exact attention of one token).
  *
- * Routing arithmetic contract ("semantics D").  The reference computes scores with a bf16 matmul whose fp32
- * accumulation order is library-defined, so its low bits are not reproducible across machines.  This oracle
- * fixes every rounding step instead:
- *   s    = bf16_rne(exact q.k)                         exact dot (float64, exact for bf16 inputs whose 128 products
- *                                                      span < 2^31), one round-to-nearest-even to bf16
+ * Routing arithmetic contract.  The reference computes scores with a bf16 matmul (modal_rd/attention.py:164) whose
+ * fp32 accumulation order is the library's; on the CPU that produced the golden routes (torch 2.10, oneDNN, AMX-BF16)
+ * that order is fixed and reproduced exactly by amx_dot() below.  Every later step is fixed here as well:
+ *   s    = bf16_rne(amx_dot(q, k))                     d even; score mode 1 uses bf16_rne(exact q.k) instead
  *   x    = fp32(s * scaling)
  *   M_i  = max_j x_ij over causal keys j <= qpos_i
  *   e_ij = det_exp2(fp32(fp32(x_ij - M_i) * LOG2E))    det_exp2: rint reduction + degree-7 Horner with fmaf
@@ -26,8 +25,8 @@
  *   p_ij = fp32(e_ij * fp32(2^40 / double(Z_i)))
  *   P_j  = sum_i floor(p_ij * 2^40)  (mean pool)  or  max_i floor(p_ij * 2^40)  (max pool)
  *   eligible j in [sink, n - window); take `budget` largest P_j, ties to the lower index; return ascending.
- * With exact scores these agree with the reference's op sequence except where two pooled probabilities sit within
- * fp32/bf16 rounding of each other.
+ * The bf16 scores are therefore bit-identical to the reference's; the softmax and mean differ from torch's fp32 ones by
+ * a few fp32 ulps, which changes a selected column only where two pooled probabilities tie to that precision.
  */
 #include <math.h>
 #include <stdint.h>
@@ -133,12 +132,36 @@ float orc_det_exp2(float x) {
 
 static inline uint64_t fix40(float v) { return (uint64_t)(v * FIX_ONE); }
 
-/* Exact bf16 score of one query row against one key row (float64 in ascending d order). */
+/*
+ * fp32 score of one query row against one key row in the accumulation order of torch's CPU bf16 matmul on an
+ * AMX-BF16 host (oneDNN brgemm, one tile dot-product per 32 elements of d): inside each 32-element block the even and
+ * the odd elements form two sequential fp32 chains E and O; the block adds fl(E + O) to the running sum. A bf16 x bf16
+ * product is exact in fp32, so every step is one fp32 rounding. (Pinned against torch.matmul on bf16 CPU tensors.)
+ */
+static inline float amx_dot(const uint16_t* a, const uint16_t* b, int d) {
+  float acc = 0.0f;
+  for (int b0 = 0; b0 < d; b0 += 32) {
+    float e = 0.0f, o = 0.0f;
+    for (int i = b0; i < b0 + 32 && i < d; i += 2) {
+      e = e + bf16_to_f32(a[i]) * bf16_to_f32(b[i]);
+      o = o + bf16_to_f32(a[i + 1]) * bf16_to_f32(b[i + 1]);
+    }
+    acc = acc + (e + o);
+  }
+  return acc;
+}
+
+/* Exact float64 dot product (bf16 inputs, d <= 128: every partial sum is exact). */
 static inline double exact_dot(const uint16_t* a, const uint16_t* b, int d) {
   double s = 0.0;
   for (int i = 0; i < d; ++i) s += (double)bf16_to_f32(a[i]) * (double)bf16_to_f32(b[i]);
   return s;
 }
+
+/* Score rounding of the routing contract: 0 = torch CPU AMX order (the reference's arithmetic), 1 = exact. */
+static int g_score_mode = 0;
+void orc_set_score_mode(int m) { g_score_mode = m; }
+float orc_amx_dot(const uint16_t* a, const uint16_t* b, int d) { return amx_dot(a, b, d); }
 
 /*
  * Pooled routing scores and the selected columns.
@@ -194,7 +217,9 @@ int orc_routes(const uint16_t* q, int64_t sq0, int64_t sq1, const uint16_t* k, i
       const uint16_t* qrow = q + h * sq0 + qp * sq1;
       float m = -INFINITY;
       for (int j = 0; j <= last; ++j) {
-        uint16_t sb = orc_bf16_from_double(exact_dot(qrow, k + g * sk0 + (int64_t)j * sk1, d));
+        const uint16_t* krow = k + g * sk0 + (int64_t)j * sk1;
+        uint16_t sb = g_score_mode ? orc_bf16_from_double(exact_dot(qrow, krow, d))
+                                   : f32_to_bf16_rne(amx_dot(qrow, krow, d));
         float xv = bf16_to_f32(sb) * scaling;
         x[j] = xv;
         if (xv > m) m = xv;

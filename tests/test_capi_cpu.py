@@ -1,0 +1,109 @@
+"""The C-ABI library without a GPU: it loads, exports every function include/bb_attn.h declares, and its host-side
+argument checks return the reference's error texts (kernels/bigger_bird_flash.py:110-130) before any launch.
+Also the Python surface's own argument errors (modal_rd/attention.py:94-100) and the FLOP-count helper."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from bigger_bird_amd import RDAttention, _lib, bigger_bird_flash
+from bigger_bird_amd.synth import attended_pairs
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "bb_attn.h"
+
+
+def _declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(bb_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_function():
+    L = _lib.lib()
+    names = _declared()
+    assert len(names) >= 12
+    for name in names:
+        assert hasattr(L, name), name
+    assert set(names) <= set(_lib.SIGNATURES), "ctypes signatures missing for some declared functions"
+
+
+def test_version_and_sizes():
+    L = _lib.lib()
+    assert L.bb_version() >= 100
+    assert L.bb_transpose_v_cols(1) == 64 and L.bb_transpose_v_cols(64) == 64 and L.bb_transpose_v_cols(65) == 128
+    assert L.bb_routes_workspace(131072, 32, 8, 1, 64) > 32 * 131072 * 8
+    assert L.bb_decode_workspace(131072, 32, 8, 128) > 0
+    # tail shape: few row tiles, no routes -> the split-key schedule asks for partials
+    tail = L.bb_sparse_flash_workspace(32, 256, 131072, 128, 32, 4, 0, 131072, 0, 256, 1)
+    main = L.bb_sparse_flash_workspace(32, 131072, 131072, 128, 32, 4, 64, 16384, 512, 131072 - 256, 1)
+    assert tail > 0 and main == 0
+
+
+def _flash_call(**over):
+    L = _lib.lib()
+    s3 = _lib.i64s(4096, 128, 1)
+    a = dict(q=ctypes.c_void_p(16), sq=s3, k=ctypes.c_void_p(16), sk=s3, v=ctypes.c_void_p(16), sv=s3, vt=None,
+             idx=None, si=_lib.i64s(1, 1, 1), n_groups=1, route_k=0, key_mask=None, smb=0, out=ctypes.c_void_p(16),
+             so=s3, BH=32, T=64, N=64, D=128, num_heads=32, kv_groups=4, front=0, window=8, route_chunk=64,
+             scale=1.0, row_end=64, ws=None, ws_bytes=0, stream=None)
+    a.update(over)
+    rc = L.bb_sparse_flash(*a.values())
+    return rc, L.bb_last_error().decode()
+
+
+@pytest.mark.parametrize("over,msg", [
+    (dict(front=-1), "front >= 0 and window >= 1 required"),
+    (dict(window=0), "front >= 0 and window >= 1 required"),
+    (dict(kv_groups=3), "must have matching heads"),
+    (dict(T=65), "Key sequence must be at least as long as query sequence"),
+    (dict(route_k=4, idx=ctypes.c_void_p(16), n_groups=2), "Routing groups must cover the sequence"),
+    (dict(D=96), "head_dim 96 unsupported"),
+    (dict(scale=0.0), "scale must be positive"),
+    (dict(sq=_lib.i64s(4096, 129, 1)), "16-byte aligned rows"),
+])
+def test_flash_argument_errors(over, msg):
+    rc, err = _flash_call(**over)
+    assert rc == -1 and msg in err
+
+
+def test_routes_argument_errors():
+    L = _lib.lib()
+    s2 = _lib.i64s(128 * 1000, 128)
+    rc = L.bb_routes(ctypes.c_void_p(16), s2, ctypes.c_void_p(16), s2, ctypes.c_void_p(16), 64, 1, 32, 8, 1000, 128,
+                     64, 512, 600, 0.1, 0, ctypes.c_void_p(16), None, ctypes.c_void_p(16), 1 << 30, None)
+    assert rc == -1 and "exceeds" in L.bb_last_error().decode()
+
+
+def test_python_surface_errors_without_gpu():
+    base = type("B", (), {})()
+    base.config = type("C", (), {"num_attention_heads": 32, "num_key_value_heads": 8})()
+    base.layer_idx, base.head_dim, base.scaling = 0, 128, 128 ** -0.5
+    base.q_proj = base.k_proj = base.v_proj = base.o_proj = None
+    with pytest.raises(ValueError, match="route_pool"):
+        RDAttention(base, route_pool="median")
+    with pytest.raises(ValueError, match="route_queries"):
+        RDAttention(base, route_queries="first")
+    with pytest.raises(ValueError, match="scope_chunk"):
+        RDAttention(base, scope_chunk=96)
+    q = torch.zeros(8, 64, 32, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="ROCm BF16"):  # no silent CPU path
+        bigger_bird_flash(q, q[:2], q[:2], torch.zeros(8, 1, 4, dtype=torch.int32), num_heads=8, kv_groups=4)
+
+
+def test_attended_pairs_matches_brute_force():
+    T, H, sink, window, tail = 300, 4, 7, 50, 20
+    g = torch.Generator().manual_seed(0)
+    routes = torch.stack([(torch.randperm(T - window - sink, generator=g)[:15] + sink).sort().values
+                          for _ in range(H)]).to(torch.int32)
+    q = torch.arange(T)[:, None]
+    kk = torch.arange(T)[None, :]
+    total = 0
+    for h in range(H):
+        allowed = (kk <= q) & ((kk < sink) | (kk > q - window))
+        member = torch.zeros(T, dtype=torch.bool)
+        member[routes[h].long()] = True
+        allowed |= member[None, :] & (kk <= q - window) & (kk >= sink)
+        allowed[T - tail:] = kk <= q[T - tail:]
+        total += int(allowed.sum())
+    assert attended_pairs(T, H, sink, window, routes, tail) == total

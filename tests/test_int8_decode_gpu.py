@@ -1,0 +1,86 @@
+"""HIP int8 quantise/dequantise, exact decode (int8 and bf16 caches) and in-place RoPE against the CPU oracle.
+
+Bars: quantise/dequantise/RoPE are integer-exact or single-rounding ops -> bitwise; decode is floating point ->
+max-abs 2e-2 / mean-abs 2e-3 against the float64 oracle (the north-star bf16 tolerance).
+"""
+import pytest
+import torch
+
+import oracle
+from bigger_bird_amd import decode_bf16, decode_int8, dequantize, quantize, rope_inplace
+from bigger_bird_amd.synth import rope_cos_sin, rope_host
+
+pytestmark = pytest.mark.gpu
+
+
+def _rand(shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("scale_dtype", [torch.float16, torch.float32])
+def test_quantize_bitwise(scale_dtype, dev):
+    print(f"case quantize {scale_dtype}", flush=True)
+    x = _rand((1, 8, 777, 128), 1, 2.0)
+    x[0, 3, 5] = 0
+    q8, s = quantize(x.to(dev)[0].transpose(0, 1), scale_dtype=scale_dtype)  # strided rows -> token-major
+    want_q, want16, want32 = oracle.quantize(x[0].transpose(0, 1).contiguous())
+    assert torch.equal(q8.cpu(), want_q)
+    want_s = want16 if scale_dtype == torch.float16 else want32
+    assert torch.equal(s.cpu().view(torch.int16 if scale_dtype == torch.float16 else torch.int32),
+                       want_s.view(torch.int16 if scale_dtype == torch.float16 else torch.int32))
+    deq = dequantize(q8, s, torch.float32).cpu()
+    assert torch.equal(deq, oracle.dequantize(want_q, want_s))
+
+
+def test_quantize_fp32_input(dev):
+    print("case quantize_fp32", flush=True)
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(300, 8, 64, generator=g) * 7
+    q8, s = quantize(x.to(dev))
+    want_q, want16, _ = oracle.quantize(x)
+    assert torch.equal(q8.cpu(), want_q) and torch.equal(s.cpu().view(torch.int16), want16.view(torch.int16))
+
+
+def _check(got, ref, what):
+    err = (got.double().cpu() - ref).abs()
+    print(f"{what}: max_abs={err.max().item():.3e} mean_abs={err.mean().item():.3e}", flush=True)
+    assert err.max().item() < 2e-2 and err.mean().item() < 2e-3, what
+
+
+@pytest.mark.parametrize("n,H,Hkv,d,f16", [(1, 32, 8, 128, True), (300, 32, 8, 128, True), (4099, 32, 8, 128, False),
+                                           (20000, 16, 2, 64, True), (131072, 32, 8, 128, False)])
+def test_decode_int8_matches_oracle(n, H, Hkv, d, f16, dev):
+    print(f"case decode_int8 n={n} H={H}/{Hkv} d={d} f16={f16}", flush=True)
+    cap = n + 5  # spare capacity past n must be ignored
+    g = torch.Generator(device=dev).manual_seed(n)
+    k = torch.randn(cap, Hkv, d, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(cap, Hkv, d, device=dev, generator=g).to(torch.bfloat16)
+    q = torch.randn(H, d, device=dev, generator=g).to(torch.bfloat16)
+    sd = torch.float16 if f16 else torch.float32
+    k8, ks = quantize(k, scale_dtype=sd)
+    v8, vs = quantize(v, scale_dtype=sd)
+    k8[n:] = 127  # garbage past n
+    out = decode_int8(q, k8, ks, v8, vs, n, d ** -0.5)
+    torch.cuda.synchronize()
+    ref = oracle.decode(q, k8, ks, v8, vs, n, d ** -0.5)
+    _check(out, ref, f"decode_int8 n={n}")
+
+
+def test_decode_bf16_matches_sdpa(dev):
+    print("case decode_bf16", flush=True)
+    n, H, Hkv, d = 5000, 32, 8, 128
+    k, v, q = _rand((Hkv, n, d), 3), _rand((Hkv, n, d), 4), _rand((H, d), 5)
+    out = decode_bf16(q.to(dev), k.to(dev), v.to(dev), d ** -0.5)
+    ref = oracle.sdpa_ref(q[:, None], k, v, causal=False, scale=d ** -0.5, groups=H // Hkv)[:, 0]
+    _check(out, ref, "decode_bf16")
+
+
+def test_rope_inplace_bitwise(dev):
+    print("case rope", flush=True)
+    T, d = 5000, 128
+    cos, sin = rope_cos_sin(T, d)
+    x = _rand((1, 8, T, d), 6, 3.0)
+    y = x.to(dev).transpose(1, 2).contiguous().transpose(1, 2)  # strided [1, H, T, d] view like q_proj output
+    rope_inplace(y, cos.to(dev), sin.to(dev))
+    assert torch.equal(y.cpu(), rope_host(x, cos, sin))

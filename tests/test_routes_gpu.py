@@ -67,3 +67,27 @@ def test_budget_covers_all_eligible(dev):
     idx = hip_routes(inp["q"].to(dev), inp["k"].to(dev), num_heads=H, num_kv_heads=Hkv, sink=sink, window=window,
                      budget=T - sink - window, scaling=d ** -0.5).cpu()
     assert torch.equal(idx, torch.arange(sink, T - window, dtype=torch.int32).expand(H, -1))
+
+
+GOLDEN = ["config1", "small_mean", "odd_planted", "max_pool", "spread", "mha_d32", "vertical_sqrt", "config2"]
+
+
+@pytest.mark.parametrize("name", GOLDEN)
+def test_routes_match_reference_golden(name, dev):
+    """HIP routes against the reference's own routes() on the same seeded inputs (tests/golden): set-exact, with
+    the documented lower-index rule only where the reference's pooled values tie exactly at the boundary."""
+    import golden_routes
+
+    print(f"case golden {name}", flush=True)
+    g = golden_routes.case(name)
+    idx, pooled = hip_routes(g["q"].to(dev), g["k"].to(dev), num_heads=g["H"], num_kv_heads=g["Hkv"], sink=g["sink"],
+                             window=g["window"], budget=g["budget"], n_route=g["n_route"], route_pool=g["route_pool"],
+                             route_queries=g["route_queries"], scaling=g["scaling"], return_pooled=True)
+    torch.cuda.synchronize()
+    tied = golden_routes.check_against_golden(idx.cpu(), g, pooled=pooled.cpu(), what=name)
+    if name != "max_pool":
+        assert tied == 0 and torch.equal(idx.cpu(), g["routes"])
+    if g["planted"] is not None:
+        G = g["H"] // g["Hkv"]
+        for h in range(g["H"]):
+            assert set(g["planted"][0, h // G].tolist()) <= set(idx[h].cpu().tolist())

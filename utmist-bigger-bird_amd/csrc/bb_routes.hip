@@ -3,7 +3,9 @@
 // [sink, n - window), returned ascending as int32.
 //
 // The arithmetic is fixed so that results are reproducible bit for bit on any device and by the CPU oracle:
-//   s    = bf16_rne(exact q.k)             float64 FMA chain from bf16 operands (exact), one RNE step to bf16
+//   s    = bf16_rne(q.k in the reference's order)   torch's CPU bf16 matmul (oneDNN, AMX-BF16): per 32-element block
+//                                                   of d, fp32 chains over the even and the odd elements, then
+//                                                   acc = acc + (even + odd); one RNE step to bf16
 //   x    = fp32(s * scaling); M = row max over causal keys j <= qpos
 //   e    = det_exp2(fp32(fp32(x - M) * log2e))
 //   Z    = sum floor(e * 2^40) (uint64)    p = fp32(e * fp32(2^40 / double(Z)))
@@ -11,7 +13,7 @@
 // Integer sums make every reduction order-independent; there are no floating-point atomics.
 //
 // Kernels (all on the caller's stream, no host synchronisation):
-//   scores_kernel   exact scores of G*r route rows against a 64-key block, bf16 to the workspace, partial row max
+//   scores_kernel   scores of G*r route rows against a 256-key range, bf16 to the workspace, partial row max
 //   rowmax_kernel   partial maxima -> row max
 //   rowsum_kernel   fixed-point partial row sums over 1024-key blocks
 //   invz_kernel     partial sums -> fp32 scale 2^40 / Z per row
@@ -27,7 +29,8 @@
 namespace bb {
 namespace {
 
-constexpr int kScoreKeys = 64;    // keys per scores_kernel workgroup
+constexpr int kScoreKeys = 32;    // keys per scores_kernel block (8 key groups of 4)
+constexpr int kScoreIters = 8;    // key blocks per scores_kernel workgroup
 constexpr int kSumKeys = 1024;    // keys per rowsum_kernel workgroup
 constexpr int kPoolKeys = 256;    // keys per pooled_kernel workgroup
 constexpr int kMaxRows = 256;     // G * r handled by one scores workgroup (rows beyond this use more row blocks)
@@ -40,17 +43,20 @@ struct RouteGeom {
   int64_t ns;  // score row stride: n rounded up to 8 (16-byte aligned rows)
 };
 
-// Exact scores: one workgroup = up to 256 route rows x 64 keys of one KV head.
-// Thread t computes rows 8*(t/8)..+7 against keys 8*(t%8)..+7 with a float64 FMA chain over d in ascending order.
+// Scores: one workgroup = up to 256 route rows of one KV head x kScoreIters blocks of kScoreKeys keys.
+// Q^T stays in LDS for the whole key range; each key block is staged as fp32 K^T. Thread t owns rows
+// 8*(t%32)..+7 and keys 4*(t/32)..+3 of a block. Every score is built in the reference's accumulation order: per
+// 32-element block of d, two sequential fp32 chains over the even and the odd elements (fmaf of two bf16 values is
+// one rounding of the exact product sum), then acc = acc + (even + odd).
 template <int D>
 __global__ __launch_bounds__(256) void scores_kernel(RoutesParams p, RouteGeom g, float* __restrict__ pmax) {
-  __shared__ __attribute__((aligned(16))) uint16_t qs[D][kMaxRows];  // Q^T (bf16)
-  __shared__ __attribute__((aligned(16))) double ks[D][kScoreKeys];  // K^T (float64)
-  __shared__ float rmax_part[kMaxRows][8];
+  static_assert(D % 32 == 0, "head_dim must be a multiple of 32");
+  __shared__ __attribute__((aligned(16))) uint16_t qs[D][kMaxRows];        // Q^T (bf16)
+  __shared__ __attribute__((aligned(16))) float ks[D][kScoreKeys + 4];     // K^T (fp32), padded rows
+  __shared__ float rmax_part[kMaxRows][kScoreKeys / 4 + 1];
   const int tid = threadIdx.x;
-  const int kb = blockIdx.x, rblk = blockIdx.y, bkv = blockIdx.z;
+  const int kchunk = blockIdx.x, rblk = blockIdx.y, bkv = blockIdx.z;
   const int batch = bkv / p.Hkv, kvh = bkv % p.Hkv;
-  const int64_t j0 = (int64_t)kb * kScoreKeys;
   const int row0 = rblk * kMaxRows;
   const int nrows = g.rows - row0 < kMaxRows ? g.rows - row0 : kMaxRows;
 
@@ -69,80 +75,105 @@ __global__ __launch_bounds__(256) void scores_kernel(RoutesParams p, RouteGeom g
       qs[8 * c8 + 2 * w + 1][row] = (uint16_t)(v[w] >> 16);
     }
   }
-  // stage K^T as float64
-  const uint16_t* kbase = p.k + (int64_t)bkv * p.sk0;
-  for (int e = tid; e < kScoreKeys * (D / 8); e += 256) {
-    const int key = e / (D / 8), c8 = e % (D / 8);
-    const int64_t j = j0 + key;
-    u32x4_t v = j < p.n ? ld16(kbase + j * p.sk1 + 8 * c8) : u32x4_t{0, 0, 0, 0};
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      ks[8 * c8 + 2 * w][key] = (double)bf16_to_f32((uint16_t)(v[w] & 0xffffu));
-      ks[8 * c8 + 2 * w + 1][key] = (double)bf16_to_f32((uint16_t)(v[w] >> 16));
-    }
-  }
-  __syncthreads();
 
-  const int rb = tid >> 3, kq = tid & 7;
-  double acc[8][8];
+  const int rg = tid & 31, kg = tid >> 5;
+  int64_t qp[8];
 #pragma unroll
-  for (int a = 0; a < 8; ++a)
+  for (int a = 0; a < 8; ++a) {
+    const int row = 8 * rg + a;
+    qp[a] = row < nrows ? p.qpos[(row0 + row) % p.r] : -1;
+  }
+  float rmax[8];
 #pragma unroll
-    for (int b = 0; b < 8; ++b) acc[a][b] = 0.0;
-  for (int d = 0; d < D; ++d) {
-    const u32x4_t qv = *reinterpret_cast<const u32x4_t*>(&qs[d][8 * rb]);
-    double qd[8];
+  for (int a = 0; a < 8; ++a) rmax[a] = -__builtin_huge_valf();
+  const uint16_t* kbase = p.k + (int64_t)bkv * p.sk0;
+  uint16_t* srow_base = p.scores + (int64_t)bkv * g.rows * g.ns;
+
+  for (int it = 0; it < kScoreIters; ++it) {
+    const int64_t j0 = ((int64_t)kchunk * kScoreIters + it) * kScoreKeys;
+    if (j0 >= p.n) break;
+    __syncthreads();  // previous block's K^T fully consumed (and Q^T staged on the first pass)
+    for (int e = tid; e < kScoreKeys * (D / 8); e += 256) {
+      const int key = e / (D / 8), c8 = e % (D / 8);
+      const int64_t j = j0 + key;
+      const u32x4_t v = j < p.n ? ld16(kbase + j * p.sk1 + 8 * c8) : u32x4_t{0, 0, 0, 0};
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      qd[2 * w] = (double)bf16_to_f32((uint16_t)(qv[w] & 0xffffu));
-      qd[2 * w + 1] = (double)bf16_to_f32((uint16_t)(qv[w] >> 16));
+      for (int w = 0; w < 4; ++w) {
+        ks[8 * c8 + 2 * w][key] = bf16_to_f32((uint16_t)(v[w] & 0xffffu));
+        ks[8 * c8 + 2 * w + 1][key] = bf16_to_f32((uint16_t)(v[w] >> 16));
+      }
     }
-    double kd[8];
-#pragma unroll
-    for (int b = 0; b < 8; ++b) kd[b] = ks[d][8 * kq + b];
+    __syncthreads();
+
+    float acc[8][4];
 #pragma unroll
     for (int a = 0; a < 8; ++a)
 #pragma unroll
-      for (int b = 0; b < 8; ++b) acc[a][b] = fma(qd[a], kd[b], acc[a][b]);
-  }
+      for (int b = 0; b < 4; ++b) acc[a][b] = 0.0f;
+    for (int d0 = 0; d0 < D; d0 += 32) {
+      float ev[8][4], od[8][4];
+#pragma unroll
+      for (int a = 0; a < 8; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) ev[a][b] = od[a][b] = 0.0f;
+#pragma unroll 4
+      for (int t = 0; t < 16; ++t) {
+        const int de = d0 + 2 * t;
+        const u32x4_t qe = *reinterpret_cast<const u32x4_t*>(&qs[de][8 * rg]);
+        const u32x4_t qo = *reinterpret_cast<const u32x4_t*>(&qs[de + 1][8 * rg]);
+        const f32x4_t ke = *reinterpret_cast<const f32x4_t*>(&ks[de][4 * kg]);
+        const f32x4_t ko = *reinterpret_cast<const f32x4_t*>(&ks[de + 1][4 * kg]);
+#pragma unroll
+        for (int a = 0; a < 8; ++a) {
+          const float fe = bf16_to_f32((uint16_t)(qe[a >> 1] >> (16 * (a & 1))));
+          const float fo = bf16_to_f32((uint16_t)(qo[a >> 1] >> (16 * (a & 1))));
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            ev[a][b] = __builtin_fmaf(fe, ke[b], ev[a][b]);
+            od[a][b] = __builtin_fmaf(fo, ko[b], od[a][b]);
+          }
+        }
+      }
+#pragma unroll
+      for (int a = 0; a < 8; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = acc[a][b] + (ev[a][b] + od[a][b]);
+    }
 
-  // round, mask, store bf16, partial max of x = s * scaling
-  uint16_t* srow_base = p.scores + (int64_t)bkv * g.rows * g.ns;
+    // round to bf16, causal mask, store, running row max of x = s * scaling
 #pragma unroll
-  for (int a = 0; a < 8; ++a) {
-    const int row = 8 * rb + a;
-    const int rr = row0 + row;
-    float mx = -__builtin_huge_valf();
-    uint32_t packed[4];
-    const int64_t qp = row < nrows ? p.qpos[rr % p.r] : -1;
+    for (int a = 0; a < 8; ++a) {
+      const int row = 8 * rg + a;
+      const int64_t jj = j0 + 4 * kg;
+      uint16_t sb[4];
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      const int64_t j = j0 + 8 * kq + b;
-      uint16_t sb = 0xff80u;  // -inf
-      if (row < nrows && j < p.n && j <= qp) {
-        sb = bf16_from_f64(acc[a][b]);
-        mx = fmaxf(mx, bf16_to_f32(sb) * p.scaling);
+      for (int b = 0; b < 4; ++b) {
+        const int64_t j = jj + b;
+        sb[b] = 0xff80u;  // -inf
+        if (j < p.n && j <= qp[a]) {
+          sb[b] = f32_to_bf16(acc[a][b]);
+          rmax[a] = fmaxf(rmax[a], bf16_to_f32(sb[b]) * p.scaling);
+        }
       }
-      if (b & 1) packed[b >> 1] |= (uint32_t)sb << 16;
-      else packed[b >> 1] = sb;
-    }
-    if (row < nrows) {
-      const int64_t jj = j0 + 8 * kq;
-      uint16_t* dst = srow_base + (int64_t)rr * g.ns + jj;
-      if (jj + 8 <= p.n) {
-        st16(dst, u32x4_t{packed[0], packed[1], packed[2], packed[3]});
-      } else {
-        for (int b = 0; b < 8 && jj + b < p.n; ++b) dst[b] = (uint16_t)(packed[b >> 1] >> (16 * (b & 1)));
+      if (row < nrows) {
+        uint16_t* dst = srow_base + (int64_t)(row0 + row) * g.ns + jj;
+        if (jj + 4 <= p.n) {
+          *reinterpret_cast<u32x2_t*>(dst) =
+              u32x2_t{(uint32_t)sb[0] | ((uint32_t)sb[1] << 16), (uint32_t)sb[2] | ((uint32_t)sb[3] << 16)};
+        } else {
+          for (int b = 0; b < 4 && jj + b < p.n; ++b) dst[b] = sb[b];
+        }
       }
     }
-    rmax_part[row][kq] = mx;
   }
+#pragma unroll
+  for (int a = 0; a < 8; ++a) rmax_part[8 * rg + a][kg] = rmax[a];
   __syncthreads();
   if (tid < nrows) {
     float mx = rmax_part[tid][0];
 #pragma unroll
-    for (int b = 1; b < 8; ++b) mx = fmaxf(mx, rmax_part[tid][b]);
-    pmax[((int64_t)bkv * g.n_kb1 + kb) * g.rows + row0 + tid] = mx;
+    for (int b = 1; b < kScoreKeys / 4; ++b) mx = fmaxf(mx, rmax_part[tid][b]);
+    pmax[((int64_t)bkv * g.n_kb1 + kchunk) * g.rows + row0 + tid] = mx;
   }
 }
 
@@ -364,7 +395,7 @@ RouteGeom geom(int64_t n, int H, int Hkv, int r) {
   RouteGeom g;
   g.G = H / Hkv;
   g.rows = g.G * r;
-  g.n_kb1 = (int)((n + kScoreKeys - 1) / kScoreKeys);
+  g.n_kb1 = (int)((n + kScoreKeys * kScoreIters - 1) / (kScoreKeys * kScoreIters));
   g.n_kb2 = (int)((n + kSumKeys - 1) / kSumKeys);
   g.row_blocks = (g.rows + kMaxRows - 1) / kMaxRows;
   g.ns = (n + 7) & ~(int64_t)7;
