@@ -40,6 +40,8 @@ def parse_args():
     ap.add_argument("--T", type=int, default=131072)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a plain 1 GiB device copy 5 times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--cpu-sample-blocks", type=int, default=96,
                     help="64-row blocks (of 4 heads each) timed for the CPU baseline")
     return ap.parse_args()
@@ -126,6 +128,14 @@ def main():
 
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a ROCm GPU")
+    if args.copy_probe:
+        src = torch.ones(1 << 29, dtype=torch.int16, device="cuda")  # 1 GiB
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": src.numel() * 2, "launches": 5}), flush=True)
+        return
     from bigger_bird_amd import RDAttention, _lib
     from bigger_bird_amd.synth import attended_pairs, make_inputs
 

@@ -6,7 +6,7 @@
 #include <cstdlib>
 #include <cstring>
 
-#include "../../include/bb_attn.h"
+#include "bb_attn.h"
 #include "bb_internal.h"
 
 namespace {
@@ -49,6 +49,16 @@ int flash_waves() {
     return v == 4 ? 4 : 8;
   }();
   return w;
+}
+
+// The software-pipelined main-pass kernel is used wherever it applies; BB_FLASH_PIPE=0 selects the generic kernel
+// (for measurement).
+bool flash_pipe_enabled() {
+  static bool on = [] {
+    const char* e = getenv("BB_FLASH_PIPE");
+    return !(e && e[0] == '0');
+  }();
+  return on;
 }
 
 FlashSchedule flash_schedule(int BH, int64_t T, int64_t N, int num_heads, int kv_groups, int64_t front, int64_t window,
@@ -100,6 +110,7 @@ static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 size_t bb_sparse_flash_workspace(int BH, int64_t T, int64_t N, int D, int num_heads, int kv_groups, int64_t front,
                                  int64_t window, int route_k, int64_t row_end, int have_vt) {
   if (BH <= 0 || T <= 0 || N <= 0 || kv_groups <= 0 || BH % kv_groups) return 0;
+  if (window >= N) route_k = 0;
   if (row_end <= 0 || row_end > T) row_end = T;
   FlashSchedule s = flash_schedule(BH, T, N, num_heads, kv_groups, front, window, route_k, row_end);
   size_t bytes = 0;
@@ -148,6 +159,9 @@ int bb_sparse_flash(const void* q, const int64_t* sq, const void* k, const int64
   if (front > N) front = N;
   if (row_end <= 0 || row_end > T) row_end = T;
 
+  // A routed key j is attended only when j <= q - window; with window >= N no key qualifies, so the routes are
+  // dropped (this is how the exact tail calls the kernel: window = N with a -1 route list).
+  if (window >= N) route_k = 0;
   FlashSchedule s = flash_schedule(BH, T, N, num_heads, kv_groups, front, window, route_k, row_end);
   bb::FlashParams p;
   memset(&p, 0, sizeof(p));
@@ -200,6 +214,8 @@ int bb_sparse_flash(const void* q, const int64_t* sq, const void* k, const int64
     if (e != hipSuccess) return hip_status(e, "bb_sparse_flash split kernel");
     return hip_status(bb::launch_flash_merge(p, D, st), "bb_sparse_flash merge kernel");
   }
+  if (flash_pipe_enabled() && s.hpw == 4 && bb::flash_pipe_supported(p, D))
+    return hip_status(bb::launch_flash_pipe(p, st), "bb_sparse_flash pipelined kernel");
   return hip_status(bb::launch_flash(p, D, s.hpw, false, st), "bb_sparse_flash kernel");
 }
 

@@ -25,9 +25,12 @@ BB_DEV uint16_t f32_to_bf16(float f) {
   return (uint16_t)(u >> 16);
 }
 
-// Two floats -> packed bf16x2 (RNE), low half = a.
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
+
+// Two floats -> packed bf16x2 (RNE, one v_cvt_pk_bf16_f32), low half = a.
 BB_DEV uint32_t pack_bf16x2(float a, float b) {
-  return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+  const bf16x2_t v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 BB_DEV bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }

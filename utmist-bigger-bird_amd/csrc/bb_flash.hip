@@ -26,109 +26,11 @@
 //   * blockIdx -> (KV head, row tile) is XCD-aware: consecutive workgroups on one XCD walk neighbouring row tiles of
 //     one KV head, so their windows overlap in that XCD's L2.
 #include "bb_common.h"
+#include "bb_flash_tiles.h"
 #include "bb_internal.h"
 
 namespace bb {
 namespace {
-
-constexpr int kTileKeys = 64;
-constexpr float kRescaleThreshold = 8.0f;  // log2 units
-
-template <int D>
-struct Layout {
-  static constexpr int CPR = D / 8;                 // 16-byte chunks per K row
-  static constexpr int kKElems = kTileKeys * D;     // K tile: 64 rows x D, chunk slot = chunk ^ (row % CPR)
-  static constexpr int kVElems = D * kTileKeys;     // V^T tile: D rows x 64 keys, slot = chunk ^ ((d >> 1) & 7)
-  static constexpr int kTileElems = kKElems + kVElems;
-  static constexpr int kBlocks = kKElems * 2 / 1024;  // 1 KB direct-load blocks per K (or V^T) tile
-};
-
-template <int D>
-BB_DEV int k_off(int row, int chunk) {
-  return row * D + 8 * (chunk ^ (row & (Layout<D>::CPR - 1)));
-}
-BB_DEV int vt_off(int d, int chunk) { return d * kTileKeys + 8 * (chunk ^ ((d >> 1) & 7)); }
-
-BB_DEV void lds_dma16(const void* g, uint16_t* lds) {
-  __builtin_amdgcn_global_load_lds(g, reinterpret_cast<__attribute__((address_space(3))) void*>(
-                                          reinterpret_cast<uintptr_t>(lds)),
-                                   16, 0, 0);
-}
-
-BB_DEV void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
-
-// Issue direct loads of one window tile (K rows k0..k0+63, V^T columns k0..k0+63). Block b of the K (V^T) tile is
-// written by wave b % NW; lane l of a block lands at byte 16 * l of it.
-template <int D, int NW>
-BB_DEV void issue_window_tile(uint16_t* kl, uint16_t* vt, const uint16_t* kbase, int64_t sk1, const uint16_t* vtbase,
-                              int64_t np, int64_t k0, int64_t N, int wave, int lane) {
-  for (int b = wave; b < Layout<D>::kBlocks; b += NW) {
-    const int e = b * 512 + 8 * lane;
-    const int row = e / D, slot = (e % D) / 8;
-    const int chunk = slot ^ (row & (Layout<D>::CPR - 1));
-    int64_t pos = k0 + row;
-    if (pos >= N) pos = N - 1;  // clamped rows are masked out
-    lds_dma16(kbase + pos * sk1 + 8 * chunk, kl + b * 512);
-  }
-  for (int b = wave; b < Layout<D>::kBlocks; b += NW) {
-    const int d = 8 * b + lane / 8, slot = lane % 8;
-    const int chunk = slot ^ ((d >> 1) & 7);
-    lds_dma16(vtbase + (int64_t)d * np + k0 + 8 * chunk, vt + b * 512);
-  }
-}
-
-template <int D, int QB>
-struct WaveState {
-  bf16x8_t qf[QB][D / 16];
-  f32x16_t o[QB][D / 32];
-  float m[QB];
-  float l[QB];
-};
-
-BB_DEV int clamp64(int64_t x, int lo, int hi) { return x < lo ? lo : (x > hi ? hi : (int)x); }
-
-// Window/front mask of one tile for one query row, reduced to int32 thresholds on the tile-relative key kk:
-// valid iff kk <= causal && kk < in_n && (kk < front || kk > win).
-struct WindowMask {
-  int64_t k0, N, front, window;
-  const uint8_t* km;
-  struct Row {
-    int causal, in_n, front, win;
-    const uint8_t* km;
-    BB_DEV bool operator()(int kk) const {
-      bool ok = kk <= causal && kk < in_n && (kk < front || kk > win);
-      if (km) ok = ok && km[kk];
-      return ok;
-    }
-  };
-  BB_DEV Row row(int64_t q) const {
-    return Row{clamp64(q - k0, -1, kTileKeys), clamp64(N - k0, 0, kTileKeys), clamp64(front - k0, 0, kTileKeys),
-               clamp64(q - window - k0, -1, kTileKeys), km ? km + k0 : nullptr};
-  }
-};
-
-// Routed mask: gathered key kk (LDS list, -1 = empty) is valid iff key <= q - window and q is in this route group.
-struct RoutedMask {
-  const int32_t* keys;
-  int64_t window, route_chunk, group;
-  const uint8_t* km;
-  struct Row {
-    const int32_t* keys;
-    int lim;
-    bool grp;
-    const uint8_t* km;
-    BB_DEV bool operator()(int kk) const {
-      const int key = keys[kk];
-      bool ok = grp && key >= 0 && key <= lim;
-      if (km) ok = ok && km[key >= 0 ? key : 0];
-      return ok;
-    }
-  };
-  BB_DEV Row row(int64_t q) const {
-    const int64_t lim = q - window;
-    return Row{keys, lim > 0x7fffffff ? 0x7fffffff : (lim < -1 ? -1 : (int)lim), q / route_chunk == group, km};
-  }
-};
 
 // One 64-key tile for one wave: S^T = K Q^T, online softmax, O^T += V^T P^T.
 template <int D, int QB, bool MASKED, typename Mask>
@@ -201,13 +103,11 @@ BB_DEV void tile_step(WaveState<D, QB>& st, const uint16_t* kl, const uint16_t* 
   for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const int c0 = 4 * kb + 2 * u;
+      const int unit = 2 * (2 * kb + u) + h;
 #pragma unroll
       for (int dv = 0; dv < D / 32; ++dv) {
         const int d = 32 * dv + li;
-        const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vt + vt_off(d, c0) + 4 * h);
-        const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vt + vt_off(d, c0 + 1) + 4 * h);
-        const bf16x8_t a = as_bf16x8(u32x4_t{lo[0], lo[1], hi[0], hi[1]});
+        const bf16x8_t a = as_bf16x8(*reinterpret_cast<const u32x4_t*>(vt + vt_off(d, unit)));
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) st.o[qb][dv] = mfma32(a, pk[qb][kb][u], st.o[qb][dv]);
       }
@@ -403,7 +303,7 @@ __global__ __launch_bounds__(64 * NW, 1) void flash_kernel(FlashParams p) {
               const uint32_t lo = __builtin_amdgcn_perm(vr[1][w], vr[0][w], sel);
               const uint32_t hi = __builtin_amdgcn_perm(vr[3][w], vr[2][w], sel);
               const int d = 8 * bq + e;
-              *reinterpret_cast<u32x2_t*>(vt + vt_off(d, a >> 1) + 4 * (a & 1)) = u32x2_t{lo, hi};
+              *reinterpret_cast<u32x2_t*>(vt + vt_off(d, 2 * (a >> 2) + (a & 1)) + 4 * ((a >> 1) & 1)) = u32x2_t{lo, hi};
             }
           }
         }
@@ -498,7 +398,8 @@ __global__ __launch_bounds__(256) void flash_merge_kernel(FlashParams p) {
   }
 }
 
-// V [n_kvbh][N][D] (strided) -> V^T [n_kvbh][D][np], zero columns for keys >= N.
+// V [n_kvbh][N][D] (strided) -> V^T [n_kvbh][D][np], zero columns for keys >= N; keys of every 16-key group in
+// vt_key_pos order.
 template <int D>
 __global__ __launch_bounds__(256) void transpose_v_kernel(const uint16_t* __restrict__ v, int64_t sv0, int64_t sv1,
                                                           int64_t N, int64_t np, uint16_t* __restrict__ vt) {
@@ -520,10 +421,13 @@ __global__ __launch_bounds__(256) void transpose_v_kernel(const uint16_t* __rest
   uint16_t* dst = vt + (int64_t)kvbh * D * np;
   for (int e = threadIdx.x; e < D * (kTileKeys / 8); e += 256) {
     const int d = e / (kTileKeys / 8), c8 = e % (kTileKeys / 8);
+    // row position 8 c8 + j holds key vt_key_pos(8 c8 + j) (the permutation is its own inverse)
     uint32_t w[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      w[i] = (uint32_t)tile[8 * c8 + 2 * i][d] | ((uint32_t)tile[8 * c8 + 2 * i + 1][d] << 16);
+    for (int i = 0; i < 4; ++i) {
+      const int ka = vt_key_pos(8 * c8 + 2 * i);  // positions 2i and 2i + 1 hold consecutive keys
+      w[i] = (uint32_t)tile[ka][d] | ((uint32_t)tile[ka + 1][d] << 16);
+    }
     st16(dst + (int64_t)d * np + k0 + 8 * c8, u32x4_t{w[0], w[1], w[2], w[3]});
   }
 }

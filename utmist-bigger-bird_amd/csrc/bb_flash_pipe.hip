@@ -1,0 +1,506 @@
+// Ping-pong sink + causal window + routed sparse flash attention for gfx950 (head_dim 128, four query heads per
+// KV head, no token mask): the main pass of Bigger Bird v3 prefill at production shape.
+//
+// Same semantics as bb_flash.hip (kernels/bigger_bird_flash.py:42-96 of the reference). Work decomposition:
+//   * a workgroup = 8 waves = the 4 query heads of one KV head x 2 blocks of 32 query rows (64 rows); every K / V^T
+//     tile staged in LDS is read by all 8 waves (GQA reuse inside the workgroup);
+//   * waves w and w + 4 share a SIMD. Per 64-key tile a wave runs an MFMA phase  (O^T += V^T(t-1) P(t-1)^T,
+//     S(t) = K(t) Q^T: 32 MFMAs) and a VALU phase (online softmax of S(t) into P(t)), separated by workgroup
+//     barriers. Waves 4..7 start one barrier late, so on every SIMD one wave is in its MFMA phase while the other is
+//     in its VALU phase: the matrix cores and the VALUs work at the same time instead of in turn;
+//   * K and V^T tiles stream global->LDS with 16-byte buffer loads straight into LDS (no staging registers) through a
+//     four-stage ring, issued two tiles ahead; rows past N read as zeros through the buffer resource bounds;
+//   * the exponent offset is refreshed only when a tile max exceeds it by more than 2^8 (O rescales stay rare);
+//   * routed keys differ per head: after the window loop the two waves of a head gather its routed K rows and V rows
+//     into that head's LDS tile.
+#include "bb_common.h"
+#include "bb_flash_tiles.h"
+#include "bb_internal.h"
+
+namespace bb {
+namespace {
+
+constexpr int PD = 128;                 // head_dim
+constexpr int PNW = 8;                  // waves per workgroup
+constexpr int PHEADS = 4;               // query heads per workgroup
+constexpr int PROWS = 64;               // query rows per workgroup (2 blocks of 32)
+constexpr int PTE = kTileKeys * PD;     // elements of one K (or V^T) tile
+constexpr int PST = 4;                  // ring stages, each a K tile and a V^T tile
+constexpr int PBLK = PTE * 2 / 1024;    // 1 KB direct-load blocks per tile (16)
+constexpr int PLDS = PST * 2 * PTE;     // 128 KB; the routed phase reuses it as 4 heads x (K + V^T)
+static_assert(PHEADS * 2 * PTE <= PLDS, "routed tiles fit the ring");
+
+typedef __attribute__((__vector_size__(4 * sizeof(int32_t)))) int32_t i32x4_t;
+
+// Element masks. In the S^T layout lane (li, h) holds, for key half kb of a tile, the keys
+// kk = 32 kb + 4 h + j(r), j(r) = 8 (r / 4) + r % 4, r = 0..15; j(r) grows with r, so each of the conditions
+// kk <= q - k0 (causal), kk < front - k0 and kk > q - window - k0 selects a prefix or a suffix of r. Masks are
+// returned as 16 bits per key half.
+BB_DEV uint32_t prefix_upto(int a) {  // bits r with j(r) <= a
+  if (a < 0) return 0u;
+  if (a >= 27) return 0xFFFFu;
+  const int n = 4 * (a >> 3) + ((a & 7) < 3 ? (a & 7) + 1 : 4);
+  return (1u << n) - 1u;
+}
+
+BB_DEV int clamp_rel(int64_t x) { return (int)(x > 64 ? 64 : (x < -1 ? -1 : x)); }
+
+struct PipeWindowMask {  // front | causal window (nothing when !any)
+  int64_t k0, front, window;
+  bool any;
+  BB_DEV uint32_t bits(int64_t q, int kb, int h) const {
+    if (!any) return 0u;
+    const int64_t base = k0 + 32 * kb + 4 * h;
+    const uint32_t causal = prefix_upto(clamp_rel(q - base));
+    const uint32_t fr = prefix_upto(clamp_rel(front - base - 1));
+    const uint32_t win = ~prefix_upto(clamp_rel(q - window - base)) & 0xFFFFu;
+    return causal & (fr | win);
+  }
+};
+
+struct PipeRoutedMask {  // gathered key list (-1 = empty): key <= q - window, and q in the list's route group
+  const int32_t* keys;
+  int64_t window, route_chunk, group;
+  BB_DEV uint32_t bits(int64_t q, int kb, int h) const {
+    const int64_t lim64 = q / route_chunk == group ? q - window : -1;
+    const int lim = lim64 > 0x7fffffff ? 0x7fffffff : (lim64 < -1 ? -1 : (int)lim64);
+    uint32_t b = 0;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const i32x4_t k4 = *reinterpret_cast<const i32x4_t*>(keys + 32 * kb + 8 * g + 4 * h);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) b |= (uint32_t)(k4[e] >= 0 && k4[e] <= lim) << (4 * g + e);
+    }
+    return b;
+  }
+};
+
+// Direct global->LDS tile loads through buffer resources (one per KV head: rows past N read as zeros, and every
+// per-lane offset is a loop-invariant 32-bit value). Block b (1 KB) of a tile is loaded by wave b % 8; its lanes
+// land at byte 16 * lane of the block.
+struct TileLoader {
+  __amdgpu_buffer_rsrc_t krs, vrs;
+  uint32_t kvoff, vvoff;    // per-lane byte offsets of this wave's first block
+  uint32_t kstep, vstep;    // byte distance between this wave's two blocks (8 blocks apart)
+  uint32_t krow_bytes;
+  int wave;
+
+  BB_DEV void init(const uint16_t* kbase, int64_t sk1, int64_t N, const uint16_t* vtbase, int64_t np, int w,
+                   int lane) {
+    wave = w;
+    krow_bytes = (uint32_t)(sk1 * 2);
+    krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kbase), 0, (int)(N * sk1 * 2), 0x00020000);
+    vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vtbase), 0, (int)(PD * np * 2), 0x00020000);
+    // K block b = w + 8i: rows 4b + lane/16, 16-byte chunk (lane%16) ^ (row%16); row%16 does not depend on i
+    const int krow = 4 * w + lane / 16;
+    kvoff = (uint32_t)krow * krow_bytes + 16u * (uint32_t)((lane % 16) ^ (krow & 15));
+    kstep = 32u * krow_bytes;
+    // V^T block b = w + 8i: d = 8b + lane/8, 16-byte unit (lane%8) ^ vt_swz(d); vt_swz(d) does not depend on i
+    const int d = 8 * w + lane / 8;
+    vvoff = (uint32_t)d * (uint32_t)(np * 2) + 16u * (uint32_t)((lane % 8) ^ vt_swz(d));
+    vstep = 64u * (uint32_t)(np * 2);
+  }
+  BB_DEV void tile(uint16_t* kl, uint16_t* vt, int64_t k0) const {
+    // The K tile offset goes into the per-lane offset: the buffer range check covers it (and not the scalar
+    // offset), so rows past N read as zeros instead of touching memory past the tensor.
+    const uint32_t kb = kvoff + (uint32_t)k0 * krow_bytes, vb = (uint32_t)k0 * 2u;
+#pragma unroll
+    for (int i = 0; i < PBLK / PNW; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          krs, reinterpret_cast<__attribute__((address_space(3))) void*>(
+                   reinterpret_cast<uintptr_t>(kl + (wave + PNW * i) * 512)),
+          16, kb + i * kstep, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < PBLK / PNW; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          vrs, reinterpret_cast<__attribute__((address_space(3))) void*>(
+                   reinterpret_cast<uintptr_t>(vt + (wave + PNW * i) * 512)),
+          16, vvoff, vb + i * vstep, 0, 0);
+  }
+};
+
+BB_DEV void vm_wait_tile(bool one_tile_in_flight) {
+  // vmcnt(4) keeps the most recent tile's 4 loads (2 K + 2 V^T blocks) in flight; vmcnt(0) drains everything
+  if (one_tile_in_flight) __builtin_amdgcn_s_waitcnt(0x0F74);
+  else __builtin_amdgcn_s_waitcnt(0x0F70);
+}
+
+// Workgroup barrier without a memory fence: the tile ring publishes its direct loads with explicit vmcnt waits,
+// so the barrier must not drain the loads still in flight for the tile after next (a __syncthreads fence would).
+// The wavefront-scope fences emit nothing but keep the compiler from moving memory accesses across it.
+BB_DEV void ring_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+}
+
+struct PingState {
+  bf16x8_t qf[PD / 16];
+  f32x16_t o[PD / 32];
+  f32x16_t s[2];       // S^T of the current tile, per 32-key half
+  bf16x8_t pk[2][2];   // P^T fragments of the previous tile
+  float m, l;
+};
+
+// S(t) = K Q^T (16 MFMAs).
+BB_DEV void ping_qk(PingState& st, const uint16_t* kl, int li, int h) {
+  st.s[0] = f32x16_t{};
+  st.s[1] = f32x16_t{};
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int dk = 0; dk < PD / 16; ++dk) {
+      const bf16x8_t a = as_bf16x8(*reinterpret_cast<const u32x4_t*>(kl + k_off<PD>(32 * kb + li, 2 * dk + h)));
+      st.s[kb] = mfma32(a, st.qf[dk], st.s[kb]);
+    }
+}
+
+// O^T += V^T P^T (16 MFMAs).
+BB_DEV void ping_pv(PingState& st, const uint16_t* vt, int li, int h) {
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int unit = 2 * (2 * kb + u) + h;
+#pragma unroll
+      for (int dv = 0; dv < PD / 32; ++dv) {
+        const int d = 32 * dv + li;
+        st.o[dv] = mfma32(as_bf16x8(*reinterpret_cast<const u32x4_t*>(vt + vt_off(d, unit))), st.pk[kb][u], st.o[dv]);
+      }
+    }
+}
+
+// MFMA phase of the window loop: O^T += V^T(t-1) P(t-1)^T (16 MFMAs), then S(t) = K(t) Q^T (16 MFMAs), with the LDS
+// fragment reads software-pipelined four MFMAs ahead through a register ring (the LDS latency would otherwise idle the
+// matrix core between each read and the MFMA that consumes it). Fragment i < 16 is the V^T fragment of PV step
+// (kb, u, dv) = (i / 8, i / 4 % 2, i % 4); fragment 16 + j the K fragment of QK step (kb, dk) = (j / 8, j % 8).
+constexpr int kRing = 4;
+BB_DEV const u32x4_t* ping_frag(const uint16_t* kl, const uint16_t* vt, int i, int li, int h) {
+  if (i < 16) {
+    const int kb = i / 8, u = (i / 4) % 2, dv = i % 4;
+    return reinterpret_cast<const u32x4_t*>(vt + vt_off(32 * dv + li, 2 * (2 * kb + u) + h));
+  }
+  const int j = i - 16, kb = j / 8, dk = j % 8;
+  return reinterpret_cast<const u32x4_t*>(kl + k_off<PD>(32 * kb + li, 2 * dk + h));
+}
+
+BB_DEV void ping_mfma_phase(PingState& st, const uint16_t* kl, const uint16_t* vt, int li, int h) {
+  u32x4_t ring[kRing];
+#pragma unroll
+  for (int i = 0; i < kRing; ++i) ring[i] = *ping_frag(kl, vt, i, li, h);
+  st.s[0] = f32x16_t{};
+  st.s[1] = f32x16_t{};
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const bf16x8_t a = as_bf16x8(ring[i % kRing]);
+    if (i < 16) {
+      const int kb = i / 8, u = (i / 4) % 2, dv = i % 4;
+      st.o[dv] = mfma32(a, st.pk[kb][u], st.o[dv]);
+    } else {
+      const int j = i - 16, kb = j / 8, dk = j % 8;
+      st.s[kb] = mfma32(a, st.qf[dk], st.s[kb]);
+    }
+    if (i + kRing < 32) ring[i % kRing] = *ping_frag(kl, vt, i + kRing, li, h);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// Online softmax of S(t) into P(t): running max m (log2 units), sum l, O rescaled when m moves.
+template <bool MASKED, typename Mask>
+BB_DEV void ping_softmax(PingState& st, float c, int64_t q, const Mask& mask, int h) {
+  if constexpr (MASKED) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const uint32_t bits = mask.bits(q, kb, h);
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (!((bits >> r) & 1u)) st.s[kb][r] = -__builtin_huge_valf();
+    }
+  }
+  // NaN-propagating maximum (v_maximum3_f32): fmaxf would first canonicalise every MFMA result
+  float mx = __builtin_elementwise_maximum(st.s[0][0], st.s[1][0]);
+#pragma unroll
+  for (int r = 1; r < 16; ++r) mx = __builtin_elementwise_maximum(mx, __builtin_elementwise_maximum(st.s[0][r], st.s[1][r]));
+  mx = xhalf_max(mx);
+  const float mt = mx * c;
+  const bool need = mt > st.m + kRescaleThreshold;
+  if (__builtin_amdgcn_ballot_w64(need)) {
+    const float alpha = need ? fast_exp2(st.m - mt) : 1.0f;
+    if (need) st.m = mt;
+    st.l *= alpha;
+#pragma unroll
+    for (int dv = 0; dv < PD / 32; ++dv)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) st.o[dv][r] *= alpha;
+  }
+  const float nm = -st.m;
+  float sum = 0.0f;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      float pe[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        pe[e] = fast_exp2(fmaf(st.s[kb][8 * u + e], c, nm));
+        sum += pe[e];
+      }
+      st.pk[kb][u] = as_bf16x8(u32x4_t{pack_bf16x2(pe[0], pe[1]), pack_bf16x2(pe[2], pe[3]),
+                                       pack_bf16x2(pe[4], pe[5]), pack_bf16x2(pe[6], pe[7])});
+    }
+  st.l += sum;
+}
+
+__global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) {
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[PLDS];
+  __shared__ __attribute__((aligned(16))) int32_t route_keys[PHEADS][kTileKeys];
+  __shared__ int head_batches[PHEADS];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = lane >> 5, li = lane & 31;
+  const int hd = wave & 3, rbk = wave >> 2;  // head slot, row block (= ping-pong group)
+
+  // ---- work item: (KV head, 64-row tile), XCD-aware as in flash_kernel ----
+  const int lanes_total = p.n_kvbh * p.head_splits;
+  const int per_lane = p.row_tiles;
+  int lane_id, within;
+  const int bid = blockIdx.x;
+  if (p.remap) {
+    const int x = bid & 7, sidx = bid >> 3;
+    lane_id = x + 8 * (sidx / per_lane);
+    within = sidx % per_lane;
+  } else {
+    lane_id = bid % lanes_total;
+    within = bid / lanes_total;
+  }
+  const int rt = p.row_tiles - 1 - within;
+  const int kvbh = lane_id / p.head_splits, hsplit = lane_id % p.head_splits;
+  const int batch = kvbh / p.Hkv_pb;
+  const int bh = batch * p.H + (kvbh % p.Hkv_pb) * p.G + hsplit * PHEADS + hd;
+
+  const int64_t T_eff = p.row_end < p.T ? p.row_end : p.T;
+  const int64_t r0 = (int64_t)rt * PROWS;
+  const int64_t r1 = (r0 + PROWS < T_eff ? r0 + PROWS : T_eff) - 1;
+  const int64_t qlo = r0 + p.offset, qhi = r1 + p.offset;
+  const int64_t rw = r0 + 32 * rbk;            // first row of this wave
+  const bool wave_live = rw <= r1;
+  const int64_t qw0 = rw + p.offset, qw1 = (rw + 31 < r1 ? rw + 31 : r1) + p.offset;
+  const int64_t qme = qw0 + li;                // this lane's query position
+
+  PingState st;
+  {
+    const int64_t row = rw + li;
+    const bool live = row < T_eff;
+    const uint16_t* qrow = p.q + (int64_t)bh * p.sq0 + (live ? row : T_eff - 1) * p.sq1 + 8 * h;
+#pragma unroll
+    for (int dk = 0; dk < PD / 16; ++dk) {
+      const u32x4_t v = ld16(qrow + 16 * dk);
+      st.qf[dk] = as_bf16x8(live ? v : u32x4_t{0, 0, 0, 0});
+    }
+#pragma unroll
+    for (int dv = 0; dv < PD / 32; ++dv) st.o[dv] = f32x16_t{};
+    st.m = -1.0e20f;
+    st.l = 0.0f;
+  }
+
+  const uint16_t* kbase = p.k + (int64_t)kvbh * p.sk0;
+  const uint16_t* vbase = p.v + (int64_t)kvbh * p.sv0;
+  const uint16_t* vtbase = p.vt + (int64_t)kvbh * PD * p.np;
+
+  // ---- tiles (64-aligned): front range [0, f1) and window range [w0, w1) ----
+  const int64_t front_end = p.front < qhi + 1 ? p.front : qhi + 1;
+  int64_t wlo = qlo - p.window + 1;
+  if (wlo < 0) wlo = 0;
+  int64_t f1 = front_end > 0 ? (front_end + kTileKeys - 1) / kTileKeys : 0;
+  int64_t w0 = wlo / kTileKeys;
+  const int64_t w1 = qhi / kTileKeys + 1;
+  if (w0 <= f1) {  // the ranges touch: one range from 0
+    f1 = 0;
+    w0 = 0;
+  }
+  // Tiles every row of the workgroup attends in full: j with 64j+63 <= qlo and (64j+63 < front or
+  // 64j >= qhi - window + 1), i.e. [0, ua) from the front and [ub, uc) in the window. They run through the ping-pong
+  // loop with no element mask; the few edge tiles (window start, diagonal, a partial front tile) follow.
+  const int64_t a_lim = (p.front < qlo + 1 ? p.front : qlo + 1) / kTileKeys;
+  const int64_t ua = a_lim < (f1 > 0 ? f1 : w1) ? a_lim : (f1 > 0 ? f1 : w1);
+  int64_t ub = qhi - p.window + 1 <= 0 ? 0 : (qhi - p.window + 1 + kTileKeys - 1) / kTileKeys;
+  if (ub < w0) ub = w0;
+  if (ub < ua) ub = ua;
+  int64_t uc = (qlo + 1) / kTileKeys;
+  if (uc > w1) uc = w1;
+  if (uc < ub) uc = ub;
+  const int nu = (int)(ua + (uc - ub));
+  auto upos = [&](int t) -> int64_t { return (t < ua ? (int64_t)t : ub + (t - ua)) * kTileKeys; };
+
+  uint16_t* ring = smem;
+  auto kst = [&](int t) { return ring + (t & (PST - 1)) * 2 * PTE; };
+  auto vst = [&](int t) { return ring + (t & (PST - 1)) * 2 * PTE + PTE; };
+  TileLoader ld;
+  ld.init(kbase, p.sk1, p.N, vtbase, p.np, wave, lane);
+  const PipeWindowMask nomask{0, 0, 0, true};
+
+  if (nu > 0) {
+    ld.tile(kst(0), vst(0), upos(0));
+    if (nu > 1) ld.tile(kst(1), vst(1), upos(1));
+    vm_wait_tile(nu > 1);
+    ring_barrier();
+    if (rbk == 1) ring_barrier();  // waves 4..7 run one phase behind
+    // tile 0: QK only
+    if (nu > 2) ld.tile(kst(2), vst(2), upos(2));
+    ping_qk(st, kst(0), li, h);
+    vm_wait_tile(nu > 2);
+    ring_barrier();
+    ping_softmax<false>(st, p.c, qme, nomask, h);
+    ring_barrier();
+    for (int t = 1; t < nu; ++t) {
+      // MFMA phase: PV of tile t-1, QK of tile t; tile t+2 starts loading into the stage tile t-2 used
+      if (t + 2 < nu) ld.tile(kst(t + 2), vst(t + 2), upos(t + 2));
+      __builtin_amdgcn_s_setprio(1);
+      ping_mfma_phase(st, kst(t), vst(t - 1), li, h);
+      __builtin_amdgcn_s_setprio(0);
+      vm_wait_tile(t + 2 < nu);  // tile t+1 has landed
+      ring_barrier();
+      // VALU phase: softmax of tile t
+      ping_softmax<false>(st, p.c, qme, nomask, h);
+      ring_barrier();
+    }
+    ping_pv(st, vst(nu - 1), li, h);
+    if (rbk == 0) ring_barrier();  // realign the two groups
+  }
+
+  // ---- edge tiles (element masks), one at a time through ring stage 0 ----
+  {
+    const int64_t ranges[2][2] = {{0, f1}, {w0, w1}};
+#pragma unroll 1
+    for (int rg = 0; rg < 2; ++rg) {
+#pragma unroll 1
+      for (int64_t j = ranges[rg][0]; j < ranges[rg][1]; ++j) {
+        if (j < ua || (j >= ub && j < uc)) continue;  // done in the loop above
+        const int64_t k0 = j * kTileKeys;
+        __syncthreads();  // the stage is free
+        ld.tile(kst(0), vst(0), k0);
+        vm_wait_tile(false);
+        __syncthreads();
+        const int64_t k1 = k0 + kTileKeys - 1;
+        const bool live = wave_live && k0 <= qw1 && !(k0 >= p.front && k1 <= qw0 - p.window);
+        const PipeWindowMask wm{k0, p.front, p.window, live};
+        ping_qk(st, kst(0), li, h);
+        ping_softmax<true>(st, p.c, qme, wm, h);
+        ping_pv(st, vst(0), li, h);
+      }
+    }
+  }
+
+  // ---- routed keys: per-head gathered tiles; the two waves of a head share the gather ----
+  if (p.route_k > 0) {
+    __syncthreads();  // every wave is done with the ring
+    uint16_t* kl = smem + hd * 2 * PTE;
+    uint16_t* vt = kl + PTE;
+    int64_t g_first = qlo / p.route_chunk, g_last = qhi / p.route_chunk;
+    if (g_last >= p.n_groups) g_last = p.n_groups - 1;
+    for (int64_t g = g_first; g <= g_last; ++g) {
+      const int32_t* irow = p.idx + (int64_t)bh * p.si0 + g * p.si1;
+      // batches of 64 route slots holding at least one key some row of the workgroup can use
+      if (rbk == 0) {
+        int nbh = 0;
+        for (int s0 = 0; s0 < p.route_k; s0 += kTileKeys) {
+          const int sl = s0 + lane;
+          const int64_t key = sl < p.route_k ? irow[(int64_t)sl * p.si2] : -1;
+          const bool ok = key >= p.front && key < p.N && key <= qhi - p.window;
+          if (__builtin_amdgcn_ballot_w64(ok)) nbh = s0 / kTileKeys + 1;
+        }
+        if (lane == 0) head_batches[hd] = nbh;
+      }
+      __syncthreads();
+      int nb = 0;
+      const int my_nb = head_batches[hd];
+#pragma unroll
+      for (int x = 0; x < PHEADS; ++x) nb = nb > head_batches[x] ? nb : head_batches[x];
+      for (int bi = 0; bi < nb; ++bi) {
+        const bool work = bi < my_nb;
+        if (work && rbk == 0) {
+          const int sl = bi * kTileKeys + lane;
+          const int64_t key = sl < p.route_k ? irow[(int64_t)sl * p.si2] : -1;
+          const bool ok = key >= p.front && key < p.N && key <= qhi - p.window;
+          route_keys[hd][lane] = ok ? (int32_t)key : -1;
+        }
+        __syncthreads();
+        if (work) {
+          // K rows by direct loads (the head's two waves split the 16 blocks)
+          for (int b = rbk; b < PBLK; b += 2) {
+            const int e = b * 512 + 8 * lane;
+            const int row = e / PD, sl2 = (e % PD) / 8;
+            const int chk = sl2 ^ (row & (PD / 8 - 1));
+            const int32_t kr = route_keys[hd][row];
+            lds_dma16(kbase + (int64_t)(kr >= 0 ? kr : 0) * p.sk1 + 8 * chk, kl + b * 512);
+          }
+          // V rows -> V^T through registers: units of 4 keys x 8 d
+          for (int u = lane + 64 * rbk; u < (kTileKeys / 4) * (PD / 8); u += 128) {
+            const int bq = u % (PD / 8), a4 = u / (PD / 8);
+            u32x4_t vr[4];
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2) {
+              const int32_t kr = route_keys[hd][4 * a4 + s2];
+              vr[s2] = kr >= 0 ? ld16(vbase + (int64_t)kr * p.sv1 + 8 * bq) : u32x4_t{0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const int w = e >> 1;
+              const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+              const uint32_t lo = __builtin_amdgcn_perm(vr[1][w], vr[0][w], sel);
+              const uint32_t hi = __builtin_amdgcn_perm(vr[3][w], vr[2][w], sel);
+              const int d = 8 * bq + e;
+              *reinterpret_cast<u32x2_t*>(vt + vt_off(d, 2 * (a4 >> 2) + (a4 & 1)) + 4 * ((a4 >> 1) & 1)) =
+                  u32x2_t{lo, hi};
+            }
+          }
+        }
+        vm_wait_tile(false);
+        __syncthreads();
+        if (work && wave_live) {
+          const PipeRoutedMask rm{route_keys[hd], p.window, p.route_chunk, g};
+          ping_qk(st, kl, li, h);
+          ping_softmax<true>(st, p.c, qme, rm, h);
+          ping_pv(st, vt, li, h);
+        }
+        __syncthreads();
+      }
+    }
+  }
+
+  // ---- epilogue ----
+  if (!wave_live) return;
+  const int64_t row = rw + li;
+  const float lt = xhalf_sum(st.l);
+  if (row >= T_eff) return;
+  const float inv = 1.0f / fmaxf(lt, 1.0e-20f);
+  uint16_t* orow = p.out + (int64_t)bh * p.so0 + row * p.so1;
+#pragma unroll
+  for (int dv = 0; dv < PD / 32; ++dv)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int d0 = 32 * dv + 8 * g4 + 4 * h;
+      const u32x2_t w = {pack_bf16x2(st.o[dv][4 * g4] * inv, st.o[dv][4 * g4 + 1] * inv),
+                         pack_bf16x2(st.o[dv][4 * g4 + 2] * inv, st.o[dv][4 * g4 + 3] * inv)};
+      *reinterpret_cast<u32x2_t*>(orow + d0) = w;
+    }
+}
+
+}  // namespace
+
+bool flash_pipe_supported(const FlashParams& p, int D) {
+  // buffer offsets are 32-bit: one KV head's K rows and V^T must each span < 2 GiB
+  const bool fits = p.N * p.sk1 * 2 < ((int64_t)1 << 31) && (int64_t)PD * p.np * 2 < ((int64_t)1 << 31);
+  return D == PD && p.G % PHEADS == 0 && p.key_mask == nullptr && fits;
+}
+
+hipError_t launch_flash_pipe(const FlashParams& p, hipStream_t stream) {
+  const int64_t items = (int64_t)p.n_kvbh * p.head_splits * p.row_tiles;
+  if (items <= 0) return hipSuccess;
+  if (items > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(flash_ping_kernel, dim3((unsigned)items), dim3(64 * PNW), 0, stream, p);
+  return hipGetLastError();
+}
+
+}  // namespace bb

@@ -25,6 +25,9 @@ struct FlashParams {
 
 hipError_t launch_flash(const FlashParams& p, int D, int hpw, bool split, hipStream_t stream);
 hipError_t launch_flash_merge(const FlashParams& p, int D, hipStream_t stream);
+// Software-pipelined main-pass kernel (head_dim 128, kv_groups % 4 == 0, no token mask, 64-aligned route groups).
+bool flash_pipe_supported(const FlashParams& p, int D);
+hipError_t launch_flash_pipe(const FlashParams& p, hipStream_t stream);
 hipError_t launch_transpose_v(const uint16_t* v, int64_t sv0, int64_t sv1, int n_kvbh, int64_t N, int64_t np, int D,
                               uint16_t* vt, hipStream_t stream);
 
