@@ -82,6 +82,17 @@ def staged_prefill(attn, q, k, v, ev):
     return out[None], idx
 
 
+def main_traffic():
+    """HBM bytes per launch of the main kernel from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+    (profiles/prefill_128k_hbm_traffic.json, scaled by a calibrating 1 GiB copy); None when absent."""
+    path = ROOT / "profiles" / "prefill_128k_hbm_traffic.json"
+    try:
+        data = json.loads(path.read_text())
+        return int(data["kernels"]["flash_ping_kernel"]["bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def cpu_baseline(q, k, v, routes, cfg, args):
     """The reference's CPU path (routes() op sequence + bigger_bird_flash_ref masked-dense semantics), restated in
     torch CPU ops by the oracle, timed on a bounded sample and scaled to one layer:
@@ -215,9 +226,10 @@ def main():
         "stage_tflops": {"main": round(main_tflops, 1), "tail": round(tail_tflops, 1)},
         "wall_s_timed": round(wall, 3),
         "h100_reference_ms": H100_REFERENCE_MS,
-        "roofline": {"bound": "mfma", "kernel": "flash_kernel (main sink+window+routed pass)",
+        "roofline": {"bound": "mfma", "kernel": "flash_ping_kernel (main sink+window+routed pass)",
                      "achieved": round(main_tflops, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(main_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "frac": round(main_tflops / PEAK_BF16_TFLOPS, 4), "traffic": main_traffic(),
+                     "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE/WRITE_SIZE, copy-calibrated)",
                      "flop_per_launch": flops_main, "avg_launch_ms": round(stage_avg["main"], 4)},
         "cpu_baseline": None,
     }
