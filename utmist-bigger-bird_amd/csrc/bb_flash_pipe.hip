@@ -9,8 +9,10 @@
 //     barriers. Waves 4..7 start one barrier late, so on every SIMD one wave is in its MFMA phase while the other is
 //     in its VALU phase: the matrix cores and the VALUs work at the same time instead of in turn;
 //   * K and V^T tiles stream global->LDS with 16-byte buffer loads straight into LDS (no staging registers) through a
-//     four-stage ring, issued two tiles ahead; rows past N read as zeros through the buffer resource bounds;
-//   * the exponent offset is refreshed only when a tile max exceeds it by more than 2^8 (O rescales stay rare);
+//     four-stage ring, issued two tiles ahead at the end of a VALU phase; rows past N read as zeros through the buffer
+//     resource bounds;
+//   * the exponent offset moves only when a probability would exceed 2^8 (O rescales stay rare); tiles without masked
+//     elements skip the per-tile maximum unless the row sum says the offset must move;
 //   * routed keys differ per head: after the window loop the two waves of a head gather its routed K rows and V rows
 //     into that head's LDS tile.
 #include "bb_common.h"
@@ -127,10 +129,13 @@ BB_DEV void vm_wait_tile(bool one_tile_in_flight) {
 
 // Workgroup barrier without a memory fence: the tile ring publishes its direct loads with explicit vmcnt waits,
 // so the barrier must not drain the loads still in flight for the tile after next (a __syncthreads fence would).
-// The wavefront-scope fences emit nothing but keep the compiler from moving memory accesses across it.
+// The wavefront-scope fences emit nothing but keep the compiler from moving memory accesses across it; the
+// scheduling barriers keep register arithmetic on its side too (the phases must not leak into each other).
 BB_DEV void ring_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
 }
 
@@ -205,34 +210,8 @@ BB_DEV void ping_mfma_phase(PingState& st, const uint16_t* kl, const uint16_t* v
   }
 }
 
-// Online softmax of S(t) into P(t): running max m (log2 units), sum l, O rescaled when m moves.
-template <bool MASKED, typename Mask>
-BB_DEV void ping_softmax(PingState& st, float c, int64_t q, const Mask& mask, int h) {
-  if constexpr (MASKED) {
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const uint32_t bits = mask.bits(q, kb, h);
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        if (!((bits >> r) & 1u)) st.s[kb][r] = -__builtin_huge_valf();
-    }
-  }
-  // NaN-propagating maximum (v_maximum3_f32): fmaxf would first canonicalise every MFMA result
-  float mx = __builtin_elementwise_maximum(st.s[0][0], st.s[1][0]);
-#pragma unroll
-  for (int r = 1; r < 16; ++r) mx = __builtin_elementwise_maximum(mx, __builtin_elementwise_maximum(st.s[0][r], st.s[1][r]));
-  mx = xhalf_max(mx);
-  const float mt = mx * c;
-  const bool need = mt > st.m + kRescaleThreshold;
-  if (__builtin_amdgcn_ballot_w64(need)) {
-    const float alpha = need ? fast_exp2(st.m - mt) : 1.0f;
-    if (need) st.m = mt;
-    st.l *= alpha;
-#pragma unroll
-    for (int dv = 0; dv < PD / 32; ++dv)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) st.o[dv][r] *= alpha;
-  }
+// P(t) = 2^(S(t) c - m) as bf16 MFMA fragments; returns this lane's sum of the fp32 values.
+BB_DEV float ping_exp(PingState& st, float c) {
   const float nm = -st.m;
   float sum = 0.0f;
 #pragma unroll
@@ -248,6 +227,62 @@ BB_DEV void ping_softmax(PingState& st, float c, int64_t q, const Mask& mask, in
       st.pk[kb][u] = as_bf16x8(u32x4_t{pack_bf16x2(pe[0], pe[1]), pack_bf16x2(pe[2], pe[3]),
                                        pack_bf16x2(pe[4], pe[5]), pack_bf16x2(pe[6], pe[7])});
     }
+  return sum;
+}
+
+// Tile maximum of S(t) over the 64 keys of this lane's query, times c.
+BB_DEV float ping_tile_max(const PingState& st, float c) {
+  // NaN-propagating maximum (v_maximum3_f32): fmaxf would first canonicalise every MFMA result
+  float mx = __builtin_elementwise_maximum(st.s[0][0], st.s[1][0]);
+#pragma unroll
+  for (int r = 1; r < 16; ++r) mx = __builtin_elementwise_maximum(mx, __builtin_elementwise_maximum(st.s[0][r], st.s[1][r]));
+  return xhalf_max(mx) * c;
+}
+
+// Moves the exponent offset of the lanes with `need` to mt, rescaling O and l.
+BB_DEV void ping_rescale(PingState& st, bool need, float mt) {
+  const float alpha = need ? fast_exp2(st.m - mt) : 1.0f;
+  if (need) st.m = mt;
+  st.l *= alpha;
+#pragma unroll
+  for (int dv = 0; dv < PD / 32; ++dv)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) st.o[dv][r] *= alpha;
+}
+
+// Online softmax of a masked tile S(t) into P(t): running offset m (log2 units), sum l, O rescaled when the tile
+// maximum exceeds m by more than kRescaleThreshold.
+template <typename Mask>
+BB_DEV void ping_softmax_masked(PingState& st, float c, int64_t q, const Mask& mask, int h) {
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    const uint32_t bits = mask.bits(q, kb, h);
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      if (!((bits >> r) & 1u)) st.s[kb][r] = -__builtin_huge_valf();
+  }
+  const float mt = ping_tile_max(st, c);
+  const bool need = mt > st.m + kRescaleThreshold;
+  if (__builtin_amdgcn_ballot_w64(need)) ping_rescale(st, need, mt);
+  st.l += ping_exp(st, c);
+}
+
+// Online softmax of a tile with no masked element. The tile is exponentiated against the current offset first;
+// only when a probability may exceed 2^kRescaleThreshold (this lane's or the partner lane's sum does: every term is
+// at most the sum; an infinite or NaN sum counts too) is the tile maximum taken, the offset moved and the tile
+// exponentiated again. Same bound on P as the masked form, without a maximum per tile in the common case.
+BB_DEV void ping_softmax_open(PingState& st, float c) {
+  float sum = ping_exp(st, c);
+  const float lim = __builtin_amdgcn_exp2f(kRescaleThreshold);
+  const bool over = !(sum <= lim);
+  const auto sw = __builtin_amdgcn_permlane32_swap((uint32_t)over, (uint32_t)over, false, false);
+  const bool need = (sw[0] | sw[1]) != 0u;
+  if (__builtin_amdgcn_ballot_w64(need)) {
+    const float mt = ping_tile_max(st, c);
+    // the new offset never goes below the old one, so rows that do not need it keep theirs
+    ping_rescale(st, need, __builtin_elementwise_maximum(mt, st.m));
+    sum = ping_exp(st, c);
+  }
   st.l += sum;
 }
 
@@ -338,7 +373,6 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
   auto vst = [&](int t) { return ring + (t & (PST - 1)) * 2 * PTE + PTE; };
   TileLoader ld;
   ld.init(kbase, p.sk1, p.N, vtbase, p.np, wave, lane);
-  const PipeWindowMask nomask{0, 0, 0, true};
 
   if (nu > 0) {
     ld.tile(kst(0), vst(0), upos(0));
@@ -351,18 +385,20 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
     ping_qk(st, kst(0), li, h);
     vm_wait_tile(nu > 2);
     ring_barrier();
-    ping_softmax<false>(st, p.c, qme, nomask, h);
+    ping_softmax_open(st, p.c);
     ring_barrier();
     for (int t = 1; t < nu; ++t) {
-      // MFMA phase: PV of tile t-1, QK of tile t; tile t+2 starts loading into the stage tile t-2 used
-      if (t + 2 < nu) ld.tile(kst(t + 2), vst(t + 2), upos(t + 2));
+      // MFMA phase: PV of tile t-1, QK of tile t
       __builtin_amdgcn_s_setprio(1);
       ping_mfma_phase(st, kst(t), vst(t - 1), li, h);
       __builtin_amdgcn_s_setprio(0);
-      vm_wait_tile(t + 2 < nu);  // tile t+1 has landed
+      vm_wait_tile(false);  // tile t+1 has landed
       ring_barrier();
-      // VALU phase: softmax of tile t
-      ping_softmax<false>(st, p.c, qme, nomask, h);
+      // VALU phase: softmax of tile t, then tile t+2 starts loading into the stage tile t-2 used (every wave is past
+      // the MFMA phase that last read it). The loads come after the exponentials: issuing a direct load stalls the
+      // wave for as long as the CU's address unit is busy with the other waves' loads.
+      ping_softmax_open(st, p.c);
+      if (t + 2 < nu) ld.tile(kst(t + 2), vst(t + 2), upos(t + 2));
       ring_barrier();
     }
     ping_pv(st, vst(nu - 1), li, h);
@@ -386,7 +422,7 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
         const bool live = wave_live && k0 <= qw1 && !(k0 >= p.front && k1 <= qw0 - p.window);
         const PipeWindowMask wm{k0, p.front, p.window, live};
         ping_qk(st, kst(0), li, h);
-        ping_softmax<true>(st, p.c, qme, wm, h);
+        ping_softmax_masked(st, p.c, qme, wm, h);
         ping_pv(st, vst(0), li, h);
       }
     }
@@ -461,7 +497,7 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
         if (work && wave_live) {
           const PipeRoutedMask rm{route_keys[hd], p.window, p.route_chunk, g};
           ping_qk(st, kl, li, h);
-          ping_softmax<true>(st, p.c, qme, rm, h);
+          ping_softmax_masked(st, p.c, qme, rm, h);
           ping_pv(st, vt, li, h);
         }
         __syncthreads();
