@@ -14,6 +14,8 @@ Printed JSON (one line): value = ms per layer (lower is better); effective TFLOP
 4*d FLOP per pair counted from the actual routes; `roofline` for the dominant kernel (the main sparse kernel) from
 HIP events around its launches on the stream it runs on; `cpu_baseline` = the CPU restatement of the reference's
 PyTorch path (oracle.routes_reference_order + oracle.flash_ref) timed on a bounded sample and scaled to a layer.
+Also reported, next to the headline: `tail_roofline` (the exact 256-row tail, TFLOP/s and HBM GB/s) and `decode`
+(INT8-KV decode: microseconds per step and HBM GB/s against 8 TB/s).
 """
 import argparse
 import json
@@ -29,6 +31,7 @@ for _p in (str(ROOT), str(ROOT / "utmist-bigger-bird_amd")):
 
 METRIC = "ms/layer sparse prefill @128K; effective TFLOP/s and % of bf16 MFMA peak"
 PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+PEAK_HBM_GBPS = 8000.0         # MI355X HBM3E
 H100_REFERENCE_MS = 124.6      # the reference's published sparse ms/layer at 131072 tokens (H100)
 
 
@@ -40,6 +43,7 @@ def parse_args():
     ap.add_argument("--T", type=int, default=131072)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true", help="skip the INT8 decode leg (BASELINE configs[4])")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 1 GiB device copy 5 times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--cpu-sample-blocks", type=int, default=96,
@@ -129,6 +133,52 @@ def cpu_baseline(q, k, v, routes, cfg, args):
                        f"{(t_routes / Hkv + t_blocks):.1f} s")}
 
 
+def decode_leg(dev, seed):
+    """exact decode over an INT8 cache of 131072 tokens (32 q / 8 KV heads, d=128, per-token
+    per-head fp32 scales = absmax/127), 256 steps; each step quantises one new token into the cache and attends to
+    all n + 1 rows with a fresh bf16 query. Reported per step with the cache bytes a step must read."""
+    import torch
+    from bigger_bird_amd import decode_int8, quantize
+
+    n0, steps, H, Hkv, d = 131072, 256, 32, 8, 128
+    g = torch.Generator(device=dev).manual_seed(seed + 5)
+    k = torch.randn(n0 + steps, Hkv, d, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(n0 + steps, Hkv, d, device=dev, generator=g).to(torch.bfloat16)
+    qs = torch.randn(steps, H, d, device=dev, generator=g).to(torch.bfloat16)
+    k8 = torch.empty(n0 + steps, Hkv, d, dtype=torch.int8, device=dev)
+    v8 = torch.empty_like(k8)
+    ks = torch.empty(n0 + steps, Hkv, 1, dtype=torch.float32, device=dev)
+    vs = torch.empty_like(ks)
+    quantize(k[:n0], out=(k8[:n0], ks[:n0]), scale_dtype=torch.float32)
+    quantize(v[:n0], out=(v8[:n0], vs[:n0]), scale_dtype=torch.float32)
+    scale = d ** -0.5
+
+    def step(i):
+        quantize(k[n0 + i:n0 + i + 1], out=(k8[n0 + i:n0 + i + 1], ks[n0 + i:n0 + i + 1]), scale_dtype=torch.float32)
+        quantize(v[n0 + i:n0 + i + 1], out=(v8[n0 + i:n0 + i + 1], vs[n0 + i:n0 + i + 1]), scale_dtype=torch.float32)
+        return decode_int8(qs[i], k8, ks, v8, vs, n0 + i + 1, scale)
+
+    with torch.inference_mode():
+        for i in range(8):  # warm-up (rewrites the same rows)
+            step(i)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(steps):
+            step(i)
+        b.record()
+        torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1e3 / steps
+    n_mean = n0 + (steps + 1) / 2
+    bytes_step = 2 * Hkv * n_mean * (d + 4) + 2 * H * d * 2  # int8 K and V rows + fp32 scales, q in + out
+    gbps = bytes_step / (us * 1e-6) / 1e9
+    return {"workload": "BASELINE configs[4]: INT8-KV exact decode, 131072 cached tokens (+1 per step), 32q/8kv heads, "
+                        "d=128, fp32 per-token per-head scales, 256 steps",
+            "us_per_step": round(us, 2), "bytes_per_step": int(bytes_step), "achieved_gbps": round(gbps, 1),
+            "peak_gbps": PEAK_HBM_GBPS, "frac": round(gbps / PEAK_HBM_GBPS, 4),
+            "kernels": "quantize x2 + decode_mfma_kernel + decode_merge_kernel per step"}
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -202,6 +252,8 @@ def main():
     tflops = flops_total / (ms_per_step * 1e-3) / 1e12
     main_tflops = flops_main / (stage_avg["main"] * 1e-3) / 1e12
     tail_tflops = flops_tail / (stage_avg["tail"] * 1e-3) / 1e12
+    # the tail reads every K and V row of the layer once per KV head (plus its 256 query rows in and out)
+    tail_bytes = 2 * Hkv * T * d * 2 + 2 * H * r * d * 2
     result = {
         "metric": METRIC,
         "value": round(ms_per_step, 3),
@@ -231,6 +283,12 @@ def main():
                      "frac": round(main_tflops / PEAK_BF16_TFLOPS, 4), "traffic": main_traffic(),
                      "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE/WRITE_SIZE, copy-calibrated)",
                      "flop_per_launch": flops_main, "avg_launch_ms": round(stage_avg["main"], 4)},
+        "tail_roofline": {"bound": "mfma", "achieved": round(tail_tflops, 1), "peak": PEAK_BF16_TFLOPS,
+                          "unit": "TFLOP/s", "frac": round(tail_tflops / PEAK_BF16_TFLOPS, 4),
+                          "hbm_gbps": round(tail_bytes / (stage_avg["tail"] * 1e-3) / 1e9, 1),
+                          "hbm_frac": round(tail_bytes / (stage_avg["tail"] * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+                          "bytes": tail_bytes},
+        "decode": None if args.no_decode else decode_leg(dev, args.seed),
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:

@@ -288,12 +288,14 @@ int bb_int8_dequantize(const int8_t* q, const void* scale, int scale_is_f16, int
                     "bb_int8_dequantize");
 }
 
-static int decode_splits(int64_t n, int Hkv) {
-  int64_t want = cdiv(4 * kCUs, Hkv);
-  int64_t by_len = cdiv(n, 256);
-  int64_t s = want < by_len ? want : by_len;
-  return (int)(s < 1 ? 1 : s);
+// Keys per decode workgroup: about four workgroups per CU, at least 256 keys, a multiple of 128 (four 32-key wave
+// chunks of the MFMA decode).
+static int64_t decode_split_len(int64_t n, int Hkv) {
+  int64_t len = cdiv(n, cdiv(4 * kCUs, Hkv));
+  if (len < 256) len = 256;
+  return cdiv(len, 128) * 128;
 }
+static int decode_splits(int64_t n, int Hkv) { return (int)cdiv(n, decode_split_len(n, Hkv)); }
 
 size_t bb_decode_workspace(int64_t n, int H, int Hkv, int D) {
   if (n <= 0 || Hkv <= 0) return 0;
@@ -327,9 +329,8 @@ int bb_decode(const void* q, int64_t sq, const int8_t* k8, const void* ks, const
   if (skb) { p.skb0 = skb[0]; p.skb1 = skb[1]; }
   if (svb) { p.svb0 = svb[0]; p.svb1 = svb[1]; }
   p.n = n; p.H = H; p.Hkv = Hkv; p.D = D; p.scale_is_f16 = scale_is_f16;
+  p.split_len = decode_split_len(n, Hkv);
   p.n_splits = decode_splits(n, Hkv);
-  p.split_len = cdiv(n, p.n_splits);
-  p.n_splits = (int)cdiv(n, p.split_len);
   p.c = (float)((double)scale * 1.4426950408889634);
   p.out = static_cast<uint16_t*>(out);
   p.so = so;

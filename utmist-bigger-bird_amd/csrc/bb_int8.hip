@@ -224,30 +224,267 @@ __global__ __launch_bounds__(kDecThreads) void decode_kernel(DecodeParams p) {
   }
 }
 
-template <int D>
-__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
-  const int h = blockIdx.x;
-  for (int d = threadIdx.x; d < D; d += 256) {
-    const float* base = p.part + (int64_t)h * p.n_splits * (D + 2);
-    float M = -1.0e30f;
-    for (int s = 0; s < p.n_splits; ++s) M = fmaxf(M, base[s * (D + 2) + D]);
-    float L = 0.0f, O = 0.0f;
-    for (int s = 0; s < p.n_splits; ++s) {
-      const float w = fast_exp2(base[s * (D + 2) + D] - M);
-      L += w * base[s * (D + 2) + D + 1];
-      O += w * base[s * (D + 2) + d];
+// ---------------------------------------------------------------------------------------------------------------
+// MFMA decode for the production shape (head_dim 128, four query heads per KV head, int8 cache). Workgroup (split,
+// KV head): 4 waves, wave w taking 32-key chunks w, w + 4, ... of the split's key range. Per chunk a wave
+//   * loads the chunk's 32 K rows and 32 V rows as int8, each lane one contiguous 64-byte half row of each (16-byte
+//     loads through buffer resources that read rows past n as zeros);
+//   * computes S = Q K^T on one 32x32x16 bf16 MFMA column block (rows 0..3 of Q are the four heads, rows 4..31 are
+//     zero; int8 values are exact in bf16). The contraction runs over d in the order 64 hh + 8 dk + e on both
+//     operands, so a lane's K operand is its own half row;
+//   * runs the online softmax on lanes 0..31 (one key each) for the four heads, with the exponent offset moved only
+//     when a probability would exceed 2^8, and stores P (times the V row scale) to LDS as bf16 [head][key];
+//   * stores the V rows to LDS (144-byte pitch, so the transposed reads below hit distinct banks) and reads them back
+//     with ds_read_b64_tr_b8, which hands each lane 8 keys of one d: the V^T operand;
+//   * accumulates O^T += V^T P^T on 8 MFMAs (4 blocks of 32 d x 2 steps of 16 keys).
+// The four waves' states merge through LDS into one partial (m, l, o) per head and split for decode_merge_kernel.
+constexpr int kMdWaves = 4;
+constexpr int kMdChunk = 32;    // keys per wave step
+constexpr int kMdVPitch = 144;  // LDS bytes per V row
+struct MdLds {
+  uint8_t v[kMdWaves][kMdChunk * kMdVPitch];
+  uint16_t pt[kMdWaves][4 * kMdChunk + 8];  // P^T bf16 [head][key], then one zero 16-byte block
+  float m[kMdWaves][4];
+  float l[kMdWaves][4];
+  float o[kMdWaves][4][128];
+};
+typedef int v2i_t __attribute__((ext_vector_type(2)));
+
+BB_DEV u32x2_t i8x4_to_bf16x4(uint32_t w) {
+  return u32x2_t{pack_bf16x2((float)(int8_t)(w & 0xffu), (float)(int8_t)((w >> 8) & 0xffu)),
+                 pack_bf16x2((float)(int8_t)((w >> 16) & 0xffu), (float)(int8_t)(w >> 24))};
+}
+BB_DEV bf16x8_t i8x8_to_bf16x8(uint32_t w0, uint32_t w1) {
+  const u32x2_t a = i8x4_to_bf16x4(w0), b = i8x4_to_bf16x4(w1);
+  return as_bf16x8(u32x4_t{a[0], a[1], b[0], b[1]});
+}
+BB_DEV float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  return v;
+}
+BB_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+template <bool F16S>
+__global__ __launch_bounds__(64 * kMdWaves, 2) void decode_mfma_kernel(DecodeParams p) {
+  __shared__ __attribute__((aligned(16))) MdLds sm;
+  constexpr int D = 128;
+  const int split = blockIdx.x, g = blockIdx.y;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int li = lane & 31, hh = lane >> 5;
+  const int64_t j_begin = (int64_t)split * p.split_len;
+  const int64_t j_end = j_begin + p.split_len < p.n ? j_begin + p.split_len : p.n;
+
+  bf16x8_t qa[8];  // Q rows 0..3 = query heads 4g..4g+3; fragment dk holds d = 64 hh + 8 dk + 0..7
+#pragma unroll
+  for (int dk = 0; dk < 8; ++dk)
+    qa[dk] = as_bf16x8(li < 4 ? ld16(p.q + (int64_t)(4 * g + li) * p.sq + 64 * hh + 8 * dk) : u32x4_t{0, 0, 0, 0});
+
+  // one buffer resource per cache over KV head g's rows 0..n-1 (row j at byte j * row_bytes): rows >= n read as 0
+  const int64_t row_bytes = (int64_t)p.Hkv * D;
+  const int range = (int)((p.n - 1) * row_bytes + D);
+  const __amdgpu_buffer_rsrc_t krs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(p.k8 + (int64_t)g * D), 0, range, 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(p.v8 + (int64_t)g * D), 0, range, 0x00020000);
+
+  float m[4], l[4];
+#pragma unroll
+  for (int h = 0; h < 4; ++h) { m[h] = -1.0e20f; l[h] = 0.0f; }
+  f32x16_t o[4];
+#pragma unroll
+  for (int dv = 0; dv < 4; ++dv) o[dv] = f32x16_t{};
+  uint8_t* vl = sm.v[wave];
+  uint16_t* pl = sm.pt[wave];
+  if (lane < 8) pl[4 * kMdChunk + lane] = 0;  // the zero block read by the lanes of query columns 4..31
+
+  // chunk c's rows and scales; the loop fetches chunk c + 4 while it computes on chunk c
+  struct Rows {
+    u32x4_t k[4], v[4];
+    float ks, vs;
+  };
+  auto fetch = [&](int64_t c, Rows& r) {
+    const int64_t key = j_begin + c * kMdChunk + li;
+    const uint32_t off = (uint32_t)(key * row_bytes) + 64u * (uint32_t)hh;  // 32-bit: decode_mfma_fits
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) {
+      r.k[c4] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(krs, off + 16u * c4, 0, 0));
+      r.v[c4] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(vrs, off + 16u * c4, 0, 0));
     }
-    p.out[(int64_t)h * p.so + d] = f32_to_bf16(O / fmaxf(L, 1.0e-20f));
+    const int64_t si = (key < p.n ? key : p.n - 1) * p.Hkv + g;
+    if constexpr (F16S) {
+      r.ks = __half2float(reinterpret_cast<const __half*>(p.ks)[si]);
+      r.vs = __half2float(reinterpret_cast<const __half*>(p.vs)[si]);
+    } else {
+      r.ks = reinterpret_cast<const float*>(p.ks)[si];
+      r.vs = reinterpret_cast<const float*>(p.vs)[si];
+    }
+  };
+  const int64_t nchunks = (j_end - j_begin + kMdChunk - 1) / kMdChunk;
+  Rows cur;
+  if (wave < nchunks) fetch(wave, cur);
+  for (int64_t c = wave; c < nchunks; c += kMdWaves) {
+    // unconditional, so the wait counts stay exact: past the last chunk this re-reads the current one (cache hits)
+    Rows nxt;
+    fetch(c + kMdWaves < nchunks ? c + kMdWaves : c, nxt);
+    const int64_t key = j_begin + c * kMdChunk + li;
+    const bool valid = hh == 0 && key < j_end;
+    const u32x4_t* kr = cur.k;
+    const u32x4_t* vr = cur.v;
+    const float ksc = cur.ks, vsc = cur.vs;
+    // S = Q K^T: lane (key li, hh = 0) gets the four heads' scores in elements 0..3
+    f32x16_t sacc = f32x16_t{};
+#pragma unroll
+    for (int dk = 0; dk < 8; ++dk)
+      sacc = mfma32(qa[dk], i8x8_to_bf16x8(kr[dk >> 1][2 * (dk & 1)], kr[dk >> 1][2 * (dk & 1) + 1]), sacc);
+    float x[4], pr[4];
+    bool over = false;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      x[h] = valid ? sacc[h] * ksc * p.c : -__builtin_huge_valf();
+      pr[h] = fast_exp2(x[h] - m[h]);
+      over |= !(pr[h] <= 256.0f);
+    }
+    if (__builtin_amdgcn_ballot_w64(over)) {
+      float alpha_lane = 1.0f;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const float mn = fmaxf(m[h], wave_max(x[h]));
+        const float alpha = fast_exp2(m[h] - mn);
+        m[h] = mn;
+        l[h] *= alpha;
+        if (li == h) alpha_lane = alpha;
+        pr[h] = fast_exp2(x[h] - m[h]);
+      }
+#pragma unroll
+      for (int dv = 0; dv < 4; ++dv)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dv][r] *= alpha_lane;
+    }
+    // P^T (times the V row scale) and the V rows to LDS
+    if (hh == 0) {
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        l[h] += pr[h];
+        pl[h * kMdChunk + li] = f32_to_bf16(pr[h] * vsc);
+      }
+    }
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) *reinterpret_cast<u32x4_t*>(vl + li * kMdVPitch + 64 * hh + 16 * c4) = vr[c4];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // O^T += V^T P^T
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const bf16x8_t pb = as_bf16x8(ld16(li < 4 ? pl + li * kMdChunk + 16 * ks + 8 * hh : pl + 4 * kMdChunk));
+      const int s16 = lane & 15;
+      const int src_key = 16 * ks + 8 * hh + (s16 >> 1);
+#pragma unroll
+      for (int dv = 0; dv < 4; ++dv) {
+        const int src_d = 32 * dv + 16 * ((lane >> 4) & 1) + 8 * (s16 & 1);
+        const v2i_t t = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            reinterpret_cast<__attribute__((address_space(3))) v2i_t*>(
+                reinterpret_cast<uintptr_t>(vl + src_key * kMdVPitch + src_d)));
+        o[dv] = mfma32(i8x8_to_bf16x8((uint32_t)t.x, (uint32_t)t.y), pb, o[dv]);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    cur = nxt;
+  }
+
+  // merge the four waves: m is wave-uniform, l is spread over the key lanes, O^T column h sits in lanes h and h + 32
+#pragma unroll
+  for (int h = 0; h < 4; ++h) l[h] = wave_sum(l[h]);
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < 4; ++h) { sm.m[wave][h] = m[h]; sm.l[wave][h] = l[h]; }
+  }
+  if (li < 4) {
+#pragma unroll
+    for (int dv = 0; dv < 4; ++dv)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sm.o[wave][li][32 * dv + 8 * (r >> 2) + 4 * hh + (r & 3)] = o[dv][r];
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < 4 * D; t += 64 * kMdWaves) {
+    const int h = t / D, d = t % D;
+    float M = sm.m[0][h];
+#pragma unroll
+    for (int w = 1; w < kMdWaves; ++w) M = fmaxf(M, sm.m[w][h]);
+    float L = 0.0f, O = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kMdWaves; ++w) {
+      const float wt = fast_exp2(sm.m[w][h] - M);
+      L += wt * sm.l[w][h];
+      O += wt * sm.o[w][h][d];
+    }
+    float* dst = p.part + ((int64_t)(4 * g + h) * p.n_splits + split) * (D + 2);
+    dst[d] = O;
+    if (d == 0) { dst[D] = M; dst[D + 1] = L; }
+  }
+}
+
+// the MFMA decode addresses KV head g's rows with 32-bit buffer offsets, including the rows of a last partial chunk
+bool decode_mfma_fits(const DecodeParams& p) {
+  return (p.n + kMdChunk) * (int64_t)p.Hkv * 128 < ((int64_t)1 << 31);
+}
+
+// Split merge: one workgroup per query head; thread (d, split group) folds every (1024 / D)-th split of column d
+// (all loads independent, so they overlap), then the groups combine through LDS.
+constexpr int kMergeThreads = 1024;
+template <int D>
+__global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(DecodeParams p) {
+  constexpr int NG = kMergeThreads / D;
+  __shared__ float red_m[kMergeThreads], red_l[NG], red_o[NG][D];
+  const int h = blockIdx.x, t = threadIdx.x, d = t % D, grp = t / D;
+  const float* base = p.part + (int64_t)h * p.n_splits * (D + 2);
+  float M = -1.0e30f;
+  for (int s = t; s < p.n_splits; s += kMergeThreads) M = fmaxf(M, base[(int64_t)s * (D + 2) + D]);
+  red_m[t] = M;
+  __syncthreads();
+  for (int w = kMergeThreads / 2; w > 0; w >>= 1) {
+    if (t < w) red_m[t] = fmaxf(red_m[t], red_m[t + w]);
+    __syncthreads();
+  }
+  M = red_m[0];
+  float L = 0.0f, O = 0.0f;
+#pragma unroll 4
+  for (int s = grp; s < p.n_splits; s += NG) {
+    const float* r = base + (int64_t)s * (D + 2);
+    const float w = fast_exp2(r[D] - M);
+    L += w * r[D + 1];
+    O += w * r[d];
+  }
+  red_o[grp][d] = O;
+  if (d == 0) red_l[grp] = L;
+  __syncthreads();
+  if (grp == 0) {
+    float lt = 0.0f, ot = 0.0f;
+#pragma unroll
+    for (int g2 = 0; g2 < NG; ++g2) { lt += red_l[g2]; ot += red_o[g2][d]; }
+    p.out[(int64_t)h * p.so + d] = f32_to_bf16(ot / fmaxf(lt, 1.0e-20f));
   }
 }
 
 template <int D, int G>
 hipError_t launch_decode_dg(const DecodeParams& p, hipStream_t stream) {
-  if (p.k8)
+  if (D == 128 && G == 4 && p.k8 && decode_mfma_fits(p)) {
+    if (p.scale_is_f16)
+      hipLaunchKernelGGL(decode_mfma_kernel<true>, dim3(p.n_splits, p.Hkv), dim3(64 * kMdWaves), 0, stream, p);
+    else
+      hipLaunchKernelGGL(decode_mfma_kernel<false>, dim3(p.n_splits, p.Hkv), dim3(64 * kMdWaves), 0, stream, p);
+  } else if (p.k8)
     hipLaunchKernelGGL((decode_kernel<D, G, true>), dim3(p.n_splits, p.Hkv), dim3(kDecThreads), 0, stream, p);
   else
     hipLaunchKernelGGL((decode_kernel<D, G, false>), dim3(p.n_splits, p.Hkv), dim3(kDecThreads), 0, stream, p);
-  hipLaunchKernelGGL(decode_merge_kernel<D>, dim3(p.H), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL(decode_merge_kernel<D>, dim3(p.H), dim3(kMergeThreads), 0, stream, p);
   return hipGetLastError();
 }
 
