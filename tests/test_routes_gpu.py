@@ -91,3 +91,35 @@ def test_routes_match_reference_golden(name, dev):
         G = g["H"] // g["Hkv"]
         for h in range(g["H"]):
             assert set(g["planted"][0, h // G].tolist()) <= set(idx[h].cpu().tolist())
+
+
+@pytest.mark.parametrize("name,T,scale_q,scale_k", [
+    ("config2_shape", 131072, 1.0, 1.0),
+    ("large_values", 16384, 40.0, 25.0),
+    ("tiny_values", 16384, 1e-3, 2e-3),
+    ("mixed_rows", 16384, 1.0, 1.0),
+])
+def test_mfma_scores_match_reference_order(name, T, scale_q, scale_k, dev, monkeypatch):
+    """The MFMA score path with exact fix-up must give the same bf16 scores as computing every score in the
+    reference order; compared through the pooled fixed-point values (every unmasked score of a row enters them)
+    and the selected indices, at production size and at magnitudes that put many scores near rounding boundaries."""
+    print(f"case mfma_scores {name} T={T}", flush=True)
+    H, Hkv, d, sink, window, budget = 32, 8, 128, 64, min(16384, T // 4), 512
+    inp = make_inputs(T, H, Hkv, d, seed=11, planted=64 if name == "config2_shape" else 0, sink=sink, window=window,
+                      device=dev, rng="device")
+    q, k = inp["q"] * scale_q, inp["k"] * scale_k
+    if name == "mixed_rows":  # rows and keys spanning many binades, some exact zeros and repeated keys
+        g = torch.Generator(device=dev).manual_seed(3)
+        q = q * torch.exp2(torch.randint(-12, 8, (1, H, T, 1), device=dev, generator=g).to(q.dtype))
+        k = k * torch.exp2(torch.randint(-12, 8, (1, Hkv, T, 1), device=dev, generator=g).to(k.dtype))
+        k[:, :, 1000:1100] = 0
+        k[:, :, 2000:2100] = k[:, :, 3000:3001]
+    kw = dict(num_heads=H, num_kv_heads=Hkv, sink=sink, window=window, budget=budget, scaling=d ** -0.5,
+              return_pooled=True)
+    idx, pooled = hip_routes(q, k, **kw)
+    monkeypatch.setenv("BB_ROUTES_REFERENCE_ORDER", "1")
+    idx_ref, pooled_ref = hip_routes(q, k, **kw)
+    monkeypatch.delenv("BB_ROUTES_REFERENCE_ORDER")
+    torch.cuda.synchronize()
+    assert torch.equal(pooled.cpu(), pooled_ref.cpu()), f"{name}: pooled values differ"
+    assert torch.equal(idx.cpu(), idx_ref.cpu()), f"{name}: route indices differ"

@@ -224,6 +224,13 @@ size_t bb_routes_workspace(int64_t n, int H, int Hkv, int B, int r) {
   return bb::routes_workspace_bytes(n, H, Hkv, B, r);
 }
 
+// BB_ROUTES_REFERENCE_ORDER=1 computes every route score with the reference-order chain instead of MFMA + exact
+// fix-up (same results by construction; the switch exists to cross-check that).
+static int routes_reference_order() {
+  const char* e = getenv("BB_ROUTES_REFERENCE_ORDER");
+  return e && e[0] == '1';
+}
+
 int bb_routes(const void* q, const int64_t* sq, const void* k, const int64_t* sk, const int64_t* qpos, int r, int B,
               int H, int Hkv, int64_t n, int D, int64_t sink, int64_t window, int budget, float scaling, int pool_max,
               int32_t* idx_out, uint64_t* pooled_out, void* ws, size_t ws_bytes, void* stream) {
@@ -254,6 +261,7 @@ int bb_routes(const void* q, const int64_t* sq, const void* k, const int64_t* sk
   p.window = (int)(window < n ? window : n);
   p.budget = budget; p.pool_max = pool_max; p.scaling = scaling;
   p.out_idx = idx_out;
+  p.scores_reference_order = routes_reference_order();
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e = bb::launch_routes(p, ws, ws_bytes, st);
   if (e != hipSuccess) return hip_status(e, "bb_routes");

@@ -39,6 +39,7 @@ struct RoutesParams {
   int64_t sq0, sq1, sk0, sk1;
   int64_t n;
   int H, Hkv, B, D, r, sink, window, budget, pool_max;
+  int scores_reference_order;  // 1: every score by the reference-order chain (no MFMA), for cross-checks
   float scaling;
   uint16_t* scores;     // [B*Hkv][G*r][n] bf16 workspace
   uint32_t* rowmax;     // [B*H*r] ordered-float keys

@@ -177,14 +177,217 @@ __global__ __launch_bounds__(256) void scores_kernel(RoutesParams p, RouteGeom g
   }
 }
 
-__global__ void rowmax_kernel(RoutesParams p, RouteGeom g, const float* __restrict__ pmax) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t total = (int64_t)p.B * p.Hkv * g.rows;
-  if (t >= total) return;
-  const int64_t bkv = t / g.rows, row = t % g.rows;
+// MFMA scores with exact fix-up (head_dim 128). The bf16 score of every (route row, key) must be the one the
+// reference order above produces. Both that order and the MFMA path sum the same 128 exact bf16 products in fp32:
+//   * reference order: at most 21 roundings on any path (16 in an even or odd chain, one for even + odd, four for the
+//     block sum), so its error is at most 21 u sum|q_d k_d| (u = 2^-24);
+//   * MFMA path: each of the eight 16-element slices of d is its own MFMA with a zero accumulator, so a slice's
+//     error is at most 16 x 2^-23 x max|p| <= 32 u sum_slice|p| (16 products aligned to the largest and truncated,
+//     then one rounding), and the eight partials are added in fp32 (7 u): at most 39 u sum|q_d k_d| in all.
+// sum|q_d k_d| comes from a second, accumulating MFMA over |q| and |k| (sign bits cleared; its relative error,
+// below 2^-16, only scales the slack). With B = kScoreSlack sum|q_d k_d| + 2^-100 (kScoreSlack >= 60 u): if s - B
+// and s + B round to the same bf16 value, so does the exact reference-order score, and that value is taken;
+// otherwise (scores near a rounding boundary, or tiny) the score is recomputed in the reference order.
+//
+// Workgroup: one KV head, up to 256 route rows (G r), kScoreIters blocks of 32 keys; 8 waves, wave w owns rows
+// 32w..32w+31 (one MFMA block, Q^T operands in registers; two waves per SIMD hide each other's MFMA, LDS and
+// fix-up latencies). Per key block S^T = K Q^T (eight slice partials) and |K| |Q|^T run on 16 MFMAs with K from LDS.
+// Scores go through an LDS tile per wave so that fix-ups land before one coalesced store.
+constexpr float kScoreSlack = 4.0e-6f;  // 67 u >= (21 + 39) u (1 + 2^-16)
+constexpr int kMsRowPitch = 136;        // bf16 elements per staged Q row (272 bytes: conflict-free row reads)
+constexpr int kMsKPitch = 132;          // floats per fp32 K row (fix-up reads)
+
+constexpr int kMsWaves = 8;
+
+template <int D>
+__global__ __launch_bounds__(64 * kMsWaves) void scores_mfma_kernel(RoutesParams p, RouteGeom g,
+                                                                  float* __restrict__ pmax) {
+  static_assert(D == 128, "MFMA scores are built for head_dim 128");
+  __shared__ __attribute__((aligned(16))) uint16_t qs[kMaxRows][kMsRowPitch];  // Q rows (bf16)
+  __shared__ __attribute__((aligned(16))) uint16_t kt[kScoreKeys][D];          // K block, chunk c of key j at c ^ (j % 16)
+  __shared__ __attribute__((aligned(16))) float kf[kScoreKeys][kMsKPitch];     // the same block in fp32
+  __shared__ __attribute__((aligned(16))) uint16_t st[kMsWaves][32][kScoreKeys];  // per-wave score tile (bf16)
+  __shared__ uint32_t flist[kMsWaves][32 * kScoreKeys];                          // per-wave fix-up list: lane << 4 | r
+  __shared__ uint32_t rmax_fix[kMaxRows];                                      // ordered-float max of fixed-up x
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int li = lane & 31, h = lane >> 5;
+  const int kchunk = blockIdx.x, rblk = blockIdx.y, bkv = blockIdx.z;
+  const int batch = bkv / p.Hkv, kvh = bkv % p.Hkv;
+  const int row0 = rblk * kMaxRows;
+  const int nrows = g.rows - row0 < kMaxRows ? g.rows - row0 : kMaxRows;
+
+  // stage Q rows: row -> (head slot, route query i)
+  for (int e = tid; e < kMaxRows * (D / 8); e += 64 * kMsWaves) {
+    const int row = e / (D / 8), c8 = e % (D / 8);
+    u32x4_t v = {0, 0, 0, 0};
+    if (row < nrows) {
+      const int rr = row0 + row, hs = rr / p.r, i = rr % p.r;
+      const int head = batch * p.H + kvh * g.G + hs;
+      v = ld16(p.q + (int64_t)head * p.sq0 + p.qpos[i] * p.sq1 + 8 * c8);
+    }
+    *reinterpret_cast<u32x4_t*>(&qs[row][8 * c8]) = v;
+  }
+  for (int e = tid; e < kMaxRows; e += 64 * kMsWaves) rmax_fix[e] = 0u;  // ordered key below every float
+  __syncthreads();
+
+  // B operands (Q^T of row 32 wave + li) and the causal limit
+  const int myrow = 32 * wave + li;
+  constexpr u32x4_t kAbs = {0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu};
+  u32x4_t qf[D / 16];
+#pragma unroll
+  for (int dk = 0; dk < D / 16; ++dk) qf[dk] = *reinterpret_cast<const u32x4_t*>(&qs[myrow][16 * dk + 8 * h]);
+  const int64_t qlim = myrow < nrows ? p.qpos[(row0 + myrow) % p.r] : -1;
+  float rmax = -__builtin_huge_valf();
+  const uint16_t* kbase = p.k + (int64_t)bkv * p.sk0;
+  uint16_t* srow_base = p.scores + (int64_t)bkv * g.rows * g.ns;
+  uint16_t (*tile)[kScoreKeys] = st[wave];
+  uint32_t* fl = flist[wave];
+
+  // K blocks: thread (key tid / 16, chunk tid % 16) holds 16 bytes; the next block's load is in flight while the
+  // current one is processed
+  const int skey = tid >> 4, schunk = tid & 15;
+  auto kload = [&](int it) -> u32x4_t {
+    const int64_t j = ((int64_t)kchunk * kScoreIters + it) * kScoreKeys + skey;
+    return j < p.n ? ld16(kbase + j * p.sk1 + 8 * schunk) : u32x4_t{0, 0, 0, 0};
+  };
+  u32x4_t knext = kload(0);
+  for (int it = 0; it < kScoreIters; ++it) {
+    const int64_t j0 = ((int64_t)kchunk * kScoreIters + it) * kScoreKeys;
+    if (j0 >= p.n) break;
+    __syncthreads();  // the previous K block is no longer read
+    {  // stage the K block, bf16 for the MFMA and fp32 for the fix-ups
+      const int key = skey, c = schunk;
+      const u32x4_t v = knext;
+      *reinterpret_cast<u32x4_t*>(&kt[key][8 * (c ^ (key & 15))]) = v;
+      *reinterpret_cast<f32x4_t*>(&kf[key][8 * c]) = f32x4_t{
+          __uint_as_float(v[0] << 16), __uint_as_float(v[0] & 0xffff0000u), __uint_as_float(v[1] << 16),
+          __uint_as_float(v[1] & 0xffff0000u)};
+      *reinterpret_cast<f32x4_t*>(&kf[key][8 * c + 4]) = f32x4_t{
+          __uint_as_float(v[2] << 16), __uint_as_float(v[2] & 0xffff0000u), __uint_as_float(v[3] << 16),
+          __uint_as_float(v[3] & 0xffff0000u)};
+    }
+    __syncthreads();
+    if (it + 1 < kScoreIters) knext = kload(it + 1);
+
+    // S^T = K Q^T as eight slice partials (zero accumulators) summed in fp32, and A^T = |K| |Q|^T
+    // (each partial is added one step later, while the next slice's MFMAs run: two partials live at a time)
+    f32x16_t acc = f32x16_t{}, aac = f32x16_t{}, prev = f32x16_t{};
+#pragma unroll
+    for (int dk = 0; dk < D / 16; ++dk) {
+      const u32x4_t kv = *reinterpret_cast<const u32x4_t*>(&kt[li][8 * ((2 * dk + h) ^ (li & 15))]);
+      const f32x16_t cur = mfma32(as_bf16x8(kv), as_bf16x8(qf[dk]), f32x16_t{});
+      aac = mfma32(as_bf16x8(kv & kAbs), as_bf16x8(qf[dk] & kAbs), aac);
+      if (dk == 1) acc = prev;
+      else if (dk > 1) acc = acc + prev;
+      prev = cur;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    acc = acc + prev;
+
+    // certify or flag every score; lane (li, h) holds row li's keys 8 (r / 4) + 4 h + r % 4 of the block
+    int64_t lim64 = (qlim < p.n - 1 ? qlim : p.n - 1) - j0;  // live keys: kk <= lim
+    const int lim = lim64 < -1 ? -1 : (lim64 > kScoreKeys ? kScoreKeys : (int)lim64);
+    const int limh = lim - 4 * h;  // compared with the lane-independent part of kk
+    // fix-up entries are (lane << 4) | r; the zero comes from an instruction the compiler cannot look through, so
+    // the 16 entry values are formed in the loop rather than hoisted out of it (and spilled)
+    uint32_t opaque_zero;
+    asm volatile("s_mov_b32 %0, 0" : "=s"(opaque_zero));
+    const uint32_t ebase = ((uint32_t)lane << 4) + opaque_zero;
+    uint32_t nfix = 0;
+    uint32_t outw[8];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kk = 8 * (r >> 2) + 4 * h + (r & 3);
+      const float sv = acc[r];
+      const float bound = kScoreSlack * aac[r] + 7.9e-31f;
+      const uint32_t pr = pack_bf16x2(sv - bound, sv + bound);
+      const bool live = 8 * (r >> 2) + (r & 3) <= limh;
+      const bool sure = (pr & 0xffffu) == (pr >> 16);
+      uint32_t out = 0xff80u;  // -inf for masked keys
+      if (live && sure) {
+        out = pr & 0xffffu;
+        rmax = fmaxf(rmax, __uint_as_float(out << 16) * p.scaling);
+      }
+      if (r & 1) outw[r >> 1] |= out << 16;
+      else outw[r >> 1] = out;
+      if ((r & 3) == 3)  // keys 8 (r / 4) + 4 h + 0..3 are consecutive: one 8-byte store
+        *reinterpret_cast<u32x2_t*>(&tile[li][kk - 3]) = u32x2_t{outw[(r >> 1) - 1], outw[r >> 1]};
+      const bool fix = live && !sure;
+      const uint64_t bal = __builtin_amdgcn_ballot_w64(fix);
+      if (fix) {
+        const uint32_t before = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+        fl[nfix + before] = ebase + (uint32_t)r;
+      }
+      nfix += (uint32_t)__builtin_popcountll(bal);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // exact recomputation of the flagged scores in the reference order
+    for (uint32_t e = lane; e < nfix; e += 64) {
+      const uint32_t ent = fl[e];
+      const int el = (int)(ent >> 4), er = (int)(ent & 15u);
+      const int lrow = el & 31, kk = 8 * (er >> 2) + 4 * (el >> 5) + (er & 3);
+      const uint16_t* qr = qs[32 * wave + lrow];
+      const float* kr = kf[kk];
+      float accx = 0.0f;
+#pragma unroll
+      for (int blk = 0; blk < D / 32; ++blk) {
+        float ev = 0.0f, od = 0.0f;
+#pragma unroll
+        for (int c2 = 0; c2 < 4; ++c2) {
+          const int c = 4 * blk + c2;  // 8-element chunk of d
+          const u32x4_t qv = *reinterpret_cast<const u32x4_t*>(qr + 8 * c);
+          const f32x4_t k0 = *reinterpret_cast<const f32x4_t*>(kr + 8 * c);
+          const f32x4_t k1 = *reinterpret_cast<const f32x4_t*>(kr + 8 * c + 4);
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const float ke = w < 2 ? k0[2 * w] : k1[2 * w - 4], ko = w < 2 ? k0[2 * w + 1] : k1[2 * w - 3];
+            ev = __builtin_fmaf(__uint_as_float(qv[w] << 16), ke, ev);
+            od = __builtin_fmaf(__uint_as_float(qv[w] & 0xffff0000u), ko, od);
+          }
+        }
+        accx = accx + (ev + od);
+      }
+      const uint16_t out = f32_to_bf16(accx);
+      tile[lrow][kk] = out;
+      atomicMax(&rmax_fix[32 * wave + lrow], float_to_ordered(bf16_to_f32(out) * p.scaling));
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // tile -> scores: 32 rows x 32 keys, one 16-byte chunk (8 keys) per lane and step
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const int e = 64 * s2 + lane, lrow = e >> 2, c = e & 3;
+      const int row = 32 * wave + lrow;
+      const int64_t j = j0 + 8 * c;
+      if (row < nrows && j + 8 <= g.ns)
+        st16(srow_base + (int64_t)(row0 + row) * g.ns + j, *reinterpret_cast<const u32x4_t*>(&tile[lrow][8 * c]));
+    }
+  }
+  // row maxima: the two halves of a row's lanes, then the fixed-up scores
+  __syncthreads();
+  {
+    const float mx = xhalf_max(rmax);
+    if (h == 0 && myrow < nrows) {
+      const uint32_t fk = rmax_fix[myrow];
+      const float fx = fk ? ordered_to_float(fk) : -__builtin_huge_valf();
+      pmax[((int64_t)bkv * g.n_kb1 + kchunk) * g.rows + row0 + myrow] = fmaxf(mx, fx);
+    }
+  }
+}
+
+// One wave per (KV head, route row): lanes stride over the key-block partials, then a wave maximum.
+__global__ __launch_bounds__(64) void rowmax_kernel(RoutesParams p, RouteGeom g, const float* __restrict__ pmax) {
+  const int row = blockIdx.x, bkv = blockIdx.y, lane = threadIdx.x;
   float mx = -__builtin_huge_valf();
-  for (int kb = 0; kb < g.n_kb1; ++kb) mx = fmaxf(mx, pmax[(bkv * g.n_kb1 + kb) * g.rows + row]);
-  p.rowmax[t] = __float_as_uint(mx);
+  for (int kb = lane; kb < g.n_kb1; kb += 64) mx = fmaxf(mx, pmax[((int64_t)bkv * g.n_kb1 + kb) * g.rows + row]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+  if (lane == 0) p.rowmax[(int64_t)bkv * g.rows + row] = __float_as_uint(mx);
 }
 
 // Fixed-point partial row sums: one wave per row (4 rows in flight per workgroup), 16 keys per lane.
@@ -379,9 +582,13 @@ template <int D>
 hipError_t launch_routes_d(RoutesParams& p, const RouteGeom& g, float* pmax, uint64_t* psum, float* invz,
                            hipStream_t stream) {
   const int nbkv = p.B * p.Hkv;
-  hipLaunchKernelGGL(scores_kernel<D>, dim3(g.n_kb1, g.row_blocks, nbkv), dim3(256), 0, stream, p, g, pmax);
+  if (D == 128 && !p.scores_reference_order)
+    hipLaunchKernelGGL(scores_mfma_kernel<128>, dim3(g.n_kb1, g.row_blocks, nbkv), dim3(64 * kMsWaves), 0, stream, p,
+                       g, pmax);
+  else
+    hipLaunchKernelGGL(scores_kernel<D>, dim3(g.n_kb1, g.row_blocks, nbkv), dim3(256), 0, stream, p, g, pmax);
   const int64_t rows_total = (int64_t)nbkv * g.rows;
-  hipLaunchKernelGGL(rowmax_kernel, dim3((unsigned)((rows_total + 255) / 256)), dim3(256), 0, stream, p, g, pmax);
+  hipLaunchKernelGGL(rowmax_kernel, dim3(g.rows, nbkv), dim3(64), 0, stream, p, g, pmax);
   hipLaunchKernelGGL(rowsum_kernel, dim3(g.n_kb2, nbkv), dim3(256), 0, stream, p, g, psum);
   hipLaunchKernelGGL(invz_kernel, dim3((unsigned)((rows_total + 255) / 256)), dim3(256), 0, stream, p, g, psum, invz);
   hipLaunchKernelGGL(pooled_kernel, dim3((unsigned)((p.n + kPoolKeys - 1) / kPoolKeys), p.B * p.H), dim3(kPoolKeys), 0,
