@@ -18,8 +18,10 @@
 //   rowsum_kernel   fixed-point partial row sums over 1024-key blocks
 //   invz_kernel     partial sums -> fp32 scale 2^40 / Z per row
 //   pooled_kernel   per (head, key): pooled fixed-point probability over the r rows
-//   topk_kernel     one 1024-thread workgroup per head: MSD radix select on the 64-bit pooled values, then an
-//                   ordered compaction that emits the selected indices ascending (ties -> lower index)
+//   topk_*_kernel   top-budget per head: log-linear histogram over many workgroups, the threshold bin, compaction of
+//                   the keys above it and of its candidates, exact choice among the candidates (value desc, index asc)
+//                   and ascending emission through a bitmap; an MSD radix select over the whole range when the
+//                   candidates overflow (heavy ties)
 #include "bb_common.h"
 #include "bb_internal.h"
 
@@ -33,6 +35,7 @@ constexpr int kScoreKeys = 32;    // keys per scores_kernel block (8 key groups 
 constexpr int kScoreIters = 8;    // key blocks per scores_kernel workgroup
 constexpr int kSumKeys = 1024;    // keys per rowsum_kernel workgroup
 constexpr int kPoolKeys = 256;    // keys per pooled_kernel workgroup
+constexpr int kTopBinsPool = 2080;  // top-k histogram bins (kTopBins), cleared by pooled_kernel
 constexpr int kMaxRows = 256;     // G * r handled by one scores workgroup (rows beyond this use more row blocks)
 constexpr float kFixOne = 1099511627776.0f;  // 2^40
 
@@ -420,21 +423,30 @@ __global__ __launch_bounds__(256) void rowsum_kernel(RoutesParams p, RouteGeom g
   }
 }
 
-__global__ void invz_kernel(RoutesParams p, RouteGeom g, const uint64_t* __restrict__ psum, float* __restrict__ invz) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t total = (int64_t)p.B * p.Hkv * g.rows;
-  if (t >= total) return;
-  const int64_t bkv = t / g.rows, row = t % g.rows;
+// One wave per (KV head, route row): integer partial sums (order-free), then 2^40 / Z.
+__global__ __launch_bounds__(64) void invz_kernel(RoutesParams p, RouteGeom g, const uint64_t* __restrict__ psum,
+                                                 float* __restrict__ invz) {
+  const int row = blockIdx.x, bkv = blockIdx.y, lane = threadIdx.x;
   uint64_t z = 0;
-  for (int kb = 0; kb < g.n_kb2; ++kb) z += psum[(bkv * g.n_kb2 + kb) * g.rows + row];
-  p.rowsum[t] = z;
-  invz[t] = (float)(1099511627776.0 / (double)z);
+  for (int kb = lane; kb < g.n_kb2; kb += 64) z += psum[((int64_t)bkv * g.n_kb2 + kb) * g.rows + row];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) z += __shfl_xor(z, off);
+  if (lane == 0) {
+    const int64_t t = (int64_t)bkv * g.rows + row;
+    p.rowsum[t] = z;
+    invz[t] = (float)(1099511627776.0 / (double)z);
+  }
 }
 
 // Pooled fixed-point probability per (query head, key): thread per key, loop over the head's r rows.
-__global__ __launch_bounds__(256) void pooled_kernel(RoutesParams p, RouteGeom g, const float* __restrict__ invz) {
+__global__ __launch_bounds__(256) void pooled_kernel(RoutesParams p, RouteGeom g, const float* __restrict__ invz,
+                                                    uint32_t* __restrict__ top_hist, uint32_t* __restrict__ top_meta) {
   const int64_t j = (int64_t)blockIdx.x * kPoolKeys + threadIdx.x;
   const int head = blockIdx.y;  // over B * H
+  if (blockIdx.x == 0) {  // clear this head's top-k histogram and list counters (the next kernels accumulate)
+    for (int b = threadIdx.x; b < kTopBinsPool; b += kPoolKeys) top_hist[(int64_t)head * kTopBinsPool + b] = 0u;
+    if (threadIdx.x < 8) top_meta[8 * head + threadIdx.x] = 0u;
+  }
   if (j >= p.n) return;
   const int batch = head / p.H, hh = head % p.H;
   const int kvh = hh / g.G, hs = hh % g.G;
@@ -457,9 +469,11 @@ __global__ __launch_bounds__(256) void pooled_kernel(RoutesParams p, RouteGeom g
   p.pooled[(int64_t)head * p.n + j] = P;
 }
 
-// Top-budget selection per head: MSD radix select over 8-bit digits, then ordered compaction.
+// Top-budget selection for one head by one 1024-thread workgroup: MSD radix select over 8-bit digits of the whole
+// eligible range, then ordered compaction. The general path (any ties, any budget); topk_final_kernel uses it when
+// the candidate set of the fast path overflows.
 constexpr int kTopThreads = 1024;
-__global__ __launch_bounds__(kTopThreads) void topk_kernel(RoutesParams p) {
+__device__ __noinline__ void topk_radix_head(const RoutesParams& p, int head) {
   __shared__ uint32_t hist[256];
   __shared__ uint64_t red[kTopThreads / 64];
   __shared__ uint32_t scan_sel[kTopThreads];
@@ -468,7 +482,7 @@ __global__ __launch_bounds__(kTopThreads) void topk_kernel(RoutesParams p) {
   __shared__ int64_t s_need;
   __shared__ int s_exact;
 
-  const int head = blockIdx.x, tid = threadIdx.x;
+  const int tid = threadIdx.x;
   const int64_t lo = p.sink < p.n ? (p.sink > 0 ? p.sink : 0) : p.n;
   int64_t hi = p.n - p.window;
   if (hi > p.n) hi = p.n;
@@ -578,23 +592,215 @@ __global__ __launch_bounds__(kTopThreads) void topk_kernel(RoutesParams p) {
   }
 }
 
+// Fast top-budget selection in four launches (all heads at once):
+//   topk_hist_kernel     many workgroups per head: 2080-bin log-linear histogram of the pooled values (bin = 32 x
+//                        bit length + the 5 bits after the leading one; 0 for zero), monotone in the value
+//   topk_pick_kernel     per head: the bin b* holding the budget-th largest value; `above` values lie in higher bins
+//   topk_compact_kernel  many workgroups per head: indices of values above b* to `sel`, (value, index) of values in
+//                        b* to the candidate list (at most kTopCand kept; the count goes on)
+//   topk_final_kernel    per head: the need = budget - above best candidates by (value desc, index asc), then all
+//                        chosen keys through an LDS bitmap of the eligible range, emitted ascending; when the
+//                        candidates overflowed or the range is too long for the bitmap, topk_radix_head instead
+constexpr int kTopBins = 2080;
+constexpr int kTopChunk = 4096;       // values per histogram / compaction workgroup (256 threads x 16)
+constexpr int kTopCand = 2048;        // candidates kept per head
+constexpr int kTopBitmapBits = 262144;
+
+static_assert(kTopBins == kTopBinsPool, "pooled_kernel clears the top-k histogram");
+struct TopMeta {
+  int32_t bstar, above, need, flags;
+  uint32_t nsel, ncand, pad0, pad1;
+};
+struct TopWs {
+  uint32_t* hist;     // [heads][kTopBins]
+  TopMeta* meta;      // [heads]
+  int32_t* sel;       // [heads][n]
+  uint64_t* candv;    // [heads][kTopCand]
+  int32_t* candi;     // [heads][kTopCand]
+};
+
+BB_DEV int top_bin(uint64_t v) {
+  if (!v) return 0;
+  const int lz = __clzll((long long)v);
+  return 32 * (64 - lz) + (int)((v << lz) >> 58 & 31u);
+}
+
+BB_DEV void top_range(const RoutesParams& p, int64_t& lo, int64_t& cnt) {
+  lo = p.sink < p.n ? (p.sink > 0 ? p.sink : 0) : p.n;
+  int64_t hi = p.n - p.window;
+  if (hi > p.n) hi = p.n;
+  cnt = hi > lo ? hi - lo : 0;
+}
+
+__global__ __launch_bounds__(256) void topk_hist_kernel(RoutesParams p, TopWs w) {
+  __shared__ uint32_t h[kTopBins];
+  const int head = blockIdx.y, tid = threadIdx.x;
+  int64_t lo, cnt;
+  top_range(p, lo, cnt);
+  for (int b = tid; b < kTopBins; b += 256) h[b] = 0;
+  __syncthreads();
+  const uint64_t* P = p.pooled + (int64_t)head * p.n + lo;
+  const int64_t t0 = (int64_t)blockIdx.x * kTopChunk;
+  for (int e = tid; e < kTopChunk; e += 256)
+    if (t0 + e < cnt) atomicAdd(&h[top_bin(P[t0 + e])], 1u);
+  __syncthreads();
+  for (int b = tid; b < kTopBins; b += 256)
+    if (h[b]) atomicAdd(&w.hist[(int64_t)head * kTopBins + b], h[b]);
+}
+
+__global__ __launch_bounds__(256) void topk_pick_kernel(RoutesParams p, TopWs w) {
+  constexpr int PER = (kTopBins + 255) / 256;  // bins per thread, taken from the top
+  __shared__ uint32_t part[256];
+  const int head = blockIdx.x, tid = threadIdx.x;
+  const uint32_t* hist = w.hist + (int64_t)head * kTopBins;
+  uint32_t c[PER], sum = 0;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int b = kTopBins - 1 - (PER * tid + k);
+    c[k] = b >= 0 ? hist[b] : 0u;
+    sum += c[k];
+  }
+  part[tid] = sum;
+  __syncthreads();
+  for (int off = 1; off < 256; off <<= 1) {  // inclusive scan over threads (top bins first)
+    const uint32_t a = tid >= off ? part[tid - off] : 0u;
+    __syncthreads();
+    part[tid] += a;
+    __syncthreads();
+  }
+  const uint32_t before = part[tid] - sum, budget = (uint32_t)p.budget;
+  if (before < budget && part[tid] >= budget) {  // the budget-th largest value lies in this thread's bins
+    uint32_t cum = before;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      if (cum + c[k] >= budget) {
+        TopMeta m = {};
+        m.bstar = kTopBins - 1 - (PER * tid + k);
+        m.above = (int32_t)cum;
+        m.need = (int32_t)(budget - cum);
+        w.meta[head] = m;
+        break;
+      }
+      cum += c[k];
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void topk_compact_kernel(RoutesParams p, TopWs w) {
+  const int head = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+  int64_t lo, cnt;
+  top_range(p, lo, cnt);
+  const uint64_t* P = p.pooled + (int64_t)head * p.n + lo;
+  TopMeta* m = w.meta + head;
+  const int bstar = m->bstar;
+  const int64_t t0 = (int64_t)blockIdx.x * kTopChunk;
+  for (int e = tid; e < kTopChunk; e += 256) {
+    const int64_t t = t0 + e;
+    const uint64_t v = t < cnt ? P[t] : 0;
+    const int b = t < cnt ? top_bin(v) : -1;
+    // wave-aggregated appends: one atomic per wave and list
+    const uint64_t bs = __builtin_amdgcn_ballot_w64(b > bstar), bc = __builtin_amdgcn_ballot_w64(b == bstar);
+    const uint32_t below_s = __builtin_amdgcn_mbcnt_hi((uint32_t)(bs >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bs, 0u));
+    const uint32_t below_c = __builtin_amdgcn_mbcnt_hi((uint32_t)(bc >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bc, 0u));
+    uint32_t base_s = 0, base_c = 0;
+    if (lane == 0) {
+      if (bs) base_s = atomicAdd(&m->nsel, (uint32_t)__builtin_popcountll(bs));
+      if (bc) base_c = atomicAdd(&m->ncand, (uint32_t)__builtin_popcountll(bc));
+    }
+    base_s = __shfl(base_s, 0);
+    base_c = __shfl(base_c, 0);
+    if (b > bstar) w.sel[(int64_t)head * p.n + base_s + below_s] = (int32_t)(lo + t);
+    if (b == bstar && base_c + below_c < (uint32_t)kTopCand) {
+      w.candv[(int64_t)head * kTopCand + base_c + below_c] = v;
+      w.candi[(int64_t)head * kTopCand + base_c + below_c] = (int32_t)(lo + t);
+    }
+  }
+}
+
+__global__ __launch_bounds__(kTopThreads) void topk_final_kernel(RoutesParams p, TopWs w) {
+  __shared__ uint64_t cv[kTopCand];
+  __shared__ int32_t ci[kTopCand];
+  __shared__ uint32_t bits[kTopBitmapBits / 32];
+  __shared__ uint32_t scan[kTopThreads];
+  const int head = blockIdx.x, tid = threadIdx.x;
+  int64_t lo, cnt;
+  top_range(p, lo, cnt);
+  const TopMeta m = w.meta[head];
+  if (m.ncand > (uint32_t)kTopCand || cnt > kTopBitmapBits) {
+    topk_radix_head(p, head);
+    return;
+  }
+  const int nc = (int)m.ncand;
+  const int words = (int)((cnt + 31) / 32);
+  for (int i = tid; i < nc; i += kTopThreads) {
+    cv[i] = w.candv[(int64_t)head * kTopCand + i];
+    ci[i] = w.candi[(int64_t)head * kTopCand + i];
+  }
+  for (int i = tid; i < words; i += kTopThreads) bits[i] = 0u;
+  __syncthreads();
+  // chosen candidates: fewer than `need` others beat them (larger value, or equal value and lower index)
+  for (int i = tid; i < nc; i += kTopThreads) {
+    const uint64_t v = cv[i];
+    const int32_t ix = ci[i];
+    int rank = 0;
+    for (int j = 0; j < nc; ++j) rank += (cv[j] > v) || (cv[j] == v && ci[j] < ix);
+    if (rank < m.need) atomicOr(&bits[(ix - lo) >> 5], 1u << ((ix - lo) & 31));
+  }
+  for (uint32_t i = tid; i < m.nsel; i += kTopThreads) {
+    const int32_t ix = w.sel[(int64_t)head * p.n + i];
+    atomicOr(&bits[(ix - lo) >> 5], 1u << ((ix - lo) & 31));
+  }
+  __syncthreads();
+  // ascending emission: each thread a contiguous run of words, exclusive scan of their bit counts
+  const int per = (words + kTopThreads - 1) / kTopThreads;
+  const int w0 = tid * per, w1 = w0 + per < words ? w0 + per : words;
+  uint32_t mine = 0;
+  for (int x = w0; x < w1; ++x) mine += __builtin_popcount(bits[x]);
+  scan[tid] = mine;
+  __syncthreads();
+  for (int off = 1; off < kTopThreads; off <<= 1) {
+    const uint32_t a = tid >= off ? scan[tid - off] : 0u;
+    __syncthreads();
+    scan[tid] += a;
+    __syncthreads();
+  }
+  uint32_t pos = scan[tid] - mine;
+  int32_t* out = p.out_idx + (int64_t)head * p.budget;
+  for (int x = w0; x < w1; ++x) {
+    uint32_t b = bits[x];
+    while (b) {
+      const int bit = __builtin_ctz(b);
+      b &= b - 1;
+      if (pos < (uint32_t)p.budget) out[pos] = (int32_t)(lo + 32 * x + bit);
+      ++pos;
+    }
+  }
+}
+
 template <int D>
 hipError_t launch_routes_d(RoutesParams& p, const RouteGeom& g, float* pmax, uint64_t* psum, float* invz,
-                           hipStream_t stream) {
+                           const TopWs& tw, hipStream_t stream) {
   const int nbkv = p.B * p.Hkv;
   if (D == 128 && !p.scores_reference_order)
     hipLaunchKernelGGL(scores_mfma_kernel<128>, dim3(g.n_kb1, g.row_blocks, nbkv), dim3(64 * kMsWaves), 0, stream, p,
                        g, pmax);
   else
     hipLaunchKernelGGL(scores_kernel<D>, dim3(g.n_kb1, g.row_blocks, nbkv), dim3(256), 0, stream, p, g, pmax);
-  const int64_t rows_total = (int64_t)nbkv * g.rows;
   hipLaunchKernelGGL(rowmax_kernel, dim3(g.rows, nbkv), dim3(64), 0, stream, p, g, pmax);
   hipLaunchKernelGGL(rowsum_kernel, dim3(g.n_kb2, nbkv), dim3(256), 0, stream, p, g, psum);
-  hipLaunchKernelGGL(invz_kernel, dim3((unsigned)((rows_total + 255) / 256)), dim3(256), 0, stream, p, g, psum, invz);
+  hipLaunchKernelGGL(invz_kernel, dim3(g.rows, nbkv), dim3(64), 0, stream, p, g, psum, invz);
   hipLaunchKernelGGL(pooled_kernel, dim3((unsigned)((p.n + kPoolKeys - 1) / kPoolKeys), p.B * p.H), dim3(kPoolKeys), 0,
-                     stream, p, g, invz);
-  if (p.budget > 0)
-    hipLaunchKernelGGL(topk_kernel, dim3(p.B * p.H), dim3(kTopThreads), 0, stream, p);
+                     stream, p, g, invz, tw.hist, reinterpret_cast<uint32_t*>(tw.meta));
+  if (p.budget > 0) {
+    int64_t lo = p.sink < p.n ? (p.sink > 0 ? p.sink : 0) : p.n, hi = p.n - p.window < p.n ? p.n - p.window : p.n;
+    const int64_t cnt = hi > lo ? hi - lo : 0;
+    const unsigned chunks = (unsigned)((cnt + kTopChunk - 1) / kTopChunk);
+    const int heads = p.B * p.H;
+    hipLaunchKernelGGL(topk_hist_kernel, dim3(chunks, heads), dim3(256), 0, stream, p, tw);
+    hipLaunchKernelGGL(topk_pick_kernel, dim3(heads), dim3(256), 0, stream, p, tw);
+    hipLaunchKernelGGL(topk_compact_kernel, dim3(chunks, heads), dim3(256), 0, stream, p, tw);
+    hipLaunchKernelGGL(topk_final_kernel, dim3(heads), dim3(kTopThreads), 0, stream, p, tw);
+  }
   return hipGetLastError();
 }
 
@@ -611,6 +817,21 @@ RouteGeom geom(int64_t n, int H, int Hkv, int r) {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+size_t top_ws_bytes(int64_t n, size_t heads) {
+  return align256(heads * kTopBins * 4) + align256(heads * sizeof(TopMeta)) + align256(heads * (size_t)n * 4) +
+         align256(heads * kTopCand * 8) + align256(heads * kTopCand * 4);
+}
+
+TopWs carve_top_ws(char* w, int64_t n, size_t heads) {
+  TopWs t;
+  t.hist = reinterpret_cast<uint32_t*>(w); w += align256(heads * kTopBins * 4);
+  t.meta = reinterpret_cast<TopMeta*>(w); w += align256(heads * sizeof(TopMeta));
+  t.sel = reinterpret_cast<int32_t*>(w); w += align256(heads * (size_t)n * 4);
+  t.candv = reinterpret_cast<uint64_t*>(w); w += align256(heads * kTopCand * 8);
+  t.candi = reinterpret_cast<int32_t*>(w);
+  return t;
+}
+
 }  // namespace
 
 size_t routes_workspace_bytes(int64_t n, int H, int Hkv, int B, int r) {
@@ -624,6 +845,7 @@ size_t routes_workspace_bytes(int64_t n, int H, int Hkv, int B, int r) {
   s += align256(nbkv * g.rows * 8);                       // row sums
   s += align256(nbkv * g.rows * 4);                       // 2^40 / Z
   s += align256((size_t)B * H * (size_t)n * 8);           // pooled
+  s += top_ws_bytes(n, (size_t)B * H);
   return s;
 }
 
@@ -638,11 +860,12 @@ hipError_t launch_routes(RoutesParams& p, void* ws, size_t ws_bytes, hipStream_t
   uint64_t* psum = reinterpret_cast<uint64_t*>(w); w += align256(nbkv * g.n_kb2 * g.rows * 8);
   p.rowsum = reinterpret_cast<uint64_t*>(w); w += align256(nbkv * g.rows * 8);
   float* invz = reinterpret_cast<float*>(w); w += align256(nbkv * g.rows * 4);
-  p.pooled = reinterpret_cast<uint64_t*>(w);
+  p.pooled = reinterpret_cast<uint64_t*>(w); w += align256((size_t)p.B * p.H * (size_t)p.n * 8);
+  const TopWs tw = carve_top_ws(w, p.n, (size_t)p.B * p.H);
   switch (p.D) {
-    case 32: return launch_routes_d<32>(p, g, pmax, psum, invz, stream);
-    case 64: return launch_routes_d<64>(p, g, pmax, psum, invz, stream);
-    case 128: return launch_routes_d<128>(p, g, pmax, psum, invz, stream);
+    case 32: return launch_routes_d<32>(p, g, pmax, psum, invz, tw, stream);
+    case 64: return launch_routes_d<64>(p, g, pmax, psum, invz, tw, stream);
+    case 128: return launch_routes_d<128>(p, g, pmax, psum, invz, tw, stream);
     default: return hipErrorInvalidValue;
   }
 }
