@@ -210,7 +210,9 @@ int bb_sparse_flash(const void* q, const int64_t* sq, const void* k, const int64
   if (s.split) {
     p.part_o = reinterpret_cast<float*>(wsp);
     p.part_ml = p.part_o + (size_t)s.n_chunks * BH * T * D;
-    hipError_t e = bb::launch_flash(p, D, s.hpw, true, st);
+    hipError_t e = (flash_pipe_enabled() && s.hpw == 4 && bb::flash_pipe_supported(p, D))
+                       ? bb::launch_flash_pipe(p, st)
+                       : bb::launch_flash(p, D, s.hpw, true, st);
     if (e != hipSuccess) return hip_status(e, "bb_sparse_flash split kernel");
     return hip_status(bb::launch_flash_merge(p, D, st), "bb_sparse_flash merge kernel");
   }

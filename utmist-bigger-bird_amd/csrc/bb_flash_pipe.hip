@@ -298,7 +298,7 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
 
   // ---- work item: (KV head, 64-row tile), XCD-aware as in flash_kernel ----
   const int lanes_total = p.n_kvbh * p.head_splits;
-  const int per_lane = p.row_tiles;
+  const int per_lane = p.row_tiles * p.n_chunks;  // split mode: (row tile, key chunk) pairs
   int lane_id, within;
   const int bid = blockIdx.x;
   if (p.remap) {
@@ -309,7 +309,8 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
     lane_id = bid % lanes_total;
     within = bid / lanes_total;
   }
-  const int rt = p.row_tiles - 1 - within;
+  const int rt = p.row_tiles - 1 - within / p.n_chunks;
+  const int chunk = within % p.n_chunks;
   const int kvbh = lane_id / p.head_splits, hsplit = lane_id % p.head_splits;
   const int batch = kvbh / p.Hkv_pb;
   const int bh = batch * p.H + (kvbh % p.Hkv_pb) * p.G + hsplit * PHEADS + hd;
@@ -365,8 +366,25 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
   int64_t uc = (qlo + 1) / kTileKeys;
   if (uc > w1) uc = w1;
   if (uc < ub) uc = ub;
-  const int nu = (int)(ua + (uc - ub));
-  auto upos = [&](int t) -> int64_t { return (t < ua ? (int64_t)t : ub + (t - ua)) * kTileKeys; };
+  // split mode (exact tail: no routes): only the tiles of key chunk `chunk`, [c0, c1)
+  int64_t c0 = 0, c1 = w1 > f1 ? w1 : f1;
+  if (p.n_chunks > 1) {
+    c0 = (int64_t)chunk * p.key_chunk / kTileKeys;
+    const int64_t ce = ((int64_t)chunk + 1) * p.key_chunk / kTileKeys;
+    if (ce < c1) c1 = ce;
+  }
+  auto clip = [&](int64_t& a, int64_t& b) {
+    if (a < c0) a = c0;
+    if (b > c1) b = c1;
+    if (b < a) b = a;
+  };
+  int64_t ua0 = 0, ua1 = ua;
+  clip(ua0, ua1);
+  clip(ub, uc);
+  const int nu = (int)((ua1 - ua0) + (uc - ub));
+  auto upos = [&](int t) -> int64_t {
+    return (t < ua1 - ua0 ? ua0 + (int64_t)t : ub + (t - (ua1 - ua0))) * kTileKeys;
+  };
 
   uint16_t* ring = smem;
   auto kst = [&](int t) { return ring + (t & (PST - 1)) * 2 * PTE; };
@@ -407,12 +425,14 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
 
   // ---- edge tiles (element masks), one at a time through ring stage 0 ----
   {
-    const int64_t ranges[2][2] = {{0, f1}, {w0, w1}};
+    int64_t ranges[2][2] = {{0, f1}, {w0, w1}};
+    clip(ranges[0][0], ranges[0][1]);
+    clip(ranges[1][0], ranges[1][1]);
 #pragma unroll 1
     for (int rg = 0; rg < 2; ++rg) {
 #pragma unroll 1
       for (int64_t j = ranges[rg][0]; j < ranges[rg][1]; ++j) {
-        if (j < ua || (j >= ub && j < uc)) continue;  // done in the loop above
+        if ((j >= ua0 && j < ua1) || (j >= ub && j < uc)) continue;  // done in the loop above
         const int64_t k0 = j * kTileKeys;
         __syncthreads();  // the stage is free
         ld.tile(kst(0), vst(0), k0);
@@ -510,6 +530,21 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
   const int64_t row = rw + li;
   const float lt = xhalf_sum(st.l);
   if (row >= T_eff) return;
+  if (p.n_chunks > 1) {  // partial (O, m, l) of this key chunk for flash_merge_kernel
+    const int64_t base = ((int64_t)chunk * p.BH + bh) * p.T + row;
+    float* po = p.part_o + base * PD;
+#pragma unroll
+    for (int dv = 0; dv < PD / 32; ++dv)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4)
+        *reinterpret_cast<f32x4_t*>(po + 32 * dv + 8 * g4 + 4 * h) =
+            f32x4_t{st.o[dv][4 * g4], st.o[dv][4 * g4 + 1], st.o[dv][4 * g4 + 2], st.o[dv][4 * g4 + 3]};
+    if (h == 0) {
+      p.part_ml[2 * base] = st.m;
+      p.part_ml[2 * base + 1] = lt;
+    }
+    return;
+  }
   const float inv = 1.0f / fmaxf(lt, 1.0e-20f);
   uint16_t* orow = p.out + (int64_t)bh * p.so0 + row * p.so1;
 #pragma unroll
@@ -526,13 +561,14 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
 }  // namespace
 
 bool flash_pipe_supported(const FlashParams& p, int D) {
-  // buffer offsets are 32-bit: one KV head's K rows and V^T must each span < 2 GiB
+  // buffer offsets are 32-bit: one KV head's K rows and V^T must each span < 2 GiB; split mode needs whole tiles
   const bool fits = p.N * p.sk1 * 2 < ((int64_t)1 << 31) && (int64_t)PD * p.np * 2 < ((int64_t)1 << 31);
-  return D == PD && p.G % PHEADS == 0 && p.key_mask == nullptr && fits;
+  const bool chunks_ok = p.n_chunks == 1 || (p.key_chunk % kTileKeys == 0 && p.route_k == 0);
+  return D == PD && p.G % PHEADS == 0 && p.key_mask == nullptr && fits && chunks_ok;
 }
 
 hipError_t launch_flash_pipe(const FlashParams& p, hipStream_t stream) {
-  const int64_t items = (int64_t)p.n_kvbh * p.head_splits * p.row_tiles;
+  const int64_t items = (int64_t)p.n_kvbh * p.head_splits * p.row_tiles * p.n_chunks;
   if (items <= 0) return hipSuccess;
   if (items > 0x7fffffff) return hipErrorInvalidValue;
   hipLaunchKernelGGL(flash_ping_kernel, dim3((unsigned)items), dim3(64 * PNW), 0, stream, p);
