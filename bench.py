@@ -92,7 +92,7 @@ def main_traffic():
     path = ROOT / "profiles" / "prefill_128k_hbm_traffic.json"
     try:
         data = json.loads(path.read_text())
-        return int(data["kernels"]["flash_ping_kernel"]["bytes"])
+        return int(data["kernels"]["flash_ping_kernel [main]"]["bytes"])
     except (OSError, KeyError, ValueError):
         return None
 
