@@ -14,8 +14,9 @@ Printed JSON (one line): value = ms per layer (lower is better); effective TFLOP
 4*d FLOP per pair counted from the actual routes; `roofline` for the dominant kernel (the main sparse kernel) from
 HIP events around its launches on the stream it runs on; `cpu_baseline` = the CPU restatement of the reference's
 PyTorch path (oracle.routes_reference_order + oracle.flash_ref) timed on a bounded sample and scaled to a layer.
-Also reported, next to the headline: `tail_roofline` (the exact 256-row tail, TFLOP/s and HBM GB/s) and `decode`
-(INT8-KV decode: microseconds per step and HBM GB/s against 8 TB/s).
+Also reported, next to the headline: `tail_roofline` (the exact 256-row tail, TFLOP/s and HBM GB/s), `decode`
+(INT8-KV decode: microseconds per step and HBM GB/s against 8 TB/s) and `short_arm`
+(B=4 at T=32768: sparse prefill against dense causal SDPA on the same inputs).
 """
 import argparse
 import json
@@ -44,6 +45,8 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true", help="skip the INT8 decode leg (BASELINE configs[4])")
+    ap.add_argument("--no-short-arm", action="store_true",
+                    help="skip the B=4, T=32768 sparse-vs-dense leg (BASELINE configs[3])")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 1 GiB device copy 5 times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--cpu-sample-blocks", type=int, default=96,
@@ -179,6 +182,53 @@ def decode_leg(dev, seed):
             "kernels": "quantize x2 + decode_mfma_kernel + decode_merge_kernel per step"}
 
 
+def short_arm_leg(dev, seed):
+    """B=4, T=32768, cfg {64, 4096, 512, 256}: sparse_prefill (routes + main + tail, each batch
+    element a layer call) against dense causal attention on the same inputs (torch SDPA, flash backend forced so that
+    no [T, T] matrix is ever formed; K/V repeated to the query heads)."""
+    import torch
+    import torch.nn.functional as F
+    from bigger_bird_amd import RDAttention
+    from bigger_bird_amd.synth import make_inputs
+
+    B, H, Hkv, T, d = 4, 32, 8, 32768, 128
+    cfg = dict(sink=64, window=4096, vertical=512, exact_tail=256)
+    inp = make_inputs(T, H, Hkv, d, batch=B, seed=seed + 3, sink=cfg["sink"], window=cfg["window"], device=dev,
+                      rng="device")
+    q, k, v = inp["q"], inp["k"], inp["v"]
+    attn = RDAttention(stub_base(H, Hkv, d), **cfg)
+
+    def timed(fn, reps=3):
+        fn()
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            best = min(best, a.elapsed_time(b))
+        return best
+
+    res = {"workload": "BASELINE configs[3]: B=4, T=32768, 32q/8kv heads, d=128, cfg {64, 4096, 512, 256}"}
+    with torch.inference_mode():
+        res["sparse_ms"] = round(timed(lambda: attn.sparse_prefill(q, k, v)), 3)
+        try:
+            from torch.nn.attention import SDPBackend, sdpa_kernel
+            kr = k.repeat_interleave(H // Hkv, dim=1)
+            vr = v.repeat_interleave(H // Hkv, dim=1)
+            with sdpa_kernel(SDPBackend.FLASH_ATTENTION):
+                res["dense_ms"] = round(timed(lambda: F.scaled_dot_product_attention(q, kr, vr, is_causal=True,
+                                                                                      scale=d ** -0.5)), 3)
+            res["speedup"] = round(res["dense_ms"] / res["sparse_ms"], 2)
+            res["dense"] = "torch SDPA flash backend (ROCm), causal, K/V repeated to 32 heads"
+        except RuntimeError as e:  # no flash backend for this shape: report the sparse time only
+            res["dense_ms"] = None
+            res["dense"] = f"unavailable: {str(e)[:120]}"
+    return res
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -289,6 +339,7 @@ def main():
                           "hbm_frac": round(tail_bytes / (stage_avg["tail"] * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
                           "bytes": tail_bytes},
         "decode": None if args.no_decode else decode_leg(dev, args.seed),
+        "short_arm": None if args.no_short_arm else short_arm_leg(dev, args.seed),
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:

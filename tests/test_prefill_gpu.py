@@ -59,3 +59,39 @@ def test_sparse_prefill_matches_oracle(name, dev):
         print(f"{name} {what}: rows={pr.shape[0]} max_abs={err.max().item():.3e} mean_abs={err.mean().item():.3e}",
               flush=True)
         assert err.max().item() < 2e-2 and err.mean().item() < 2e-3
+
+
+def test_config4_batch_sampled_rows(dev):
+    """BASELINE configs[3] shape: B=4, T=32768, {64, 4096, 512, 256}; each batch element against the float64 oracle
+    on sampled rows (main pass, window edges, tail), with that element's own routes."""
+    print("case prefill config4 B=4 T=32768", flush=True)
+    from bigger_bird_amd.synth import make_inputs
+    B, H, Hkv, T, d = 4, 32, 8, 32768, 128
+    cfg = dict(sink=64, window=4096, vertical=512, exact_tail=256)
+    inp = make_inputs(T, H, Hkv, d, batch=B, seed=4, sink=cfg["sink"], window=cfg["window"], device=dev,
+                      rng="device")
+    attn = RDAttention(_base(H, Hkv, d), **cfg)
+    with torch.inference_mode():
+        out = attn.sparse_prefill(inp["q"], inp["k"], inp["v"])
+    torch.cuda.synchronize()
+    assert out.shape == (B, H, T, d) and attn.last_routes.shape == (B, H, 512)
+    W, r, G = cfg["window"], cfg["exact_tail"], H // Hkv
+    gen = torch.Generator().manual_seed(9)
+    rows = torch.tensor([0, 63, 64, W - 1, W, W + 64, T // 2, T - r - 1, T - r, T - 1])
+    rows = torch.cat([rows, torch.randint(0, T, (4,), generator=gen)])
+    for b in range(B):
+        q, k, v = inp["q"][b].cpu(), inp["k"][b].cpu(), inp["v"][b].cpu()
+        routes = attn.last_routes[b].cpu()
+        heads = torch.tensor([0, 5, 17, 31])
+        pairs = torch.stack([heads.repeat_interleave(rows.numel()), rows.repeat(heads.numel())], -1)
+        main, tail = pairs[pairs[:, 1] < T - r], pairs[pairs[:, 1] >= T - r]
+        ref_main = oracle.attn_rows(q, k, v, routes[:, None], main, front=cfg["sink"], window=W, num_heads=H,
+                                    kv_groups=G, scale=d ** -0.5)
+        none = torch.full((H, 1, 1), -1, dtype=torch.int32)
+        ref_tail = oracle.attn_rows(q, k, v, none, tail, front=0, window=T, num_heads=H, kv_groups=G,
+                                    scale=d ** -0.5)
+        o = out[b].cpu()
+        for what, pr, ref in (("main", main, ref_main), ("tail", tail, ref_tail)):
+            err = (o[pr[:, 0], pr[:, 1]].double() - ref).abs()
+            print(f"config4 b={b} {what}: max_abs={err.max().item():.3e} mean_abs={err.mean().item():.3e}", flush=True)
+            assert err.max().item() < 2e-2 and err.mean().item() < 2e-3
