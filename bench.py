@@ -45,6 +45,8 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true", help="skip the INT8 decode leg (BASELINE configs[4])")
+    ap.add_argument("--full-model", action="store_true",
+                    help="only run the full-model prefill (BASELINE configs[2]): random-init Llama-3-8B, sparse and exact arms")
     ap.add_argument("--no-short-arm", action="store_true",
                     help="skip the B=4, T=32768 sparse-vs-dense leg (BASELINE configs[3])")
     ap.add_argument("--copy-probe", action="store_true",
@@ -229,6 +231,77 @@ def short_arm_leg(dev, seed):
     return res
 
 
+def full_model_leg(dev, seed, T=131072):
+    """BASELINE configs[2] (SURVEY next step): prefill of a random-init Llama-3-8B-architecture model in bf16 (32 layers,
+    hidden 4096, 32 q / 8 KV heads, FFN 14336, vocab 128256, RoPE theta 500000) at T uniform-random token ids, with
+    RDAttention on every layer: the sparse arm (final cfg {64, 16384, 512, 256}) and the exact arm (`dense_rd`: the
+    same module with exact causal attention on the HIP kernel). KV cache on, last-token logits only, as the
+    reference's long-context prefill runs (modal_rd/RESULTS.md:37-43). Projections, MLP and norms are PyTorch."""
+    import torch
+    from transformers import LlamaConfig, LlamaForCausalLM
+    from bigger_bird_amd import install
+
+    cfg = LlamaConfig(vocab_size=128256, hidden_size=4096, intermediate_size=14336, num_hidden_layers=32,
+                      num_attention_heads=32, num_key_value_heads=8, max_position_embeddings=T, rope_theta=500000.0,
+                      rms_norm_eps=1e-5, attn_implementation="sdpa")
+    old = torch.get_default_dtype()
+    torch.manual_seed(seed)
+    try:
+        torch.set_default_dtype(torch.bfloat16)
+        with torch.device(dev):
+            model = LlamaForCausalLM(cfg)
+    finally:
+        torch.set_default_dtype(old)
+    model.eval()
+    g = torch.Generator(device=dev).manual_seed(seed + 7)
+    ids = torch.randint(0, cfg.vocab_size, (1, T), generator=g, device=dev)
+    print("full model built", file=sys.stderr, flush=True)
+
+    def run():
+        with torch.inference_mode():
+            return model(input_ids=ids, use_cache=True, logits_to_keep=1).logits[0, -1].float()
+
+    def timed(reps, arm):
+        best, logits = float("inf"), None
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            logits = run()
+            torch.cuda.synchronize()
+            best = min(best, time.perf_counter() - t0)
+            print(f"full model {arm}: {time.perf_counter() - t0:.3f} s", file=sys.stderr, flush=True)
+        return best, logits
+
+    res = {"workload": f"BASELINE configs[2]: random-init Llama-3-8B architecture, bf16, T={T}, KV cache on, "
+                       "last-token logits; arms: HF sdpa (unmodified model), RDAttention sparse final cfg on all 32 "
+                       "layers, RDAttention exact (dense_rd)"}
+    # Arm 1: the unmodified HF model (sdpa attention; flash or memory-efficient backend, never the math one).
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    lh = None
+    try:
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            run()
+            res["hf_sdpa_s"], lh = timed(1, "hf sdpa")
+            res["hf_sdpa_s"] = round(res["hf_sdpa_s"], 3)
+    except RuntimeError as e:  # no fused SDPA kernel for this shape: report, keep going with the RD arms
+        res["hf_sdpa_s"] = f"unavailable: {str(e)[:160]}"
+    attn_cfg = dict(sink=64, window=16384, vertical=512, exact_tail=256)
+    install(model, "rd", **attn_cfg)
+    run()  # warm-up: kernels loaded, allocator sized
+    sparse_s, ls = timed(2, "rd sparse")
+    install(model, "dense_rd", **attn_cfg)
+    dense_s, ld = timed(1, "dense_rd")
+    cos = torch.nn.functional.cosine_similarity
+    res.update({"sparse_s": round(sparse_s, 3), "exact_rd_s": round(dense_s, 3),
+                "h100_reference_s": {"sparse_final_cfg": 8.50, "dense": 16.22, "tokens": 127545},
+                "logits_cosine_sparse_vs_exact_rd": round(cos(ls, ld, dim=0).item(), 5),
+                "top1_sparse_eq_exact_rd": bool(ls.argmax().item() == ld.argmax().item())})
+    if lh is not None:
+        res["logits_cosine_exact_rd_vs_hf_sdpa"] = round(cos(ld, lh, dim=0).item(), 5)
+        res["logits_max_abs_exact_rd_vs_hf_sdpa"] = round((ld - lh).abs().max().item(), 5)
+    return res
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -239,6 +312,9 @@ def main():
 
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a ROCm GPU")
+    if args.full_model:
+        print(json.dumps({"full_model": full_model_leg(torch.device("cuda:0"), args.seed, args.T)}), flush=True)
+        return
     if args.copy_probe:
         src = torch.ones(1 << 29, dtype=torch.int16, device="cuda")  # 1 GiB
         dst = torch.empty_like(src)
