@@ -382,8 +382,34 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
   clip(ua0, ua1);
   clip(ub, uc);
   const int nu = (int)((ua1 - ua0) + (uc - ub));
-  auto upos = [&](int t) -> int64_t {
-    return (t < ua1 - ua0 ? ua0 + (int64_t)t : ub + (t - (ua1 - ua0))) * kTileKeys;
+  // The remaining tiles of [0, f1) u [w0, w1) need element masks: front tiles past the unmasked prefix [ua1, f1),
+  // the window start [max(w0, ua1), ub) and the diagonal [uc, w1) (typically one tile each for the last two). They
+  // run in the same loop, after the unmasked ones, with the masked softmax.
+  int64_t ma0 = ua1, ma1 = f1 > 0 ? f1 : ua1;
+  int64_t mb0 = w0 > ua1 ? w0 : ua1, mb1 = ub;
+  int64_t mc0 = uc, mc1 = w1;
+  clip(ma0, ma1);
+  clip(mb0, mb1);
+  clip(mc0, mc1);
+  const int ntot = nu + (int)((ma1 - ma0) + (mb1 - mb0) + (mc1 - mc0));
+  // tile of list entry t: t + the offset of the range t falls in, as a sum of 32-bit steps (scalar selects; kept
+  // wave-uniform explicitly so that the buffer loads take it as a scalar offset)
+  const int n1 = (int)(ua1 - ua0), n2 = nu, n3 = n2 + (int)(ma1 - ma0), n4 = n3 + (int)(mb1 - mb0);
+  const int d1 = (int)ua0, e2 = (int)ub - n1 - d1, e3 = (int)(ma0 - ub) - (n2 - n1), e4 = (int)(mb0 - ma0) - (n3 - n2),
+            e5 = (int)(mc0 - mb0) - (n4 - n3);
+  auto upos = [=](int t) -> int64_t {
+    const int d = d1 + (t >= n1 ? e2 : 0) + (t >= n2 ? e3 : 0) + (t >= n3 ? e4 : 0) + (t >= n4 ? e5 : 0);
+    return (int64_t)__builtin_amdgcn_readfirstlane(t + d) * kTileKeys;
+  };
+  // VALU phase of tile t: the lazy softmax for unmasked tiles, the masked one (front | causal window) otherwise
+  auto softmax = [&](int t) {
+    if (t < nu) {
+      ping_softmax_open(st, p.c);
+    } else {
+      const int64_t k0 = upos(t), k1 = k0 + kTileKeys - 1;
+      const bool live = wave_live && k0 <= qw1 && !(k0 >= p.front && k1 <= qw0 - p.window);
+      ping_softmax_masked(st, p.c, qme, PipeWindowMask{k0, p.front, p.window, live}, h);
+    }
   };
 
   uint16_t* ring = smem;
@@ -392,19 +418,21 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
   TileLoader ld;
   ld.init(kbase, p.sk1, p.N, vtbase, p.np, wave, lane);
 
-  if (nu > 0) {
+  if (ntot > 0) {
     ld.tile(kst(0), vst(0), upos(0));
-    if (nu > 1) ld.tile(kst(1), vst(1), upos(1));
-    vm_wait_tile(nu > 1);
+    if (ntot > 1) ld.tile(kst(1), vst(1), upos(1));
+    vm_wait_tile(ntot > 1);
     ring_barrier();
     if (rbk == 1) ring_barrier();  // waves 4..7 run one phase behind
     // tile 0: QK only
-    if (nu > 2) ld.tile(kst(2), vst(2), upos(2));
+    if (ntot > 2) ld.tile(kst(2), vst(2), upos(2));
     ping_qk(st, kst(0), li, h);
-    vm_wait_tile(nu > 2);
+    vm_wait_tile(ntot > 2);
     ring_barrier();
-    ping_softmax_open(st, p.c);
+    softmax(0);
     ring_barrier();
+    // Two copies of the loop body, unmasked tiles then masked ones, so that the register allocation of the hot one
+    // does not carry the mask arithmetic.
     for (int t = 1; t < nu; ++t) {
       // MFMA phase: PV of tile t-1, QK of tile t
       __builtin_amdgcn_s_setprio(1);
@@ -416,36 +444,22 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
       // the MFMA phase that last read it). The loads come after the exponentials: issuing a direct load stalls the
       // wave for as long as the CU's address unit is busy with the other waves' loads.
       ping_softmax_open(st, p.c);
-      if (t + 2 < nu) ld.tile(kst(t + 2), vst(t + 2), upos(t + 2));
+      if (t + 2 < ntot) ld.tile(kst(t + 2), vst(t + 2), upos(t + 2));
       ring_barrier();
     }
-    ping_pv(st, vst(nu - 1), li, h);
-    if (rbk == 0) ring_barrier();  // realign the two groups
-  }
-
-  // ---- edge tiles (element masks), one at a time through ring stage 0 ----
-  {
-    int64_t ranges[2][2] = {{0, f1}, {w0, w1}};
-    clip(ranges[0][0], ranges[0][1]);
-    clip(ranges[1][0], ranges[1][1]);
 #pragma unroll 1
-    for (int rg = 0; rg < 2; ++rg) {
-#pragma unroll 1
-      for (int64_t j = ranges[rg][0]; j < ranges[rg][1]; ++j) {
-        if ((j >= ua0 && j < ua1) || (j >= ub && j < uc)) continue;  // done in the loop above
-        const int64_t k0 = j * kTileKeys;
-        __syncthreads();  // the stage is free
-        ld.tile(kst(0), vst(0), k0);
-        vm_wait_tile(false);
-        __syncthreads();
-        const int64_t k1 = k0 + kTileKeys - 1;
-        const bool live = wave_live && k0 <= qw1 && !(k0 >= p.front && k1 <= qw0 - p.window);
-        const PipeWindowMask wm{k0, p.front, p.window, live};
-        ping_qk(st, kst(0), li, h);
-        ping_softmax_masked(st, p.c, qme, wm, h);
-        ping_pv(st, vst(0), li, h);
-      }
+    for (int t = nu > 1 ? nu : 1; t < ntot; ++t) {
+      __builtin_amdgcn_s_setprio(1);
+      ping_mfma_phase(st, kst(t), vst(t - 1), li, h);
+      __builtin_amdgcn_s_setprio(0);
+      vm_wait_tile(false);
+      ring_barrier();
+      softmax(t);
+      if (t + 2 < ntot) ld.tile(kst(t + 2), vst(t + 2), upos(t + 2));
+      ring_barrier();
     }
+    ping_pv(st, vst(ntot - 1), li, h);
+    if (rbk == 0) ring_barrier();  // realign the two groups
   }
 
   // ---- routed keys: per-head gathered tiles; the two waves of a head share the gather ----
