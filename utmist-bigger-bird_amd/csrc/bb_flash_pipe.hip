@@ -30,6 +30,7 @@ constexpr int PTE = kTileKeys * PD;     // elements of one K (or V^T) tile
 constexpr int PST = 4;                  // ring stages, each a K tile and a V^T tile
 constexpr int PBLK = PTE * 2 / 1024;    // 1 KB direct-load blocks per tile (16)
 constexpr int PLDS = PST * 2 * PTE;     // 128 KB; the routed phase reuses it as 4 heads x (K + V^T)
+constexpr int kRouteCache = 512;        // route slots per head staged in LDS at a time
 static_assert(PHEADS * 2 * PTE <= PLDS, "routed tiles fit the ring");
 
 typedef __attribute__((__vector_size__(4 * sizeof(int32_t)))) int32_t i32x4_t;
@@ -288,8 +289,8 @@ BB_DEV void ping_softmax_open(PingState& st, float c) {
 
 __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) {
   __shared__ __attribute__((aligned(1024))) uint16_t smem[PLDS];
-  __shared__ __attribute__((aligned(16))) int32_t route_keys[PHEADS][kTileKeys];
-  __shared__ int head_batches[PHEADS];
+  __shared__ __attribute__((aligned(16))) int32_t route_keys[PHEADS][kRouteCache];
+  __shared__ int head_batches[2][PHEADS];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -471,70 +472,74 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
     if (g_last >= p.n_groups) g_last = p.n_groups - 1;
     for (int64_t g = g_first; g <= g_last; ++g) {
       const int32_t* irow = p.idx + (int64_t)bh * p.si0 + g * p.si1;
-      // batches of 64 route slots holding at least one key some row of the workgroup can use
-      if (rbk == 0) {
+      // The head's route slots, kRouteCache at a time, go to LDS in one pass (usable keys, -1 elsewhere: a key some
+      // row of the workgroup attends is >= front, < N and <= qhi - window), so that the gathers below do not wait
+      // on index loads. Batches of 64 slots run up to the last one holding a usable key.
+      for (int sb = 0; sb < p.route_k; sb += kRouteCache) {
+        const int nslots = p.route_k - sb < kRouteCache ? p.route_k - sb : kRouteCache;
         int nbh = 0;
-        for (int s0 = 0; s0 < p.route_k; s0 += kTileKeys) {
+        for (int s0 = 64 * rbk; s0 < kRouteCache; s0 += 128) {
           const int sl = s0 + lane;
-          const int64_t key = sl < p.route_k ? irow[(int64_t)sl * p.si2] : -1;
+          const int64_t key = sl < nslots ? irow[(int64_t)(sb + sl) * p.si2] : -1;
           const bool ok = key >= p.front && key < p.N && key <= qhi - p.window;
+          route_keys[hd][sl] = ok ? (int32_t)key : -1;
           if (__builtin_amdgcn_ballot_w64(ok)) nbh = s0 / kTileKeys + 1;
         }
-        if (lane == 0) head_batches[hd] = nbh;
-      }
-      __syncthreads();
-      int nb = 0;
-      const int my_nb = head_batches[hd];
-#pragma unroll
-      for (int x = 0; x < PHEADS; ++x) nb = nb > head_batches[x] ? nb : head_batches[x];
-      for (int bi = 0; bi < nb; ++bi) {
-        const bool work = bi < my_nb;
-        if (work && rbk == 0) {
-          const int sl = bi * kTileKeys + lane;
-          const int64_t key = sl < p.route_k ? irow[(int64_t)sl * p.si2] : -1;
-          const bool ok = key >= p.front && key < p.N && key <= qhi - p.window;
-          route_keys[hd][lane] = ok ? (int32_t)key : -1;
-        }
+        if (lane == 0) head_batches[rbk][hd] = nbh;  // each of the head's two waves scanned half of the slots
         __syncthreads();
-        if (work) {
-          // K rows by direct loads (the head's two waves split the 16 blocks)
-          for (int b = rbk; b < PBLK; b += 2) {
-            const int e = b * 512 + 8 * lane;
-            const int row = e / PD, sl2 = (e % PD) / 8;
-            const int chk = sl2 ^ (row & (PD / 8 - 1));
-            const int32_t kr = route_keys[hd][row];
-            lds_dma16(kbase + (int64_t)(kr >= 0 ? kr : 0) * p.sk1 + 8 * chk, kl + b * 512);
+        int nb = 0, my_nb = 0;
+#pragma unroll
+        for (int x = 0; x < PHEADS; ++x)
+#pragma unroll
+          for (int y = 0; y < 2; ++y) {
+            const int v = head_batches[y][x];
+            nb = nb > v ? nb : v;
+            if (x == hd) my_nb = my_nb > v ? my_nb : v;
           }
-          // V rows -> V^T through registers: units of 4 keys x 8 d
-          for (int u = lane + 64 * rbk; u < (kTileKeys / 4) * (PD / 8); u += 128) {
-            const int bq = u % (PD / 8), a4 = u / (PD / 8);
-            u32x4_t vr[4];
-#pragma unroll
-            for (int s2 = 0; s2 < 4; ++s2) {
-              const int32_t kr = route_keys[hd][4 * a4 + s2];
-              vr[s2] = kr >= 0 ? ld16(vbase + (int64_t)kr * p.sv1 + 8 * bq) : u32x4_t{0, 0, 0, 0};
+        __syncthreads();  // head_batches and route_keys are rewritten only after every wave has read them
+        for (int bi = 0; bi < nb; ++bi) {
+          const bool work = bi < my_nb;
+          const int32_t* keys = route_keys[hd] + kTileKeys * bi;
+          if (work) {
+            // K rows by direct loads (the head's two waves split the 16 blocks)
+            for (int b = rbk; b < PBLK; b += 2) {
+              const int e = b * 512 + 8 * lane;
+              const int row = e / PD, sl2 = (e % PD) / 8;
+              const int chk = sl2 ^ (row & (PD / 8 - 1));
+              const int32_t kr = keys[row];
+              lds_dma16(kbase + (int64_t)(kr >= 0 ? kr : 0) * p.sk1 + 8 * chk, kl + b * 512);
             }
+            // V rows -> V^T through registers: units of 4 keys x 8 d
+            for (int u = lane + 64 * rbk; u < (kTileKeys / 4) * (PD / 8); u += 128) {
+              const int bq = u % (PD / 8), a4 = u / (PD / 8);
+              u32x4_t vr[4];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const int w = e >> 1;
-              const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-              const uint32_t lo = __builtin_amdgcn_perm(vr[1][w], vr[0][w], sel);
-              const uint32_t hi = __builtin_amdgcn_perm(vr[3][w], vr[2][w], sel);
-              const int d = 8 * bq + e;
-              *reinterpret_cast<u32x2_t*>(vt + vt_off(d, 2 * (a4 >> 2) + (a4 & 1)) + 4 * ((a4 >> 1) & 1)) =
-                  u32x2_t{lo, hi};
+              for (int s2 = 0; s2 < 4; ++s2) {
+                const int32_t kr = keys[4 * a4 + s2];
+                vr[s2] = kr >= 0 ? ld16(vbase + (int64_t)kr * p.sv1 + 8 * bq) : u32x4_t{0, 0, 0, 0};
+              }
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                const int w = e >> 1;
+                const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+                const uint32_t lo = __builtin_amdgcn_perm(vr[1][w], vr[0][w], sel);
+                const uint32_t hi = __builtin_amdgcn_perm(vr[3][w], vr[2][w], sel);
+                const int d = 8 * bq + e;
+                *reinterpret_cast<u32x2_t*>(vt + vt_off(d, 2 * (a4 >> 2) + (a4 & 1)) + 4 * ((a4 >> 1) & 1)) =
+                    u32x2_t{lo, hi};
+              }
             }
           }
+          vm_wait_tile(false);
+          __syncthreads();
+          if (work && wave_live) {
+            const PipeRoutedMask rm{keys, p.window, p.route_chunk, g};
+            ping_qk(st, kl, li, h);
+            ping_softmax_masked(st, p.c, qme, rm, h);
+            ping_pv(st, vt, li, h);
+          }
+          __syncthreads();
         }
-        vm_wait_tile(false);
-        __syncthreads();
-        if (work && wave_live) {
-          const PipeRoutedMask rm{route_keys[hd], p.window, p.route_chunk, g};
-          ping_qk(st, kl, li, h);
-          ping_softmax_masked(st, p.c, qme, rm, h);
-          ping_pv(st, vt, li, h);
-        }
-        __syncthreads();
       }
     }
   }

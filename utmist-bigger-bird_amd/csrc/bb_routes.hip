@@ -398,12 +398,23 @@ __global__ __launch_bounds__(256) void rowsum_kernel(RoutesParams p, RouteGeom g
   const int kb = blockIdx.x, bkv = blockIdx.y;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t j0 = (int64_t)kb * kSumKeys + 16 * lane;
+  // the next row's scores are loaded while this row's are summed
+  u32x4_t na = {0, 0, 0, 0}, nb = {0, 0, 0, 0};
+  if (wave < g.rows && j0 + 16 <= p.n) {
+    const uint16_t* src = p.scores + ((int64_t)bkv * g.rows + wave) * g.ns + j0;
+    na = ld16(src);
+    nb = ld16(src + 8);
+  }
   for (int row = wave; row < g.rows; row += 4) {
     const float M = __uint_as_float(p.rowmax[(int64_t)bkv * g.rows + row]);
     const uint16_t* src = p.scores + ((int64_t)bkv * g.rows + row) * g.ns + j0;
     uint64_t acc = 0;
     if (j0 + 16 <= p.n) {
-      const u32x4_t a = ld16(src), b = ld16(src + 8);
+      const u32x4_t a = na, b = nb;
+      if (row + 4 < g.rows) {
+        na = ld16(src + 4 * g.ns);
+        nb = ld16(src + 4 * g.ns + 8);
+      }
       uint32_t w[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
@@ -454,13 +465,27 @@ __global__ __launch_bounds__(256) void pooled_kernel(RoutesParams p, RouteGeom g
   uint64_t P = 0;
   const bool eligible = j >= p.sink && j < p.n - p.window;
   if (eligible) {
-    for (int i = 0; i < p.r; ++i) {
-      const int64_t row = (int64_t)hs * p.r + i;
-      const int64_t ridx = bkv * g.rows + row;
-      const float M = __uint_as_float(p.rowmax[ridx]);
-      const uint16_t sb = p.scores[ridx * g.ns + j];
-      const float x = bf16_to_f32(sb) * p.scaling;
-      const float e = det_exp2((x - M) * kLog2e);
+    // eight rows per step: their score loads are in flight together (one row at a time waits on every load)
+    const int64_t ridx0 = bkv * g.rows + (int64_t)hs * p.r;
+    int i = 0;
+    for (; i + 8 <= p.r; i += 8) {
+      uint16_t sb[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) sb[u] = p.scores[(ridx0 + i + u) * g.ns + j];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int64_t ridx = ridx0 + i + u;
+        const float x = bf16_to_f32(sb[u]) * p.scaling;
+        const float e = det_exp2((x - __uint_as_float(p.rowmax[ridx])) * kLog2e);
+        const uint64_t pf = fix40(e * invz[ridx]);
+        if (p.pool_max) P = pf > P ? pf : P;
+        else P += pf;
+      }
+    }
+    for (; i < p.r; ++i) {
+      const int64_t ridx = ridx0 + i;
+      const float x = bf16_to_f32(p.scores[ridx * g.ns + j]) * p.scaling;
+      const float e = det_exp2((x - __uint_as_float(p.rowmax[ridx])) * kLog2e);
       const uint64_t pf = fix40(e * invz[ridx]);
       if (p.pool_max) P = pf > P ? pf : P;
       else P += pf;
