@@ -104,6 +104,37 @@ int bb_decode(const void* q, int64_t sq, const int8_t* k8, const void* ks, const
 size_t bb_decode_workspace(int64_t n, int H, int Hkv, int D);
 
 /*
+ * Split-K sparse decode of one query token over a bf16 (is_f16 = 0) or fp16 KV cache. Every route row attends its
+ * virtual key list front | window | routed: position j for j < front, n - window + i for the window, idx[row][i]
+ * for the routed keys; positions outside [0, n) are skipped. Replaces bigger_bird_decode
+ * (kernels/bigger_bird_decode.py:66-108).
+ *   q [H, D] (row stride sq); k, v [Hkv, cap, D] (strides sk[2], sv[2]: head, token; any cache view)
+ *   idx [rows, route_k] int32 (strides si[2]; -1 = empty): rows = Hkv (pooled: the groups query heads of a KV head
+ *   share one list) or rows = H (per-head lists); NULL when route_k == 0
+ *   n_dev: the current length as one int64 in device memory (a captured graph stays valid as it grows), or NULL
+ *   to use n; splits: key chunks (0 = about four workgroups per CU); out [H, D] (row stride so), input dtype.
+ */
+int bb_sparse_decode(const void* q, int64_t sq, const void* k, const int64_t* sk, const void* v, const int64_t* sv,
+                     const int32_t* idx, const int64_t* si, int rows, int route_k, int64_t n, const int64_t* n_dev,
+                     int64_t cap, int H, int Hkv, int D, int front, int window, float scale, int splits, int is_f16,
+                     void* out, int64_t so, void* ws, size_t ws_bytes, void* stream);
+
+size_t bb_sparse_decode_workspace(int H, int Hkv, int D, int rows, int front, int window, int route_k, int splits);
+
+/*
+ * Fused decode routing for one query token: probs_out [Hkv, cap] fp32 = per KV head the mean over its query heads
+ * of the softmax probability over the first n cached keys, -1 outside [front, n - window); with k_route > 0 also
+ * idx_out [Hkv, k_route], the keys with the largest pooled probability (ties to the lower index), ascending, -1 past
+ * the eligible count. n / n_dev as in bb_sparse_decode. Replaces pooled_probs and bigger_bird_route
+ * (kernels/bigger_bird_route.py:83-115).
+ */
+int bb_decode_route(const void* q, int64_t sq, const void* k, const int64_t* sk, int64_t n, const int64_t* n_dev,
+                    int64_t cap, int H, int Hkv, int D, int front, int window, float scale, int splits, int is_f16,
+                    float* probs_out, int k_route, int32_t* idx_out, void* ws, size_t ws_bytes, void* stream);
+
+size_t bb_decode_route_workspace(int64_t cap, int H, int Hkv, int splits, int k_route);
+
+/*
  * In-place RoPE on x [B, Hh, T, D] (strides sx[3]) with cos/sin [B, T, D] (strides sc[2]; 0 to broadcast), with
  * the arithmetic of HF apply_rotary_pos_emb on bf16 tensors (bit-identical). Replaces rope_inplace
  * (modal_rd/attention.py:51-60).

@@ -1,0 +1,188 @@
+"""Split-K sparse decode and fused decode routing on the GPU (through the C ABI) against the float64 oracles.
+
+Mirrors the reference's kernels/tests/test_bigger_bird_decode.py and test_bigger_bird_route.py: the same shapes,
+strided cache views, pooled and per-head route rows, the device-side length with garbage past it, dense mode, the
+short-cache error, and the same bars (decode: atol = rtol = 1e-2; pooled probabilities: atol 1e-6, rtol 2e-3;
+routes: at least 99% overlap with the oracle's top-k, near-ties may swap). Beyond the reference: the routed keys
+must be exactly the top-k of the kernel's own probabilities with ties to the lower index, and a captured HIP graph
+of a whole decode step (append to the cache, route, decode) replays with a growing device-side length and matches
+the same step run eagerly.
+"""
+import pytest
+import torch
+
+import oracle
+from bigger_bird_amd import bigger_bird_decode, bigger_bird_route, pooled_probs
+
+pytestmark = pytest.mark.gpu
+
+
+def _cache(n, hk, d, dtype, seed, scale_k=2.0):
+    g = torch.Generator().manual_seed(seed)
+    cache = torch.randn(2, 1, hk, n, d, generator=g).to(dtype)
+    return cache[0, 0] * scale_k, cache[1, 0]
+
+
+def _routes(rows, n, front, window, r, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.stack([front + torch.randperm(n - window - front, generator=g)[:r] for _ in range(rows)])
+
+
+@pytest.mark.parametrize("n,front,window,routed,pooled,splits,dtype", [
+    (4096, 64, 1024, 256, True, None, torch.bfloat16),
+    (4096, 64, 1024, 256, False, None, torch.bfloat16),
+    (20000, 64, 4096, 512, True, 7, torch.float16),
+    (20000, 16, 333, 1000, False, 1, torch.bfloat16),
+    (70000, 64, 16384, 512, True, None, torch.bfloat16),
+])
+def test_sparse_decode_matches_oracle(n, front, window, routed, pooled, splits, dtype, dev):
+    print(f"case sparse_decode n={n} pooled={pooled} splits={splits} {dtype}", flush=True)
+    h, hk, d = 32, 8, 128
+    k, v = _cache(n, hk, d, dtype, 0)
+    g = torch.Generator().manual_seed(1)
+    q = torch.randn(h, d, generator=g).to(dtype)
+    idx = _routes(hk if pooled else h, n, front, window, routed, 2)
+    kd, vd = k.to(dev), v.to(dev)  # strided views of one [2, 1, Hkv, n, d] buffer on the host; copies keep strides
+    out = bigger_bird_decode(q.to(dev), kd, vd, idx.to(dev), front=front, window=window, scale=d ** -0.5,
+                             splits=splits)
+    ref = oracle.sparse_decode(q, k, v, idx, front=front, window=window, scale=d ** -0.5)
+    assert out.dtype == dtype and out.shape == (h, d)
+    torch.testing.assert_close(out.float().cpu().double(), ref, atol=1e-2, rtol=1e-2)
+
+
+def test_strided_cache_view(dev):
+    """K/V as views of one [2, 1, Hkv, cap, d] device buffer (the reference's cache layout), with a per-head list."""
+    print("case strided_view", flush=True)
+    h, hk, d, n = 32, 8, 128, 6000
+    g = torch.Generator().manual_seed(3)
+    cache = torch.randn(2, 1, hk, n, d, generator=g).to(torch.bfloat16).to(dev)
+    k, v = cache[0, 0], cache[1, 0]
+    q = torch.randn(h, d, generator=g).to(torch.bfloat16).to(dev)
+    idx = _routes(h, n, 32, 512, 200, 4).to(dev)
+    out = bigger_bird_decode(q, k, v, idx, front=32, window=512, scale=0.09)
+    ref = oracle.sparse_decode(q.cpu(), k.cpu(), v.cpu(), idx.cpu(), front=32, window=512, scale=0.09)
+    torch.testing.assert_close(out.float().cpu().double(), ref, atol=1e-2, rtol=1e-2)
+
+
+def test_device_length_and_dense_mode(dev):
+    """n as a GPU tensor inside a larger buffer (garbage past it); front=0 / window=cap / no routes = dense."""
+    print("case device_length_dense", flush=True)
+    h, hk, d, cap, n = 32, 8, 128, 9000, 7777
+    g = torch.Generator().manual_seed(5)
+    k = torch.randn(hk, cap, d, generator=g).to(torch.bfloat16)
+    v = torch.randn(hk, cap, d, generator=g).to(torch.bfloat16)
+    k[:, n:] = 100
+    q = torch.randn(h, d, generator=g).to(torch.bfloat16)
+    length = torch.tensor([n], device=dev)
+    idx = _routes(hk, n, 64, 1024, 300, 6)
+    sparse = bigger_bird_decode(q.to(dev), k.to(dev), v.to(dev), idx.to(dev), front=64, window=1024, scale=d ** -0.5,
+                                n=length)
+    ref = oracle.sparse_decode(q, k[:, :n], v[:, :n], idx, front=64, window=1024, scale=d ** -0.5)
+    torch.testing.assert_close(sparse.float().cpu().double(), ref, atol=1e-2, rtol=1e-2)
+    none = torch.empty(hk, 0, dtype=torch.long, device=dev)
+    dense = bigger_bird_decode(q.to(dev), k.to(dev), v.to(dev), none, front=0, window=cap, scale=d ** -0.5, n=length)
+    exact = oracle.sparse_decode(q, k[:, :n], v[:, :n], torch.empty(hk, 0, dtype=torch.long), front=0, window=n,
+                                 scale=d ** -0.5)
+    torch.testing.assert_close(dense.float().cpu().double(), exact, atol=1e-2, rtol=1e-2)
+
+
+def test_rejects_short_cache(dev):
+    k = torch.zeros(8, 100, 128, device=dev, dtype=torch.bfloat16)
+    q = torch.zeros(32, 128, device=dev, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="cache shorter than front"):
+        bigger_bird_decode(q, k, k, torch.zeros(8, 4, dtype=torch.long, device=dev), front=64, window=64)
+    with pytest.raises(ValueError, match="indices must be"):
+        bigger_bird_decode(q, k, k, torch.zeros(3, 4, dtype=torch.long, device=dev), front=8, window=8)
+    with pytest.raises(ValueError, match="FP16/BF16"):
+        bigger_bird_decode(q.float(), k, k, torch.zeros(8, 4, dtype=torch.long, device=dev), front=8, window=8)
+
+
+@pytest.mark.parametrize("cap,n,front,window,routed,dtype,device_n", [
+    (5000, 5000, 64, 1024, 256, torch.bfloat16, False),
+    (40000, 40000, 64, 4096, 1024, torch.bfloat16, False),
+    (40000, 33333, 16, 1000, 512, torch.float16, True),
+    (131072, 131072, 64, 1024, 1024, torch.bfloat16, False),
+])
+def test_route_matches_oracle(cap, n, front, window, routed, dtype, device_n, dev):
+    print(f"case route cap={cap} n={n} device_n={device_n} {dtype}", flush=True)
+    h, hk, d = 32, 8, 128
+    g = torch.Generator().manual_seed(0)
+    k = (torch.randn(hk, cap, d, generator=g) * 2).to(dtype)
+    k[:, n:] = 50
+    q = torch.randn(h, d, generator=g).to(dtype)
+    scale = d ** -0.5
+    kw = dict(front=front, window=window, scale=scale, n=torch.tensor([n], device=dev) if device_n else None)
+    k_in = (k if device_n else k[:, :n]).to(dev)
+    p = pooled_probs(q.to(dev), k_in, **kw).cpu()
+    ref = oracle.pooled_probs(q, k[:, :n], front=front, window=window, scale=scale)
+    torch.testing.assert_close(p[:, :n].double(), ref, atol=1e-6, rtol=2e-3)
+    if device_n:
+        assert (p[:, n:] == -1).all()
+    idx = bigger_bird_route(q.to(dev), k_in, routed, **kw).cpu()
+    want = ref.topk(routed, dim=-1).indices
+    for kv, (a, b) in enumerate(zip(idx.tolist(), want.tolist())):
+        assert len(set(a) & set(b)) >= 0.99 * routed, kv  # near-ties may swap at the boundary
+        # exactly the top-k of the kernel's own probabilities (value desc, index asc), ascending
+        vals = p[kv, front:n - window]
+        order = torch.argsort(-vals, stable=True)[:routed] + front
+        assert a == sorted(order.tolist()), kv
+
+
+def test_route_fewer_eligible_than_budget(dev):
+    """Fewer eligible keys than k_route: all of them, ascending, then -1."""
+    h, hk, d, n = 8, 2, 64, 300
+    g = torch.Generator().manual_seed(9)
+    k = torch.randn(hk, n, d, generator=g).to(torch.bfloat16).to(dev)
+    q = torch.randn(h, d, generator=g).to(torch.bfloat16).to(dev)
+    idx = bigger_bird_route(q, k, 64, front=10, window=250, scale=0.1).cpu()
+    want = torch.cat([torch.arange(10, 50), torch.full((24,), -1)]).to(torch.int32)
+    assert torch.equal(idx, want.expand(hk, -1))
+
+
+def test_graph_captured_decode_step(dev):
+    """A whole decode step -- append the new K/V row at the device-side length, route on the grown cache, sparse
+    decode -- captured once in a HIP graph and replayed with a growing length; every replay equals the same step run
+    eagerly (no memset nodes: the kernels clear their own histograms and counters)."""
+    print("case graph_decode", flush=True)
+    h, hk, d, cap, n0 = 32, 8, 128, 12000, 9000
+    front, window, routed = 64, 2048, 256
+    g = torch.Generator().manual_seed(11)
+    k0 = torch.randn(hk, cap, d, generator=g).to(torch.bfloat16).to(dev)
+    v0 = torch.randn(hk, cap, d, generator=g).to(torch.bfloat16).to(dev)
+    steps = [(torch.randn(h, d, generator=g).to(torch.bfloat16).to(dev),
+              torch.randn(hk, d, generator=g).to(torch.bfloat16).to(dev),
+              torch.randn(hk, d, generator=g).to(torch.bfloat16).to(dev)) for _ in range(4)]
+    scale = d ** -0.5
+
+    def step(k, v, length, q, kn, vn):
+        k.index_copy_(1, length, kn[:, None])
+        v.index_copy_(1, length, vn[:, None])
+        length.add_(1)
+        idx = bigger_bird_route(q, k, routed, front=front, window=window, scale=scale, n=length)
+        return bigger_bird_decode(q, k, v, idx, front=front, window=window, scale=scale, n=length), idx
+
+    # eager reference of the four steps
+    ke, ve, le = k0.clone(), v0.clone(), torch.tensor([n0], device=dev)
+    eager = [step(ke, ve, le, *s) for s in steps]
+    # graph: static inputs, captured once (after a warm-up on a side stream), replayed per step
+    kg, vg, lg = k0.clone(), v0.clone(), torch.tensor([n0], device=dev)
+    qs, ks_, vs_ = (torch.empty_like(t) for t in steps[0])
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        kw_, vw_, lw_ = kg.clone(), vg.clone(), lg.clone()
+        step(kw_, vw_, lw_, *steps[0])
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_g, idx_g = step(kg, vg, lg, qs, ks_, vs_)
+    for i, (q, kn, vn) in enumerate(steps):
+        qs.copy_(q)
+        ks_.copy_(kn)
+        vs_.copy_(vn)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert int(lg.item()) == n0 + i + 1
+        assert torch.equal(idx_g, eager[i][1]), i
+        assert torch.equal(out_g, eager[i][0]), i
+        _ = torch.zeros(1, device=dev).sum().item()  # unrelated eager work between replays

@@ -33,6 +33,12 @@ SIGNATURES = {
                          _vp, _i64, _vp, _sz, _vp]),
     "bb_decode_workspace": (_sz, [_i64, _i32, _i32, _i32]),
     "bb_rope_inplace": (_i32, [_vp, c_i64p, _i32, _i32, _i64, _i32, _vp, _vp, c_i64p, _vp]),
+    "bb_sparse_decode": (_i32, [_vp, _i64, _vp, c_i64p, _vp, c_i64p, _vp, c_i64p, _i32, _i32, _i64, _vp, _i64, _i32,
+                                _i32, _i32, _i32, _i32, _f32, _i32, _i32, _vp, _i64, _vp, _sz, _vp]),
+    "bb_sparse_decode_workspace": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32]),
+    "bb_decode_route": (_i32, [_vp, _i64, _vp, c_i64p, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32,
+                               _vp, _i32, _vp, _vp, _sz, _vp]),
+    "bb_decode_route_workspace": (_sz, [_i64, _i32, _i32, _i32, _i32]),
 }
 
 

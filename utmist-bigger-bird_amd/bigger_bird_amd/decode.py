@@ -1,0 +1,110 @@
+"""Decode-time operators for one new query token, HIP-backed: drop-ins for kernels/bigger_bird_decode.py (split-K
+sparse decode) and kernels/bigger_bird_route.py (fused decode routing).
+
+Same arguments, shapes and ValueError conditions as the reference. `n` may be a 1-element int64 tensor on the GPU
+holding the current cache length (keys at >= n are ignored), so a HIP graph captured once stays valid as the cache
+grows inside a fixed-capacity buffer; every other argument fixes the launch shapes. `block_n`, `num_warps` and
+`num_stages` are accepted for signature compatibility (the gfx950 kernels use fixed 64-key chunks).
+"""
+import torch
+
+from . import _lib
+
+
+def _len_arg(n, device):
+    """(host length or None, device pointer or None) for the C ABI."""
+    if n is None:
+        return None, None
+    if isinstance(n, torch.Tensor):
+        if not n.is_cuda or n.numel() != 1:
+            raise ValueError("n must be a 1-element int tensor on the GPU")
+        if n.dtype != torch.int64:
+            raise ValueError("n must be an int64 tensor (it is read in place by the kernels)")
+        return None, _lib.ptr(n)
+    return int(n), None
+
+
+def _rows16(x):
+    """head_dim contiguous with 16-byte aligned rows (a cache view qualifies); otherwise a contiguous copy."""
+    ok = x.stride(-1) == 1 and all(s % 8 == 0 for s in x.stride()[:-1]) and x.data_ptr() % 16 == 0
+    return x if ok else x.contiguous()
+
+
+def bigger_bird_decode(q, k, v, indices, *, front=64, window=4096, scale=1.0, n=None, splits=None, block_n=64,
+                       num_warps=4, num_stages=2):
+    """q [H, D] (one token), k / v [Hkv, N, D] (any strides, e.g. a cache view), indices int [Hkv or H, R].
+    `n`: current length as a 1-element GPU int64 tensor (graph safe); default all N keys. Returns [H, D] in q's dtype.
+    Attends each route group to front keys + the last `window` keys + its routed keys (positions outside [0, n) and
+    -1 entries are skipped)."""
+    if not q.is_cuda or q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("bigger_bird_decode requires CUDA FP16/BF16")
+    h, d = q.shape
+    hk, cap, _ = k.shape
+    if k.shape != v.shape or h % hk or k.shape[-1] != d:
+        raise ValueError("q [H,D] and k/v [Hkv,N,D] must match")
+    if n is None and cap < front + window:
+        raise ValueError("cache shorter than front + window: use dense attention")
+    if indices.ndim != 2 or indices.shape[0] not in (hk, h):
+        raise ValueError("indices must be [Hkv, R] (pooled) or [H, R] (per head)")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("q, k and v must share a dtype")
+    _lib.require_gpu(k, v, indices, n if isinstance(n, torch.Tensor) else None, what="bigger_bird_decode")
+    k, v = _rows16(k), _rows16(v)
+    q = q if q.stride(-1) == 1 else q.contiguous()
+    idx = indices.to(torch.int32)
+    rows, route_k = idx.shape
+    n_host, n_dev = _len_arg(n, q.device)
+    if n_host is None:
+        n_host = cap
+    out = torch.empty(h, d, dtype=q.dtype, device=q.device)
+    L = _lib.lib()
+    sp = int(splits or 0)
+    ws_bytes = L.bb_sparse_decode_workspace(h, hk, d, rows, front, window, route_k, sp)
+    ws = _lib.workspace(ws_bytes, q.device)
+    _lib.check(L.bb_sparse_decode(
+        _lib.ptr(q), q.stride(0), _lib.ptr(k), _lib.i64s(*k.stride()[:2]), _lib.ptr(v), _lib.i64s(*v.stride()[:2]),
+        _lib.ptr(idx) if route_k else None, _lib.i64s(*idx.stride()), rows, route_k, n_host, n_dev, cap, h, hk, d,
+        int(front), int(window), float(scale), sp, int(q.dtype == torch.float16), _lib.ptr(out), out.stride(0),
+        _lib.ptr(ws), ws_bytes, _lib.stream_of(q)))
+    return out
+
+
+def _route(q, k, k_route, front, window, scale, n, splits):
+    if not q.is_cuda or q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("bigger_bird_route requires CUDA FP16/BF16")
+    h, d = q.shape
+    hk, cap, _ = k.shape
+    if h % hk or k.shape[-1] != d:
+        raise ValueError("q [H,D] and k [Hkv,CAP,D] must match")
+    if k.dtype != q.dtype:
+        raise ValueError("q and k must share a dtype")
+    _lib.require_gpu(k, n if isinstance(n, torch.Tensor) else None, what="bigger_bird_route")
+    k = _rows16(k)
+    q = q if q.stride(-1) == 1 else q.contiguous()
+    n_host, n_dev = _len_arg(n, q.device)
+    if n_host is None:
+        n_host = cap
+    probs = torch.empty(hk, cap, dtype=torch.float32, device=q.device)
+    idx = torch.empty(hk, k_route, dtype=torch.int32, device=q.device) if k_route else None
+    L = _lib.lib()
+    sp = int(splits or 0)
+    ws_bytes = L.bb_decode_route_workspace(cap, h, hk, sp, k_route)
+    ws = _lib.workspace(ws_bytes, q.device)
+    _lib.check(L.bb_decode_route(
+        _lib.ptr(q), q.stride(0), _lib.ptr(k), _lib.i64s(*k.stride()[:2]), n_host, n_dev, cap, h, hk, d, int(front),
+        int(window), float(scale), sp, int(q.dtype == torch.float16), _lib.ptr(probs), int(k_route), _lib.ptr(idx),
+        _lib.ptr(ws), ws_bytes, _lib.stream_of(q)))
+    return probs, idx
+
+
+def pooled_probs(q, k, *, front=64, window=4096, scale=1.0, n=None, splits=None, block_n=64, num_warps=4):
+    """q [H, D], k [Hkv, CAP, D] -> [Hkv, CAP] fp32 pooled probabilities; -1 outside [front, n - window)."""
+    return _route(q, k, 0, front, window, scale, n, splits)[0]
+
+
+def bigger_bird_route(q, k, k_route, *, front=64, window=4096, scale=1.0, n=None, splits=None, **kw):
+    """Indices [Hkv, k_route] of the highest pooled-probability keys in [front, n - window): int32, ascending (the
+    reference returns them unsorted), ties to the lower index, -1 past the eligible count."""
+    if k_route <= 0:
+        raise ValueError("k_route must be positive")
+    return _route(q, k, int(k_route), front, window, scale, n, splits)[1]

@@ -1,6 +1,7 @@
 // C ABI of libbb_attn: argument validation (reference error texts), schedule selection, kernel launches.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -349,6 +350,119 @@ int bb_decode(const void* q, int64_t sq, const int8_t* k8, const void* ks, const
   p.part = static_cast<float*>(ws);
   (void)G;
   return hip_status(bb::launch_decode(p, static_cast<hipStream_t>(stream)), "bb_decode");
+}
+
+// Key chunks of the split-K decode kernels, as kernels/bigger_bird_decode.py:84-88 and bigger_bird_route.py:91-94
+// choose them (64-key blocks, about four workgroups per CU; `splits` > 0 requests a count).
+static int64_t decode_chunk_len(int64_t total, int programs, int splits, int64_t cap_splits) {
+  if (total <= 0) return 64;
+  int64_t s = splits > 0 ? splits : std::max<int64_t>(1, std::min<int64_t>(cdiv(total, 4 * 64), cdiv(4 * kCUs, programs)));
+  if (cap_splits > 0 && s > cap_splits) s = cap_splits;
+  return cdiv(cdiv(total, s), 64) * 64;
+}
+
+size_t bb_sparse_decode_workspace(int H, int Hkv, int D, int rows, int front, int window, int route_k, int splits) {
+  if (H <= 0 || Hkv <= 0 || rows <= 0 || D <= 0) return 0;
+  const int64_t total = (int64_t)front + window + route_k;
+  const int64_t len = decode_chunk_len(total, rows, splits, 0);
+  return (size_t)H * (size_t)cdiv(total > 0 ? total : 1, len) * (size_t)(D + 2) * sizeof(float);
+}
+
+int bb_sparse_decode(const void* q, int64_t sq, const void* k, const int64_t* sk, const void* v, const int64_t* sv,
+                     const int32_t* idx, const int64_t* si, int rows, int route_k, int64_t n, const int64_t* n_dev,
+                     int64_t cap, int H, int Hkv, int D, int front, int window, float scale, int splits, int is_f16,
+                     void* out, int64_t so, void* ws, size_t ws_bytes, void* stream) {
+  g_err[0] = 0;
+  if (!q || !k || !v || !sk || !sv || !out) return fail("q [H,D] and k/v [Hkv,N,D] must match");
+  if (H <= 0 || Hkv <= 0 || H % Hkv || cap <= 0) return fail("q [H,D] and k/v [Hkv,N,D] must match");
+  const int G = H / Hkv;
+  if (G != 1 && G != 2 && G != 4 && G != 8) return fail("decode: groups %d unsupported", G);
+  if (D != 64 && D != 128) return fail("decode: head_dim %d unsupported (64 or 128)", D);
+  if (rows != Hkv && rows != H) return fail("indices must be [Hkv, R] (pooled) or [H, R] (per head)");
+  if (route_k < 0 || (route_k > 0 && (!idx || !si))) return fail("indices must be [Hkv, R] (pooled) or [H, R] (per head)");
+  if (front < 0 || window < 0) return fail("front >= 0 and window >= 0 required");
+  if (!n_dev && cap < (int64_t)front + window) return fail("cache shorter than front + window: use dense attention");
+  if (!(scale > 0.0f)) return fail("scale must be positive");
+  if (!aligned(q, 2) || !aligned(k, 16) || !aligned(v, 16) || sk[0] % 8 || sk[1] % 8 || sv[0] % 8 || sv[1] % 8)
+    return fail("q/k/v need a contiguous head_dim and 16-byte aligned rows");
+  bb::SparseDecodeParams p;
+  memset(&p, 0, sizeof(p));
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.idx = idx;
+  p.n_dev = n_dev;
+  p.out = static_cast<uint16_t*>(out);
+  p.sq = sq; p.sk0 = sk[0]; p.sk1 = sk[1]; p.sv0 = sv[0]; p.sv1 = sv[1];
+  if (si) { p.si0 = si[0]; p.si1 = si[1]; }
+  p.so = so;
+  p.n = n_dev ? cap : (n < cap ? n : cap);
+  p.cap = cap;
+  p.H = H; p.Hkv = Hkv; p.G = G; p.D = D; p.rows = rows;
+  p.front = front; p.window = window; p.route_k = route_k; p.f16 = is_f16 ? 1 : 0;
+  const int64_t total = (int64_t)front + window + route_k;
+  p.split_len = decode_chunk_len(total, rows, splits, 0);
+  p.n_splits = (int)cdiv(total > 0 ? total : 1, p.split_len);
+  p.c = (float)((double)scale * 1.4426950408889634);
+  const size_t need = bb_sparse_decode_workspace(H, Hkv, D, rows, front, window, route_k, splits);
+  if (!ws || ws_bytes < need) return fail("workspace of %zu bytes required", need);
+  p.part = static_cast<float*>(ws);
+  return hip_status(bb::launch_sparse_decode(p, static_cast<hipStream_t>(stream)), "bb_sparse_decode");
+}
+
+static int64_t route_chunk_len(int64_t cap, int Hkv, int splits) { return decode_chunk_len(cap, Hkv, splits, 256); }
+
+size_t bb_decode_route_workspace(int64_t cap, int H, int Hkv, int splits, int k_route) {
+  if (cap <= 0 || H <= 0 || Hkv <= 0 || H % Hkv) return 0;
+  const int64_t ns = cdiv(cap, route_chunk_len(cap, Hkv, splits));
+  size_t b = align256((size_t)H * cap * 4) + 2 * align256((size_t)Hkv * ns * (H / Hkv) * 4);
+  if (k_route > 0) b += align256((size_t)Hkv * cap * 8) + align256(bb::topk_workspace_bytes(cap, Hkv));
+  return b;
+}
+
+int bb_decode_route(const void* q, int64_t sq, const void* k, const int64_t* sk, int64_t n, const int64_t* n_dev,
+                    int64_t cap, int H, int Hkv, int D, int front, int window, float scale, int splits, int is_f16,
+                    float* probs_out, int k_route, int32_t* idx_out, void* ws, size_t ws_bytes, void* stream) {
+  g_err[0] = 0;
+  if (!q || !k || !sk || !probs_out) return fail("q [H,D] and k [Hkv,CAP,D] must match");
+  if (H <= 0 || Hkv <= 0 || H % Hkv || cap <= 0) return fail("q [H,D] and k [Hkv,CAP,D] must match");
+  const int G = H / Hkv;
+  if (G != 1 && G != 2 && G != 4 && G != 8) return fail("decode routing: groups %d unsupported", G);
+  if (D != 64 && D != 128) return fail("decode routing: head_dim %d unsupported (64 or 128)", D);
+  if (front < 0 || window < 0) return fail("front >= 0 and window >= 0 required");
+  if (k_route < 0 || (k_route > 0 && !idx_out)) return fail("decode routing: k_route must be >= 0 with an output");
+  if (!(scale > 0.0f)) return fail("scale must be positive");
+  if (!aligned(q, 2) || !aligned(k, 16) || sk[0] % 8 || sk[1] % 8)
+    return fail("q/k need a contiguous head_dim and 16-byte aligned rows");
+  const size_t need = bb_decode_route_workspace(cap, H, Hkv, splits, k_route);
+  if (!ws || ws_bytes < need) return fail("workspace of %zu bytes required", need);
+  bb::DecodeRouteParams p;
+  memset(&p, 0, sizeof(p));
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.n_dev = n_dev;
+  p.sq = sq; p.sk0 = sk[0]; p.sk1 = sk[1];
+  p.n = n_dev ? cap : (n < cap ? n : cap);
+  p.cap = cap;
+  p.H = H; p.Hkv = Hkv; p.D = D; p.front = front; p.window = window; p.f16 = is_f16 ? 1 : 0;
+  p.split_len = route_chunk_len(cap, Hkv, splits);
+  p.n_splits = (int)cdiv(cap, p.split_len);
+  p.c = (float)((double)scale * 1.4426950408889634);
+  char* w = static_cast<char*>(ws);
+  p.scores = reinterpret_cast<float*>(w); w += align256((size_t)H * cap * 4);
+  p.stat_m = reinterpret_cast<float*>(w); w += align256((size_t)Hkv * p.n_splits * G * 4);
+  p.stat_l = reinterpret_cast<float*>(w); w += align256((size_t)Hkv * p.n_splits * G * 4);
+  p.probs = probs_out;
+  if (k_route > 0) {
+    p.keys = reinterpret_cast<uint64_t*>(w);
+    w += align256((size_t)Hkv * cap * 8);
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int rc = hip_status(bb::launch_decode_route_probs(p, st), "bb_decode_route");
+  if (rc != BB_OK || k_route == 0) return rc;
+  return hip_status(bb::launch_topk_rows(p.keys, Hkv, cap, p.n, n_dev, front, window, k_route, idx_out, w,
+                                         bb::topk_workspace_bytes(cap, Hkv), st),
+                    "bb_decode_route top-k");
 }
 
 int bb_rope_inplace(void* x, const int64_t* sx, int B, int Hh, int64_t T, int D, const void* cos, const void* sin,

@@ -1,0 +1,357 @@
+// Decode-time kernels for one new query token (gfx950):
+//   * split-K sparse decode (kernels/bigger_bird_decode.py of the reference): each route group attends the virtual
+//     key list front | window | routed keys of a bf16 / fp16 KV cache, cut into splits that write partial softmax
+//     states, and a merge kernel combines them;
+//   * fused decode routing (kernels/bigger_bird_route.py): per-chunk scores of all query heads of a KV head against
+//     every cached key with softmax statistics, then the pooled (mean over the group) probability per key with the
+//     front and window keys masked out. The top-k selection runs on the routes top-k kernels (bb_routes.hip).
+// The cache length may come from device memory (`n_dev`), so a captured HIP graph stays valid as the cache grows in a
+// fixed-capacity buffer; every grid is sized from host-side bounds that do not depend on it.
+#include "bb_common.h"
+#include "bb_internal.h"
+
+namespace bb {
+namespace {
+
+template <bool F16>
+BB_DEV float elem_to_f32(uint16_t h) {
+  if constexpr (F16) return (float)__builtin_bit_cast(_Float16, h);
+  else return bf16_to_f32(h);
+}
+template <bool F16>
+BB_DEV uint16_t f32_to_elem(float x) {
+  if constexpr (F16) return __builtin_bit_cast(uint16_t, (_Float16)x);
+  else return f32_to_bf16(x);
+}
+
+BB_DEV int64_t current_length(int64_t n, const int64_t* n_dev, int64_t cap) {
+  int64_t v = n_dev ? *n_dev : n;
+  if (v > cap) v = cap;
+  return v < 0 ? 0 : v;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Sparse split-K decode. Workgroup (split, route row r): 4 waves, 8 lanes per key (D / 8 values each), 32 key slots.
+// Route row r holds GR query heads (GR = groups for pooled routes [Hkv, R], 1 for per-head routes [H, R]) and reads
+// KV head (r GR) / groups. Virtual key j < front -> position j; j < front + window -> n - window + (j - front);
+// otherwise the routed index; positions outside [0, n) are skipped (kernels/bigger_bird_decode.py:38-47).
+constexpr int kSdThreads = 256;
+constexpr float kSdRescale = 8.0f;
+
+template <int D, int GR, bool F16>
+__global__ __launch_bounds__(kSdThreads) void sparse_decode_kernel(SparseDecodeParams p) {
+  constexpr int LPK = 8, DPL = D / LPK, KPW = 64 / LPK, SLOTS = kSdThreads / LPK;
+  __shared__ float part_m[SLOTS][GR];
+  __shared__ float part_l[SLOTS][GR];
+  __shared__ float part_o[SLOTS][GR][D];
+
+  const int split = blockIdx.x, r = blockIdx.y;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int kslot = lane / LPK, sub = lane % LPK;
+  const int slot = wave * KPW + kslot;
+  const int64_t n = current_length(p.n, p.n_dev, p.cap);
+  const int kv = (r * GR) / p.G;
+  const int64_t total = (int64_t)p.front + p.window + p.route_k;
+  const int64_t j_begin = (int64_t)split * p.split_len;
+  const int64_t j_end = j_begin + p.split_len < total ? j_begin + p.split_len : total;
+
+  float qv[GR][DPL];
+#pragma unroll
+  for (int h = 0; h < GR; ++h) {
+    const uint16_t* qr = p.q + (int64_t)(r * GR + h) * p.sq + DPL * sub;
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) qv[h][e] = elem_to_f32<F16>(qr[e]);
+  }
+  float m[GR], l[GR], acc[GR][DPL];
+#pragma unroll
+  for (int h = 0; h < GR; ++h) {
+    m[h] = -1.0e20f;
+    l[h] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) acc[h][e] = 0.0f;
+  }
+  const int32_t* irow = p.idx + (int64_t)r * p.si0;
+  for (int64_t j = j_begin + slot; j < j_end; j += SLOTS) {
+    int64_t pos;
+    if (j < p.front) pos = j;
+    else if (j < (int64_t)p.front + p.window) pos = n - p.window + (j - p.front);
+    else pos = irow[(j - p.front - p.window) * p.si1];
+    if (pos < 0 || pos >= n) continue;  // the 8 lanes of a key slot share j, so they skip together
+    const uint16_t* kr = p.k + (int64_t)kv * p.sk0 + pos * p.sk1 + DPL * sub;
+    const uint16_t* vr = p.v + (int64_t)kv * p.sv0 + pos * p.sv1 + DPL * sub;
+    float kf[DPL], vf[DPL];
+#pragma unroll
+    for (int e0 = 0; e0 < DPL; e0 += 8) {
+      const u32x4_t kw = ld16(kr + e0), vw = ld16(vr + e0);
+#pragma unroll
+      for (int e = 0; e < 8 && e0 + e < DPL; ++e) {
+        kf[e0 + e] = elem_to_f32<F16>((uint16_t)(kw[e >> 1] >> (16 * (e & 1))));
+        vf[e0 + e] = elem_to_f32<F16>((uint16_t)(vw[e >> 1] >> (16 * (e & 1))));
+      }
+    }
+    float s[GR];
+#pragma unroll
+    for (int h = 0; h < GR; ++h) {
+      float t = 0.0f;
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) t = fmaf(qv[h][e], kf[e], t);
+      s[h] = t;
+    }
+#pragma unroll
+    for (int off = 1; off < LPK; off <<= 1)
+#pragma unroll
+      for (int h = 0; h < GR; ++h) s[h] += __shfl_xor(s[h], off);
+#pragma unroll
+    for (int h = 0; h < GR; ++h) {
+      const float x = s[h] * p.c;
+      if (x > m[h] + kSdRescale) {
+        const float alpha = fast_exp2(m[h] - x);
+        m[h] = x;
+        l[h] *= alpha;
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) acc[h][e] *= alpha;
+      }
+      const float pr = fast_exp2(x - m[h]);
+      l[h] += pr;
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) acc[h][e] = fmaf(pr, vf[e], acc[h][e]);
+    }
+  }
+  // workgroup combine of the key slots' states, one partial (o, m, l) per query head and split
+  if (sub == 0) {
+#pragma unroll
+    for (int h = 0; h < GR; ++h) {
+      part_m[slot][h] = m[h];
+      part_l[slot][h] = l[h];
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < GR; ++h)
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) part_o[slot][h][DPL * sub + e] = acc[h][e];
+  __syncthreads();
+  for (int t = tid; t < GR * D; t += kSdThreads) {
+    const int h = t / D, d = t % D;
+    float M = -1.0e30f;
+    for (int s2 = 0; s2 < SLOTS; ++s2) M = fmaxf(M, part_m[s2][h]);
+    float L = 0.0f, O = 0.0f;
+    for (int s2 = 0; s2 < SLOTS; ++s2) {
+      const float w = fast_exp2(part_m[s2][h] - M);
+      L += w * part_l[s2][h];
+      O += w * part_o[s2][h][d];
+    }
+    float* dst = p.part + ((int64_t)(r * GR + h) * p.n_splits + split) * (D + 2);
+    dst[d] = O;
+    if (d == 0) {
+      dst[D] = M;
+      dst[D + 1] = L;
+    }
+  }
+}
+
+// Merge of the splits' partial states of one query head (kernels/bigger_bird_decode.py:104-107).
+constexpr int kSdMergeThreads = 256;
+template <int D, bool F16>
+__global__ __launch_bounds__(kSdMergeThreads) void sparse_merge_kernel(SparseDecodeParams p) {
+  constexpr int NG = kSdMergeThreads / D;
+  __shared__ float red_m[kSdMergeThreads], red_l[NG], red_o[NG][D];
+  const int h = blockIdx.x, t = threadIdx.x, d = t % D, grp = t / D;
+  const float* base = p.part + (int64_t)h * p.n_splits * (D + 2);
+  float M = -1.0e30f;
+  for (int s = t; s < p.n_splits; s += kSdMergeThreads) M = fmaxf(M, base[(int64_t)s * (D + 2) + D]);
+  red_m[t] = M;
+  __syncthreads();
+  for (int w = kSdMergeThreads / 2; w > 0; w >>= 1) {
+    if (t < w) red_m[t] = fmaxf(red_m[t], red_m[t + w]);
+    __syncthreads();
+  }
+  M = red_m[0];
+  float L = 0.0f, O = 0.0f;
+  for (int s = grp; s < p.n_splits; s += NG) {
+    const float* row = base + (int64_t)s * (D + 2);
+    const float w = fast_exp2(row[D] - M);
+    L += w * row[D + 1];
+    O += w * row[d];
+  }
+  red_o[grp][d] = O;
+  if (d == 0) red_l[grp] = L;
+  __syncthreads();
+  if (grp == 0) {
+    float lt = 0.0f, ot = 0.0f;
+#pragma unroll
+    for (int g2 = 0; g2 < NG; ++g2) {
+      lt += red_l[g2];
+      ot += red_o[g2][d];
+    }
+    p.out[(int64_t)h * p.so + d] = f32_to_elem<F16>(ot / fmaxf(lt, 1.0e-30f));
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Decode routing, pass 1 (kernels/bigger_bird_route.py:24-52): workgroup (split, KV head) scores its key range for
+// the G query heads (fp32, log2 units, to S [H, cap]) and keeps each head's running (max, sum) per key slot; the
+// slots combine into one (max, sum) per head and split.
+template <int D, int G, bool F16>
+__global__ __launch_bounds__(kSdThreads) void route_scores_kernel(DecodeRouteParams p) {
+  constexpr int LPK = 8, DPL = D / LPK, KPW = 64 / LPK, SLOTS = kSdThreads / LPK;
+  __shared__ float part_m[SLOTS][G];
+  __shared__ float part_l[SLOTS][G];
+  const int split = blockIdx.x, kv = blockIdx.y;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int kslot = lane / LPK, sub = lane % LPK;
+  const int slot = wave * KPW + kslot;
+  const int64_t n = current_length(p.n, p.n_dev, p.cap);
+  const int64_t j_begin = (int64_t)split * p.split_len;
+  const int64_t j_end = j_begin + p.split_len < n ? j_begin + p.split_len : n;
+  float qv[G][DPL];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    const uint16_t* qr = p.q + (int64_t)(kv * G + h) * p.sq + DPL * sub;
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) qv[h][e] = elem_to_f32<F16>(qr[e]);
+  }
+  float m[G], l[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    m[h] = -1.0e20f;
+    l[h] = 0.0f;
+  }
+  for (int64_t j = j_begin + slot; j < j_end; j += SLOTS) {
+    const uint16_t* kr = p.k + (int64_t)kv * p.sk0 + j * p.sk1 + DPL * sub;
+    float kf[DPL];
+#pragma unroll
+    for (int e0 = 0; e0 < DPL; e0 += 8) {
+      const u32x4_t kw = ld16(kr + e0);
+#pragma unroll
+      for (int e = 0; e < 8 && e0 + e < DPL; ++e) kf[e0 + e] = elem_to_f32<F16>((uint16_t)(kw[e >> 1] >> (16 * (e & 1))));
+    }
+    float s[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float t = 0.0f;
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) t = fmaf(qv[h][e], kf[e], t);
+      s[h] = t;
+    }
+#pragma unroll
+    for (int off = 1; off < LPK; off <<= 1)
+#pragma unroll
+      for (int h = 0; h < G; ++h) s[h] += __shfl_xor(s[h], off);
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float x = s[h] * p.c;
+      if (sub == h % LPK) p.scores[(int64_t)(kv * G + h) * p.cap + j] = x;
+      const float mn = fmaxf(m[h], x);
+      l[h] = l[h] * fast_exp2(m[h] - mn) + fast_exp2(x - mn);
+      m[h] = mn;
+    }
+  }
+  if (sub == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      part_m[slot][h] = m[h];
+      part_l[slot][h] = l[h];
+    }
+  }
+  __syncthreads();
+  if (tid < G) {
+    const int h = tid;
+    float M = -1.0e20f;
+    for (int s2 = 0; s2 < SLOTS; ++s2) M = fmaxf(M, part_m[s2][h]);
+    float L = 0.0f;
+    for (int s2 = 0; s2 < SLOTS; ++s2) L += part_l[s2][h] * fast_exp2(part_m[s2][h] - M);
+    const int64_t o = ((int64_t)kv * p.n_splits + split) * G + h;
+    p.stat_m[o] = M;
+    p.stat_l[o] = L;
+  }
+}
+
+// Decode routing, pass 2 (kernels/bigger_bird_route.py:55-80): merges each head's split statistics, then per key
+// p = mean over the group of 2^(s - M) / Z; keys outside [front, n - window) get -1. Optionally also writes the
+// order-preserving 64-bit keys (fp32 bits of p, 0 for masked keys) for the top-k kernels.
+constexpr int kRpKeys = 256;
+template <int G>
+__global__ __launch_bounds__(kRpKeys) void route_pool_kernel(DecodeRouteParams p) {
+  __shared__ float sm[G], sinv[G];
+  const int kv = blockIdx.y, tid = threadIdx.x;
+  const int64_t n = current_length(p.n, p.n_dev, p.cap);
+  if (tid < G) {
+    float M = -1.0e20f;
+    for (int s = 0; s < p.n_splits; ++s) M = fmaxf(M, p.stat_m[((int64_t)kv * p.n_splits + s) * G + tid]);
+    float L = 0.0f;
+    for (int s = 0; s < p.n_splits; ++s) {
+      const int64_t o = ((int64_t)kv * p.n_splits + s) * G + tid;
+      L += p.stat_l[o] * fast_exp2(p.stat_m[o] - M);
+    }
+    sm[tid] = M;
+    sinv[tid] = 1.0f / fmaxf(L, 1.0e-30f);
+  }
+  __syncthreads();
+  const int64_t j = (int64_t)blockIdx.x * kRpKeys + tid;
+  if (j >= p.cap) return;
+  float pr = -1.0f;
+  if (j >= p.front && j < n - p.window) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int h = 0; h < G; ++h) acc += fast_exp2(p.scores[(int64_t)(kv * G + h) * p.cap + j] - sm[h]) * sinv[h];
+    pr = acc / (float)G;
+  }
+  p.probs[(int64_t)kv * p.cap + j] = pr;
+  if (p.keys) p.keys[(int64_t)kv * p.cap + j] = pr > 0.0f ? (uint64_t)__float_as_uint(pr) : 0ull;
+}
+
+template <int D, int GR, bool F16>
+hipError_t launch_sparse_decode_t(const SparseDecodeParams& p, hipStream_t stream) {
+  hipLaunchKernelGGL((sparse_decode_kernel<D, GR, F16>), dim3(p.n_splits, p.rows), dim3(kSdThreads), 0, stream, p);
+  hipLaunchKernelGGL((sparse_merge_kernel<D, F16>), dim3(p.H), dim3(kSdMergeThreads), 0, stream, p);
+  return hipGetLastError();
+}
+
+template <int D, bool F16>
+hipError_t launch_sparse_decode_d(const SparseDecodeParams& p, hipStream_t stream) {
+  switch (p.rows == p.H ? 1 : p.G) {
+    case 1: return launch_sparse_decode_t<D, 1, F16>(p, stream);
+    case 2: return launch_sparse_decode_t<D, 2, F16>(p, stream);
+    case 4: return launch_sparse_decode_t<D, 4, F16>(p, stream);
+    case 8: return launch_sparse_decode_t<D, 8, F16>(p, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int D, int G, bool F16>
+hipError_t launch_route_t(const DecodeRouteParams& p, hipStream_t stream) {
+  hipLaunchKernelGGL((route_scores_kernel<D, G, F16>), dim3(p.n_splits, p.Hkv), dim3(kSdThreads), 0, stream, p);
+  hipLaunchKernelGGL(route_pool_kernel<G>, dim3((unsigned)((p.cap + kRpKeys - 1) / kRpKeys), p.Hkv), dim3(kRpKeys), 0,
+                     stream, p);
+  return hipGetLastError();
+}
+
+template <int D, bool F16>
+hipError_t launch_route_d(const DecodeRouteParams& p, hipStream_t stream) {
+  switch (p.H / p.Hkv) {
+    case 1: return launch_route_t<D, 1, F16>(p, stream);
+    case 2: return launch_route_t<D, 2, F16>(p, stream);
+    case 4: return launch_route_t<D, 4, F16>(p, stream);
+    case 8: return launch_route_t<D, 8, F16>(p, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+hipError_t launch_sparse_decode(const SparseDecodeParams& p, hipStream_t stream) {
+  if (p.n_splits <= 0 || p.rows <= 0) return hipErrorInvalidValue;
+  if (p.D == 64) return p.f16 ? launch_sparse_decode_d<64, true>(p, stream) : launch_sparse_decode_d<64, false>(p, stream);
+  if (p.D == 128)
+    return p.f16 ? launch_sparse_decode_d<128, true>(p, stream) : launch_sparse_decode_d<128, false>(p, stream);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_decode_route_probs(const DecodeRouteParams& p, hipStream_t stream) {
+  if (p.n_splits <= 0 || p.Hkv <= 0 || p.cap <= 0) return hipErrorInvalidValue;
+  if (p.D == 64) return p.f16 ? launch_route_d<64, true>(p, stream) : launch_route_d<64, false>(p, stream);
+  if (p.D == 128) return p.f16 ? launch_route_d<128, true>(p, stream) : launch_route_d<128, false>(p, stream);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace bb

@@ -44,8 +44,10 @@ struct RoutesParams {
   uint16_t* scores;     // [B*Hkv][G*r][n] bf16 workspace
   uint32_t* rowmax;     // [B*H*r] ordered-float keys
   uint64_t* rowsum;     // [B*H*r] fixed point 2^40
-  uint64_t* pooled;     // [B*H][n] fixed point 2^40
+  uint64_t* pooled;     // [B*H][pstride] fixed point 2^40
   int32_t* out_idx;     // [B*H][budget]
+  int64_t pstride;      // row stride of pooled (n for prefill routes)
+  const int64_t* n_dev; // top-k range length from device memory (decode routing), or null
 };
 
 size_t routes_workspace_bytes(int64_t n, int H, int Hkv, int B, int r);
@@ -76,6 +78,45 @@ struct DecodeParams {
 };
 size_t decode_workspace_bytes(int H, int D, int n_splits);
 hipError_t launch_decode(const DecodeParams& p, hipStream_t stream);
+
+// Split-K sparse decode over a bf16 / fp16 KV cache (front | window | routed keys per route row).
+struct SparseDecodeParams {
+  const uint16_t* q;     // [H, D] (row stride sq)
+  const uint16_t* k;     // [Hkv, cap, D] strided (sk0 head, sk1 token)
+  const uint16_t* v;
+  const int32_t* idx;    // [rows, route_k] strided (si0, si1), -1 = empty
+  const int64_t* n_dev;  // current length in device memory, or null (then n)
+  uint16_t* out;         // [H, D] (row stride so)
+  float* part;           // [H][n_splits][D + 2]
+  int64_t sq, sk0, sk1, sv0, sv1, si0, si1, so;
+  int64_t n, cap, split_len;
+  int H, Hkv, G, D, rows, front, window, route_k, n_splits, f16;
+  float c;               // scale * log2(e)
+};
+hipError_t launch_sparse_decode(const SparseDecodeParams& p, hipStream_t stream);
+
+// Decode routing: pooled probabilities over the cached keys for one query token.
+struct DecodeRouteParams {
+  const uint16_t* q;     // [H, D] (row stride sq)
+  const uint16_t* k;     // [Hkv, cap, D] strided
+  const int64_t* n_dev;
+  float* scores;         // [H, cap] workspace (log2 units)
+  float* stat_m;         // [Hkv][n_splits][G]
+  float* stat_l;
+  float* probs;          // [Hkv, cap] output
+  uint64_t* keys;        // [Hkv, cap] top-k keys, or null
+  int64_t sq, sk0, sk1;
+  int64_t n, cap, split_len;
+  int H, Hkv, D, front, window, n_splits, f16;
+  float c;
+};
+hipError_t launch_decode_route_probs(const DecodeRouteParams& p, hipStream_t stream);
+// Top-`budget` of 64-bit keys per row over [front, n - window) (n from n_dev when set), ascending int32 indices;
+// rows of `stride` keys; the workspace comes from topk_workspace_bytes.
+size_t topk_workspace_bytes(int64_t stride, int rows);
+hipError_t launch_topk_rows(const uint64_t* keys, int rows, int64_t stride, int64_t n, const int64_t* n_dev,
+                            int front, int window, int budget, int32_t* out, void* ws, size_t ws_bytes,
+                            hipStream_t stream);
 
 // RoPE in place (HF apply_rotary_pos_emb arithmetic in bf16).
 hipError_t launch_rope(uint16_t* x, int64_t sx0, int64_t sx1, int64_t sx2, int B, int Hh, int64_t T, int D,

@@ -22,6 +22,8 @@
 //                   the keys above it and of its candidates, exact choice among the candidates (value desc, index asc)
 //                   and ascending emission through a bitmap; an MSD radix select over the whole range when the
 //                   candidates overflow (heavy ties)
+#include <string.h>
+
 #include "bb_common.h"
 #include "bb_internal.h"
 
@@ -494,6 +496,18 @@ __global__ __launch_bounds__(256) void pooled_kernel(RoutesParams p, RouteGeom g
   p.pooled[(int64_t)head * p.n + j] = P;
 }
 
+// Eligible range [sink, n - window) of the top-k kernels; n comes from device memory when n_dev is set (decode
+// routing on a growing cache), clamped to the row stride.
+BB_DEV void top_range(const RoutesParams& p, int64_t& lo, int64_t& cnt) {
+  int64_t n = p.n_dev ? *p.n_dev : p.n;
+  if (n > p.pstride) n = p.pstride;
+  if (n < 0) n = 0;
+  lo = p.sink < n ? (p.sink > 0 ? p.sink : 0) : n;
+  int64_t hi = n - p.window;
+  if (hi > n) hi = n;
+  cnt = hi > lo ? hi - lo : 0;
+}
+
 // Top-budget selection for one head by one 1024-thread workgroup: MSD radix select over 8-bit digits of the whole
 // eligible range, then ordered compaction. The general path (any ties, any budget); topk_final_kernel uses it when
 // the candidate set of the fast path overflows.
@@ -508,12 +522,12 @@ __device__ __noinline__ void topk_radix_head(const RoutesParams& p, int head) {
   __shared__ int s_exact;
 
   const int tid = threadIdx.x;
-  const int64_t lo = p.sink < p.n ? (p.sink > 0 ? p.sink : 0) : p.n;
-  int64_t hi = p.n - p.window;
-  if (hi > p.n) hi = p.n;
-  const int64_t cnt = hi > lo ? hi - lo : 0;
-  const uint64_t* P = p.pooled + (int64_t)head * p.n + lo;
+  int64_t lo, cnt;
+  top_range(p, lo, cnt);
+  const uint64_t* P = p.pooled + (int64_t)head * p.pstride + lo;
   int32_t* out = p.out_idx + (int64_t)head * p.budget;
+  for (int i = tid; i < p.budget; i += kTopThreads) out[i] = -1;  // slots past the eligible count read -1
+  __syncthreads();
   if (p.budget <= 0 || cnt <= 0) return;
 
   // global max -> first digit
@@ -650,12 +664,6 @@ BB_DEV int top_bin(uint64_t v) {
   return 32 * (64 - lz) + (int)((v << lz) >> 58 & 31u);
 }
 
-BB_DEV void top_range(const RoutesParams& p, int64_t& lo, int64_t& cnt) {
-  lo = p.sink < p.n ? (p.sink > 0 ? p.sink : 0) : p.n;
-  int64_t hi = p.n - p.window;
-  if (hi > p.n) hi = p.n;
-  cnt = hi > lo ? hi - lo : 0;
-}
 
 __global__ __launch_bounds__(256) void topk_hist_kernel(RoutesParams p, TopWs w) {
   __shared__ uint32_t h[kTopBins];
@@ -664,7 +672,7 @@ __global__ __launch_bounds__(256) void topk_hist_kernel(RoutesParams p, TopWs w)
   top_range(p, lo, cnt);
   for (int b = tid; b < kTopBins; b += 256) h[b] = 0;
   __syncthreads();
-  const uint64_t* P = p.pooled + (int64_t)head * p.n + lo;
+  const uint64_t* P = p.pooled + (int64_t)head * p.pstride + lo;
   const int64_t t0 = (int64_t)blockIdx.x * kTopChunk;
   for (int e = tid; e < kTopChunk; e += 256)
     if (t0 + e < cnt) atomicAdd(&h[top_bin(P[t0 + e])], 1u);
@@ -715,7 +723,7 @@ __global__ __launch_bounds__(256) void topk_compact_kernel(RoutesParams p, TopWs
   const int head = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
   int64_t lo, cnt;
   top_range(p, lo, cnt);
-  const uint64_t* P = p.pooled + (int64_t)head * p.n + lo;
+  const uint64_t* P = p.pooled + (int64_t)head * p.pstride + lo;
   TopMeta* m = w.meta + head;
   const int bstar = m->bstar;
   const int64_t t0 = (int64_t)blockIdx.x * kTopChunk;
@@ -734,7 +742,7 @@ __global__ __launch_bounds__(256) void topk_compact_kernel(RoutesParams p, TopWs
     }
     base_s = __shfl(base_s, 0);
     base_c = __shfl(base_c, 0);
-    if (b > bstar) w.sel[(int64_t)head * p.n + base_s + below_s] = (int32_t)(lo + t);
+    if (b > bstar) w.sel[(int64_t)head * p.pstride + base_s + below_s] = (int32_t)(lo + t);
     if (b == bstar && base_c + below_c < (uint32_t)kTopCand) {
       w.candv[(int64_t)head * kTopCand + base_c + below_c] = v;
       w.candi[(int64_t)head * kTopCand + base_c + below_c] = (int32_t)(lo + t);
@@ -772,7 +780,7 @@ __global__ __launch_bounds__(kTopThreads) void topk_final_kernel(RoutesParams p,
     if (rank < m.need) atomicOr(&bits[(ix - lo) >> 5], 1u << ((ix - lo) & 31));
   }
   for (uint32_t i = tid; i < m.nsel; i += kTopThreads) {
-    const int32_t ix = w.sel[(int64_t)head * p.n + i];
+    const int32_t ix = w.sel[(int64_t)head * p.pstride + i];
     atomicOr(&bits[(ix - lo) >> 5], 1u << ((ix - lo) & 31));
   }
   __syncthreads();
@@ -800,6 +808,8 @@ __global__ __launch_bounds__(kTopThreads) void topk_final_kernel(RoutesParams p,
       ++pos;
     }
   }
+  // fewer chosen keys than the budget (a short eligible range): the remaining slots read -1
+  for (uint32_t i = scan[kTopThreads - 1] + tid; i < (uint32_t)p.budget; i += kTopThreads) out[i] = -1;
 }
 
 template <int D>
@@ -857,7 +867,45 @@ TopWs carve_top_ws(char* w, int64_t n, size_t heads) {
   return t;
 }
 
+// Clears the histograms and counters that the top-k kernels accumulate into (pooled_kernel does it for prefill).
+__global__ __launch_bounds__(256) void topk_clear_kernel(TopWs w) {
+  const int row = blockIdx.x;
+  for (int b = threadIdx.x; b < kTopBins; b += 256) w.hist[(int64_t)row * kTopBins + b] = 0u;
+  if (threadIdx.x == 0) w.meta[row] = TopMeta{};
+}
+
 }  // namespace
+
+size_t topk_workspace_bytes(int64_t stride, int rows) { return top_ws_bytes(stride, (size_t)rows); }
+
+hipError_t launch_topk_rows(const uint64_t* keys, int rows, int64_t stride, int64_t n, const int64_t* n_dev, int front,
+                            int window, int budget, int32_t* out, void* ws, size_t ws_bytes, hipStream_t stream) {
+  if (rows <= 0 || stride <= 0 || budget <= 0 || ws_bytes < topk_workspace_bytes(stride, rows))
+    return hipErrorInvalidValue;
+  RoutesParams p;
+  memset(&p, 0, sizeof(p));
+  p.pooled = const_cast<uint64_t*>(keys);
+  p.pstride = stride;
+  p.n = n < stride ? n : stride;
+  p.n_dev = n_dev;
+  p.sink = front;
+  p.window = window;
+  p.budget = budget;
+  p.out_idx = out;
+  const TopWs tw = carve_top_ws(static_cast<char*>(ws), stride, (size_t)rows);
+  // grids cover the largest range the device length can give: [front, stride)
+  const int64_t lo = front > 0 ? front : 0;
+  const int64_t cnt = stride > lo ? stride - lo : 0;
+  const unsigned chunks = (unsigned)((cnt + kTopChunk - 1) / kTopChunk);
+  hipLaunchKernelGGL(topk_clear_kernel, dim3(rows), dim3(256), 0, stream, tw);
+  if (chunks > 0) {
+    hipLaunchKernelGGL(topk_hist_kernel, dim3(chunks, rows), dim3(256), 0, stream, p, tw);
+    hipLaunchKernelGGL(topk_pick_kernel, dim3(rows), dim3(256), 0, stream, p, tw);
+    hipLaunchKernelGGL(topk_compact_kernel, dim3(chunks, rows), dim3(256), 0, stream, p, tw);
+  }
+  hipLaunchKernelGGL(topk_final_kernel, dim3(rows), dim3(kTopThreads), 0, stream, p, tw);
+  return hipGetLastError();
+}
 
 size_t routes_workspace_bytes(int64_t n, int H, int Hkv, int B, int r) {
   RouteGeom g = geom(n, H, Hkv, r);
@@ -878,6 +926,8 @@ hipError_t launch_routes(RoutesParams& p, void* ws, size_t ws_bytes, hipStream_t
   if (ws_bytes < routes_workspace_bytes(p.n, p.H, p.Hkv, p.B, p.r)) return hipErrorInvalidValue;
   RouteGeom g = geom(p.n, p.H, p.Hkv, p.r);
   const size_t nbkv = (size_t)p.B * p.Hkv;
+  p.pstride = p.n;
+  p.n_dev = nullptr;
   char* w = static_cast<char*>(ws);
   p.scores = reinterpret_cast<uint16_t*>(w); w += align256(nbkv * g.rows * (size_t)g.ns * 2);
   float* pmax = reinterpret_cast<float*>(w); w += align256(nbkv * g.n_kb1 * g.rows * 4);
