@@ -135,6 +135,25 @@ int bb_decode_route(const void* q, int64_t sq, const void* k, const int64_t* sk,
 size_t bb_decode_route_workspace(int64_t cap, int H, int Hkv, int splits, int k_route);
 
 /*
+ * Cache compaction for kv_evict: dst[h, i, :] = src[h, idx[h, i], :] for heads x m rows of D 16-bit elements
+ * (D % 8 == 0); src [heads, n_src, D] strides ss[2], dst strides sd[2] (head, row), idx int64 [heads, m] with row
+ * stride si0; an index outside [0, n_src) gives a zero row. Replaces the K/V gather of RDAttention.evict
+ * (modal_rd/attention.py:253-257).
+ */
+int bb_gather_rows(const void* src, const int64_t* ss, int64_t n_src, int heads, const int64_t* idx, int64_t si0, int m,
+                   int D, void* dst, const int64_t* sd, void* stream);
+
+/*
+ * Per row of vals [rows, n] fp32 (row stride sv0): the `budget` columns in [front, n - tail) with the largest
+ * values (values <= 0 and NaN rank last; ties to the lower index), ascending int32 in out [rows, budget], -1 past
+ * the eligible count. Replaces prio.topk(extra).indices.sort() of RDAttention.evict (modal_rd/attention.py:251-252).
+ */
+int bb_topk_f32(const float* vals, int64_t sv0, int rows, int64_t n, int front, int tail, int budget, int32_t* out,
+                void* ws, size_t ws_bytes, void* stream);
+
+size_t bb_topk_f32_workspace(int rows, int64_t n);
+
+/*
  * In-place RoPE on x [B, Hh, T, D] (strides sx[3]) with cos/sin [B, T, D] (strides sc[2]; 0 to broadcast), with
  * the arithmetic of HF apply_rotary_pos_emb on bf16 tensors (bit-identical). Replaces rope_inplace
  * (modal_rd/attention.py:51-60).

@@ -1,0 +1,79 @@
+"""kv_evict on the GPU (mirrors the reference's tests/test_kv_evict.py:26-64 with a tiny random-init Llama):
+prefill logits are unchanged by eviction, every layer's cache shrinks to sink + window + groups * vertical rows, the
+kept positions are sorted and unique with the sink, the window and every routed column of the layer's query heads,
+and the compacted cache equals the full cache gathered at the kept positions (torch's own gather). The two HIP
+helpers evict runs on (topk_columns, gather_rows) are also checked against torch.topk / torch.gather directly."""
+import pytest
+import torch
+
+from bigger_bird_amd import install
+from bigger_bird_amd.decode import gather_rows, topk_columns
+
+pytestmark = pytest.mark.gpu
+
+KW = dict(sink=8, window=96, vertical=24, n_route=16, exact_tail=24, block_m=16, block_n=16)
+N = 400
+
+
+def _tiny(dev):
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    cfg = LlamaConfig(vocab_size=512, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
+                      num_attention_heads=16, num_key_value_heads=4, max_position_embeddings=8192,
+                      attn_implementation="sdpa")
+    torch.manual_seed(0)
+    return LlamaForCausalLM(cfg).to(dev, torch.bfloat16).eval()
+
+
+def _prefill(model, ids):
+    from transformers import DynamicCache
+
+    cache = DynamicCache()
+    with torch.inference_mode():
+        logits = model(ids, past_key_values=cache, use_cache=True).logits
+    return logits, cache
+
+
+def test_prefill_unchanged_cache_shrinks_and_retained_set(dev):
+    print("case kv_evict_model", flush=True)
+    torch.manual_seed(4)
+    ids = torch.randint(0, 512, (1, N), device=dev)
+    model = _tiny(dev)
+    install(model, "rd", **KW)
+    want, full = _prefill(model, ids)
+    install(model, "rd", kv_evict=True, **KW)
+    got, cache = _prefill(model, ids)
+    assert torch.equal(got, want), "eviction must not change prefill output"
+    cfg = model.config
+    g = cfg.num_attention_heads // cfg.num_key_value_heads
+    d = cfg.hidden_size // cfg.num_attention_heads
+    m = KW["sink"] + KW["window"] + g * KW["vertical"]
+    for i, layer in enumerate(model.model.layers):
+        assert cache.layers[i].keys.shape == (1, cfg.num_key_value_heads, m, d)
+        assert full.layers[i].keys.shape[-2] == N
+        a = layer.self_attn
+        kept = a.kept
+        assert (kept[:, :-1] < kept[:, 1:]).all(), "positions sorted and unique"
+        assert (kept[:, :KW["sink"]] == torch.arange(KW["sink"], device=dev)).all()
+        assert (kept[:, -KW["window"]:] == torch.arange(N - KW["window"], N, device=dev)).all()
+        for h in range(cfg.num_attention_heads):  # every routed column survives
+            assert torch.isin(a.last_routes[h].long(), kept[h // g]).all()
+        gi = kept[None, :, :, None].expand(1, -1, -1, d)
+        assert torch.equal(cache.layers[i].keys, full.layers[i].keys.gather(2, gi))
+        assert torch.equal(cache.layers[i].values, full.layers[i].values.gather(2, gi))
+
+
+def test_helpers_match_torch(dev):
+    g = torch.Generator().manual_seed(3)
+    vals = torch.rand(6, 5000, generator=g).to(dev)  # distinct values: no ties
+    vals[2, 100:200] = 0.0                           # zeros rank last but are still selectable
+    front, tail, budget = 37, 900, 700
+    got = topk_columns(vals, budget, front=front, tail=tail)
+    for r in range(6):
+        seg = vals[r, front:5000 - tail]
+        want = (seg.topk(budget).indices + front).sort().values.to(torch.int32)
+        assert torch.equal(got[r], want), r
+    x = torch.randn(4, 3000, 128, generator=g).to(torch.bfloat16).to(dev)
+    idx = torch.randint(0, 3000, (4, 517), generator=g).to(dev)
+    out = gather_rows(x, idx)
+    assert torch.equal(out, x.gather(1, idx[:, :, None].expand(-1, -1, 128)))

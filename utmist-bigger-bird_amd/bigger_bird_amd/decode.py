@@ -108,3 +108,41 @@ def bigger_bird_route(q, k, k_route, *, front=64, window=4096, scale=1.0, n=None
     if k_route <= 0:
         raise ValueError("k_route must be positive")
     return _route(q, k, int(k_route), front, window, scale, n, splits)[1]
+
+
+def gather_rows(x, idx):
+    """x [heads, n, D] (16-bit dtype, any 16-byte aligned row strides), idx int [heads, m] -> [heads, m, D] with
+    out[h, i] = x[h, idx[h, i]] (a zero row for an index outside [0, n)): the cache compaction of kv_evict
+    (modal_rd/attention.py:253-257)."""
+    if not x.is_cuda or x.element_size() != 2:
+        raise ValueError("gather_rows needs a 16-bit GPU tensor")
+    heads, n, d = x.shape
+    if idx.ndim != 2 or idx.shape[0] != heads:
+        raise ValueError("idx must be [heads, m]")
+    x = _rows16(x)
+    ix = idx.to(torch.int64).contiguous()
+    out = torch.empty(heads, ix.shape[1], d, dtype=x.dtype, device=x.device)
+    _lib.check(_lib.lib().bb_gather_rows(_lib.ptr(x), _lib.i64s(*x.stride()[:2]), n, heads, _lib.ptr(ix), ix.stride(0),
+                                         ix.shape[1], d, _lib.ptr(out), _lib.i64s(*out.stride()[:2]),
+                                         _lib.stream_of(x)))
+    return out
+
+
+def topk_columns(vals, budget, *, front=0, tail=0):
+    """Per row of vals [rows, n] (fp32): the `budget` columns of [front, n - tail) with the largest values (values
+    <= 0 and NaN last, ties to the lower index), ascending int32 [rows, budget], -1 past the eligible count: the
+    prio.topk(extra).indices.sort() of kv_evict (modal_rd/attention.py:251-252)."""
+    if not vals.is_cuda:
+        raise ValueError("topk_columns runs on the GPU")
+    rows, n = vals.shape
+    out = torch.empty(rows, budget, dtype=torch.int32, device=vals.device)
+    if budget <= 0 or rows == 0:
+        return out
+    v = vals.to(torch.float32)
+    v = v if v.stride(-1) == 1 else v.contiguous()
+    L = _lib.lib()
+    ws_bytes = L.bb_topk_f32_workspace(rows, n)
+    ws = _lib.workspace(ws_bytes, vals.device)
+    _lib.check(L.bb_topk_f32(_lib.ptr(v), v.stride(0), rows, n, int(front), int(tail), int(budget), _lib.ptr(out),
+                             _lib.ptr(ws), ws_bytes, _lib.stream_of(v)))
+    return out

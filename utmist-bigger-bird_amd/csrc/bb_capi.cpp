@@ -465,6 +465,40 @@ int bb_decode_route(const void* q, int64_t sq, const void* k, const int64_t* sk,
                     "bb_decode_route top-k");
 }
 
+int bb_gather_rows(const void* src, const int64_t* ss, int64_t n_src, int heads, const int64_t* idx, int64_t si0, int m,
+                   int D, void* dst, const int64_t* sd, void* stream) {
+  g_err[0] = 0;
+  if (!src || !ss || !dst || !sd || (m > 0 && !idx)) return fail("gather: null argument");
+  if (heads < 0 || m < 0 || D <= 0 || D % 8) return fail("gather: rows must be whole 16-byte units");
+  if (!aligned(src, 16) || !aligned(dst, 16) || ss[0] % 8 || ss[1] % 8 || sd[0] % 8 || sd[1] % 8)
+    return fail("gather: rows must be 16-byte aligned");
+  return hip_status(bb::launch_gather_rows(static_cast<const uint16_t*>(src), ss[0], ss[1], n_src, heads, idx, si0, m, D,
+                                           static_cast<uint16_t*>(dst), sd[0], sd[1], static_cast<hipStream_t>(stream)),
+                    "bb_gather_rows");
+}
+
+size_t bb_topk_f32_workspace(int rows, int64_t n) {
+  if (rows <= 0 || n <= 0) return 0;
+  return align256((size_t)rows * n * 8) + align256(bb::topk_workspace_bytes(n, rows));
+}
+
+int bb_topk_f32(const float* vals, int64_t sv0, int rows, int64_t n, int front, int tail, int budget, int32_t* out,
+                void* ws, size_t ws_bytes, void* stream) {
+  g_err[0] = 0;
+  if (!vals || !out) return fail("topk: null argument");
+  if (rows <= 0 || n <= 0 || budget <= 0 || front < 0 || tail < 0) return fail("topk: empty selection");
+  const size_t need = bb_topk_f32_workspace(rows, n);
+  if (!ws || ws_bytes < need) return fail("workspace of %zu bytes required", need);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  uint64_t* keys = static_cast<uint64_t*>(ws);
+  int rc = hip_status(bb::launch_f32_keys(vals, sv0, rows, n, keys, st), "bb_topk_f32 keys");
+  if (rc != BB_OK) return rc;
+  char* w = static_cast<char*>(ws) + align256((size_t)rows * n * 8);
+  return hip_status(bb::launch_topk_rows(keys, rows, n, n, nullptr, front, tail, budget, out, w,
+                                         bb::topk_workspace_bytes(n, rows), st),
+                    "bb_topk_f32");
+}
+
 int bb_rope_inplace(void* x, const int64_t* sx, int B, int Hh, int64_t T, int D, const void* cos, const void* sin,
                     const int64_t* sc, void* stream) {
   g_err[0] = 0;

@@ -300,6 +300,32 @@ __global__ __launch_bounds__(kRpKeys) void route_pool_kernel(DecodeRouteParams p
   if (p.keys) p.keys[(int64_t)kv * p.cap + j] = pr > 0.0f ? (uint64_t)__float_as_uint(pr) : 0ull;
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// Cache compaction for kv_evict (modal_rd/attention.py:250-257): dst[h, i, :] = src[h, idx[h, i], :] for rows of
+// D 16-bit elements (16 bytes per thread), and the float priorities -> order-preserving 64-bit keys for the top-k.
+__global__ __launch_bounds__(256) void gather_rows_kernel(const uint16_t* __restrict__ src, int64_t ss0, int64_t ss1,
+                                                          int64_t n_src, const int64_t* __restrict__ idx, int64_t si0,
+                                                          int m, int D, uint16_t* __restrict__ dst, int64_t sd0,
+                                                          int64_t sd1) {
+  const int h = blockIdx.y, cpr = D / 8;
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= (int64_t)m * cpr) return;
+  const int i = (int)(e / cpr), c = (int)(e % cpr);
+  const int64_t row = idx[(int64_t)h * si0 + i];
+  const bool ok = row >= 0 && row < n_src;  // an index outside the source gives a zero row
+  st16(dst + (int64_t)h * sd0 + (int64_t)i * sd1 + 8 * c,
+       ok ? ld16(src + (int64_t)h * ss0 + row * ss1 + 8 * c) : u32x4_t{0, 0, 0, 0});
+}
+
+__global__ __launch_bounds__(256) void f32_keys_kernel(const float* __restrict__ vals, int64_t sv0, int64_t n,
+                                                       uint64_t* __restrict__ keys) {
+  const int r = blockIdx.y;
+  const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (j >= n) return;
+  const float x = vals[(int64_t)r * sv0 + j];
+  keys[(int64_t)r * n + j] = x > 0.0f ? (uint64_t)__float_as_uint(x) : 0ull;  // NaN and x <= 0 sort last
+}
+
 template <int D, int GR, bool F16>
 hipError_t launch_sparse_decode_t(const SparseDecodeParams& p, hipStream_t stream) {
   hipLaunchKernelGGL((sparse_decode_kernel<D, GR, F16>), dim3(p.n_splits, p.rows), dim3(kSdThreads), 0, stream, p);
@@ -345,6 +371,22 @@ hipError_t launch_sparse_decode(const SparseDecodeParams& p, hipStream_t stream)
   if (p.D == 128)
     return p.f16 ? launch_sparse_decode_d<128, true>(p, stream) : launch_sparse_decode_d<128, false>(p, stream);
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_gather_rows(const uint16_t* src, int64_t ss0, int64_t ss1, int64_t n_src, int heads,
+                              const int64_t* idx, int64_t si0, int m, int D, uint16_t* dst, int64_t sd0, int64_t sd1,
+                              hipStream_t stream) {
+  const int64_t work = (int64_t)m * (D / 8);
+  if (work <= 0 || heads <= 0) return hipSuccess;
+  hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)((work + 255) / 256), heads), dim3(256), 0, stream, src, ss0,
+                     ss1, n_src, idx, si0, m, D, dst, sd0, sd1);
+  return hipGetLastError();
+}
+
+hipError_t launch_f32_keys(const float* vals, int64_t sv0, int rows, int64_t n, uint64_t* keys, hipStream_t stream) {
+  if (rows <= 0 || n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(f32_keys_kernel, dim3((unsigned)((n + 255) / 256), rows), dim3(256), 0, stream, vals, sv0, n, keys);
+  return hipGetLastError();
 }
 
 hipError_t launch_decode_route_probs(const DecodeRouteParams& p, hipStream_t stream) {

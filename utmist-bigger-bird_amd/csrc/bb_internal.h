@@ -118,6 +118,12 @@ hipError_t launch_topk_rows(const uint64_t* keys, int rows, int64_t stride, int6
                             int front, int window, int budget, int32_t* out, void* ws, size_t ws_bytes,
                             hipStream_t stream);
 
+// Row gather (cache compaction) and float -> top-k key conversion.
+hipError_t launch_gather_rows(const uint16_t* src, int64_t ss0, int64_t ss1, int64_t n_src, int heads,
+                              const int64_t* idx, int64_t si0, int m, int D, uint16_t* dst, int64_t sd0, int64_t sd1,
+                              hipStream_t stream);
+hipError_t launch_f32_keys(const float* vals, int64_t sv0, int rows, int64_t n, uint64_t* keys, hipStream_t stream);
+
 // RoPE in place (HF apply_rotary_pos_emb arithmetic in bf16).
 hipError_t launch_rope(uint16_t* x, int64_t sx0, int64_t sx1, int64_t sx2, int B, int Hh, int64_t T, int D,
                        const uint16_t* cos, const uint16_t* sin, int64_t sc0, int64_t sc1, hipStream_t stream);
