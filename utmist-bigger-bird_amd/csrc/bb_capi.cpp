@@ -456,12 +456,13 @@ int bb_decode_route(const void* q, int64_t sq, const void* k, const int64_t* sk,
   if (k_route > 0) {
     p.keys = reinterpret_cast<uint64_t*>(w);
     w += align256((size_t)Hkv * cap * 8);
+    bb::topk_hist_meta(w, cap, Hkv, &p.top_hist, &p.top_meta);  // filled by the pool pass
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
   int rc = hip_status(bb::launch_decode_route_probs(p, st), "bb_decode_route");
   if (rc != BB_OK || k_route == 0) return rc;
   return hip_status(bb::launch_topk_rows(p.keys, Hkv, cap, p.n, n_dev, front, window, k_route, idx_out, w,
-                                         bb::topk_workspace_bytes(cap, Hkv), st),
+                                         bb::topk_workspace_bytes(cap, Hkv), bb::kTopFloatKeys | bb::kTopHistReady, st),
                     "bb_decode_route top-k");
 }
 
@@ -495,7 +496,7 @@ int bb_topk_f32(const float* vals, int64_t sv0, int rows, int64_t n, int front, 
   if (rc != BB_OK) return rc;
   char* w = static_cast<char*>(ws) + align256((size_t)rows * n * 8);
   return hip_status(bb::launch_topk_rows(keys, rows, n, n, nullptr, front, tail, budget, out, w,
-                                         bb::topk_workspace_bytes(n, rows), st),
+                                         bb::topk_workspace_bytes(n, rows), bb::kTopFloatKeys, st),
                     "bb_topk_f32");
 }
 

@@ -9,6 +9,7 @@
 // fixed-capacity buffer; every grid is sized from host-side bounds that do not depend on it.
 #include "bb_common.h"
 #include "bb_internal.h"
+#include "bb_topk.h"
 
 namespace bb {
 namespace {
@@ -24,6 +25,26 @@ BB_DEV uint16_t f32_to_elem(float x) {
   else return f32_to_bf16(x);
 }
 
+// fp32 c + a.x b.x + a.y b.y over packed 16-bit pairs (one v_dot2c_f32_{bf16,f16}).
+template <bool F16>
+BB_DEV float dot2(uint32_t a, uint32_t b, float c) {
+  typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 f16x2_t;
+  if constexpr (F16)
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b), c, false);
+  else return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// q row slice of one lane as packed pairs (DPL 16-bit values, DPL / 2 words).
+template <int DPL>
+BB_DEV void load_q_pairs(const uint16_t* qr, uint32_t (&qw)[DPL / 2]) {
+#pragma unroll
+  for (int e0 = 0; e0 < DPL / 8; ++e0) {
+    const u32x4_t w = ld16(qr + 8 * e0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qw[4 * e0 + i] = w[i];
+  }
+}
+
 BB_DEV int64_t current_length(int64_t n, const int64_t* n_dev, int64_t cap) {
   int64_t v = n_dev ? *n_dev : n;
   if (v > cap) v = cap;
@@ -31,19 +52,21 @@ BB_DEV int64_t current_length(int64_t n, const int64_t* n_dev, int64_t cap) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Sparse split-K decode. Workgroup (split, route row r): 4 waves, 8 lanes per key (D / 8 values each), 32 key slots.
-// Route row r holds GR query heads (GR = groups for pooled routes [Hkv, R], 1 for per-head routes [H, R]) and reads
-// KV head (r GR) / groups. Virtual key j < front -> position j; j < front + window -> n - window + (j - front);
-// otherwise the routed index; positions outside [0, n) are skipped (kernels/bigger_bird_decode.py:38-47).
+// Sparse split-K decode. Workgroup (split, route row r): 4 waves, 8 lanes per key (D / 8 values each), 32 key slots,
+// two keys per slot and step (their K and V rows in flight together). Route row r holds GR query heads (GR = groups
+// for pooled routes [Hkv, R], 1 for per-head routes [H, R]) and reads KV head (r GR) / groups. Virtual key
+// j < front -> position j; j < front + window -> n - window + (j - front); otherwise the routed index; positions
+// outside [0, n) are skipped (kernels/bigger_bird_decode.py:38-47). The key slots of a wave combine through lane
+// shuffles, the four waves through LDS.
 constexpr int kSdThreads = 256;
 constexpr float kSdRescale = 8.0f;
 
 template <int D, int GR, bool F16>
 __global__ __launch_bounds__(kSdThreads) void sparse_decode_kernel(SparseDecodeParams p) {
-  constexpr int LPK = 8, DPL = D / LPK, KPW = 64 / LPK, SLOTS = kSdThreads / LPK;
-  __shared__ float part_m[SLOTS][GR];
-  __shared__ float part_l[SLOTS][GR];
-  __shared__ float part_o[SLOTS][GR][D];
+  constexpr int LPK = 8, DPL = D / LPK, KPW = 64 / LPK, SLOTS = kSdThreads / LPK, NW = kSdThreads / 64;
+  __shared__ float part_m[NW][GR];
+  __shared__ float part_l[NW][GR];
+  __shared__ float part_o[NW][GR][D];
 
   const int split = blockIdx.x, r = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -55,13 +78,9 @@ __global__ __launch_bounds__(kSdThreads) void sparse_decode_kernel(SparseDecodeP
   const int64_t j_begin = (int64_t)split * p.split_len;
   const int64_t j_end = j_begin + p.split_len < total ? j_begin + p.split_len : total;
 
-  float qv[GR][DPL];
+  uint32_t qw[GR][DPL / 2];
 #pragma unroll
-  for (int h = 0; h < GR; ++h) {
-    const uint16_t* qr = p.q + (int64_t)(r * GR + h) * p.sq + DPL * sub;
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) qv[h][e] = elem_to_f32<F16>(qr[e]);
-  }
+  for (int h = 0; h < GR; ++h) load_q_pairs<DPL>(p.q + (int64_t)(r * GR + h) * p.sq + DPL * sub, qw[h]);
   float m[GR], l[GR], acc[GR][DPL];
 #pragma unroll
   for (int h = 0; h < GR; ++h) {
@@ -71,74 +90,98 @@ __global__ __launch_bounds__(kSdThreads) void sparse_decode_kernel(SparseDecodeP
     for (int e = 0; e < DPL; ++e) acc[h][e] = 0.0f;
   }
   const int32_t* irow = p.idx + (int64_t)r * p.si0;
-  for (int64_t j = j_begin + slot; j < j_end; j += SLOTS) {
-    int64_t pos;
-    if (j < p.front) pos = j;
-    else if (j < (int64_t)p.front + p.window) pos = n - p.window + (j - p.front);
-    else pos = irow[(j - p.front - p.window) * p.si1];
-    if (pos < 0 || pos >= n) continue;  // the 8 lanes of a key slot share j, so they skip together
-    const uint16_t* kr = p.k + (int64_t)kv * p.sk0 + pos * p.sk1 + DPL * sub;
-    const uint16_t* vr = p.v + (int64_t)kv * p.sv0 + pos * p.sv1 + DPL * sub;
-    float kf[DPL], vf[DPL];
+  const uint16_t* kbase = p.k + (int64_t)kv * p.sk0 + DPL * sub;
+  const uint16_t* vbase = p.v + (int64_t)kv * p.sv0 + DPL * sub;
+  for (int64_t j0 = j_begin + slot; j0 < j_end; j0 += 2 * SLOTS) {
+    int64_t pos[2];
+    bool ok[2];
 #pragma unroll
-    for (int e0 = 0; e0 < DPL; e0 += 8) {
-      const u32x4_t kw = ld16(kr + e0), vw = ld16(vr + e0);
+    for (int u = 0; u < 2; ++u) {
+      const int64_t j = j0 + u * SLOTS;
+      int64_t ps;
+      if (j < p.front) ps = j;
+      else if (j < (int64_t)p.front + p.window) ps = n - p.window + (j - p.front);
+      else ps = j < j_end ? irow[(j - p.front - p.window) * p.si1] : -1;
+      ok[u] = j < j_end && ps >= 0 && ps < n;  // the 8 lanes of a key slot agree
+      pos[u] = ok[u] ? ps : 0;
+    }
+    u32x4_t kw[2][DPL / 8], vw[2][DPL / 8];
 #pragma unroll
-      for (int e = 0; e < 8 && e0 + e < DPL; ++e) {
-        kf[e0 + e] = elem_to_f32<F16>((uint16_t)(kw[e >> 1] >> (16 * (e & 1))));
-        vf[e0 + e] = elem_to_f32<F16>((uint16_t)(vw[e >> 1] >> (16 * (e & 1))));
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int e0 = 0; e0 < DPL / 8; ++e0) {
+        kw[u][e0] = ld16(kbase + pos[u] * p.sk1 + 8 * e0);
+        vw[u][e0] = ld16(vbase + pos[u] * p.sv1 + 8 * e0);
+      }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      if (!ok[u]) continue;
+      float s[GR];
+#pragma unroll
+      for (int h = 0; h < GR; ++h) {
+        float t = 0.0f;
+#pragma unroll
+        for (int w = 0; w < DPL / 2; ++w) t = dot2<F16>(qw[h][w], kw[u][w >> 2][w & 3], t);
+        s[h] = t;
+      }
+#pragma unroll
+      for (int off = 1; off < LPK; off <<= 1)
+#pragma unroll
+        for (int h = 0; h < GR; ++h) s[h] += __shfl_xor(s[h], off);
+#pragma unroll
+      for (int h = 0; h < GR; ++h) {
+        const float x = s[h] * p.c;
+        if (x > m[h] + kSdRescale) {
+          const float alpha = fast_exp2(m[h] - x);
+          m[h] = x;
+          l[h] *= alpha;
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) acc[h][e] *= alpha;
+        }
+        const float pr = fast_exp2(x - m[h]);
+        l[h] += pr;
+#pragma unroll
+        for (int e = 0; e < DPL; ++e)
+          acc[h][e] = fmaf(pr, elem_to_f32<F16>((uint16_t)(vw[u][e >> 3][(e & 7) >> 1] >> (16 * (e & 1)))), acc[h][e]);
       }
     }
-    float s[GR];
+  }
+  // combine the 8 key slots of the wave (lane bits 3..5), then the waves through LDS
+#pragma unroll
+  for (int off = LPK; off < 64; off <<= 1)
 #pragma unroll
     for (int h = 0; h < GR; ++h) {
-      float t = 0.0f;
+      const float mo = __shfl_xor(m[h], off), lo = __shfl_xor(l[h], off);
+      const float mn = fmaxf(m[h], mo);
+      const float a = fast_exp2(m[h] - mn), b = fast_exp2(mo - mn);
+      m[h] = mn;
+      l[h] = l[h] * a + lo * b;
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) t = fmaf(qv[h][e], kf[e], t);
-      s[h] = t;
+      for (int e = 0; e < DPL; ++e) acc[h][e] = acc[h][e] * a + __shfl_xor(acc[h][e], off) * b;
     }
-#pragma unroll
-    for (int off = 1; off < LPK; off <<= 1)
-#pragma unroll
-      for (int h = 0; h < GR; ++h) s[h] += __shfl_xor(s[h], off);
+  if (kslot == 0) {
 #pragma unroll
     for (int h = 0; h < GR; ++h) {
-      const float x = s[h] * p.c;
-      if (x > m[h] + kSdRescale) {
-        const float alpha = fast_exp2(m[h] - x);
-        m[h] = x;
-        l[h] *= alpha;
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) acc[h][e] *= alpha;
+      if (sub == 0) {
+        part_m[wave][h] = m[h];
+        part_l[wave][h] = l[h];
       }
-      const float pr = fast_exp2(x - m[h]);
-      l[h] += pr;
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) acc[h][e] = fmaf(pr, vf[e], acc[h][e]);
+      for (int e = 0; e < DPL; ++e) part_o[wave][h][DPL * sub + e] = acc[h][e];
     }
   }
-  // workgroup combine of the key slots' states, one partial (o, m, l) per query head and split
-  if (sub == 0) {
-#pragma unroll
-    for (int h = 0; h < GR; ++h) {
-      part_m[slot][h] = m[h];
-      part_l[slot][h] = l[h];
-    }
-  }
-#pragma unroll
-  for (int h = 0; h < GR; ++h)
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) part_o[slot][h][DPL * sub + e] = acc[h][e];
   __syncthreads();
   for (int t = tid; t < GR * D; t += kSdThreads) {
     const int h = t / D, d = t % D;
     float M = -1.0e30f;
-    for (int s2 = 0; s2 < SLOTS; ++s2) M = fmaxf(M, part_m[s2][h]);
+#pragma unroll
+    for (int w2 = 0; w2 < NW; ++w2) M = fmaxf(M, part_m[w2][h]);
     float L = 0.0f, O = 0.0f;
-    for (int s2 = 0; s2 < SLOTS; ++s2) {
-      const float w = fast_exp2(part_m[s2][h] - M);
-      L += w * part_l[s2][h];
-      O += w * part_o[s2][h][d];
+#pragma unroll
+    for (int w2 = 0; w2 < NW; ++w2) {
+      const float w = fast_exp2(part_m[w2][h] - M);
+      L += w * part_l[w2][h];
+      O += w * part_o[w2][h][d];
     }
     float* dst = p.part + ((int64_t)(r * GR + h) * p.n_splits + split) * (D + 2);
     dst[d] = O;
@@ -167,11 +210,23 @@ __global__ __launch_bounds__(kSdMergeThreads) void sparse_merge_kernel(SparseDec
   }
   M = red_m[0];
   float L = 0.0f, O = 0.0f;
-  for (int s = grp; s < p.n_splits; s += NG) {
-    const float* row = base + (int64_t)s * (D + 2);
-    const float w = fast_exp2(row[D] - M);
-    L += w * row[D + 1];
-    O += w * row[d];
+  constexpr int U = 8;  // splits per step: their loads are in flight together
+  for (int s0 = grp; s0 < p.n_splits; s0 += U * NG) {
+    float mv[U], lv[U], ov[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int s = s0 + u * NG;
+      const float* row = base + (int64_t)(s < p.n_splits ? s : 0) * (D + 2);
+      mv[u] = s < p.n_splits ? row[D] : -1.0e30f;
+      lv[u] = row[D + 1];
+      ov[u] = row[d];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float w = s0 + u * NG < p.n_splits ? fast_exp2(mv[u] - M) : 0.0f;
+      L += w * lv[u];
+      O += w * ov[u];
+    }
   }
   red_o[grp][d] = O;
   if (d == 0) red_l[grp] = L;
@@ -190,7 +245,9 @@ __global__ __launch_bounds__(kSdMergeThreads) void sparse_merge_kernel(SparseDec
 // ---------------------------------------------------------------------------------------------------------------
 // Decode routing, pass 1 (kernels/bigger_bird_route.py:24-52): workgroup (split, KV head) scores its key range for
 // the G query heads (fp32, log2 units, to S [H, cap]) and keeps each head's running (max, sum) per key slot; the
-// slots combine into one (max, sum) per head and split.
+// slots combine into one (max, sum) per head and split. Each key slot takes four keys per step (all rows in flight).
+// Split 0 also clears the KV head's top-k histogram and counters, which the pool pass fills.
+constexpr int kRsKeysPerSlot = 4;
 template <int D, int G, bool F16>
 __global__ __launch_bounds__(kSdThreads) void route_scores_kernel(DecodeRouteParams p) {
   constexpr int LPK = 8, DPL = D / LPK, KPW = 64 / LPK, SLOTS = kSdThreads / LPK;
@@ -200,50 +257,56 @@ __global__ __launch_bounds__(kSdThreads) void route_scores_kernel(DecodeRoutePar
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int kslot = lane / LPK, sub = lane % LPK;
   const int slot = wave * KPW + kslot;
+  if (p.top_hist && split == 0) {
+    for (int b = tid; b < kTopBins; b += kSdThreads) p.top_hist[(int64_t)kv * kTopBins + b] = 0u;
+    if (tid < kTopMetaWords) p.top_meta[(int64_t)kv * kTopMetaWords + tid] = 0u;
+  }
   const int64_t n = current_length(p.n, p.n_dev, p.cap);
   const int64_t j_begin = (int64_t)split * p.split_len;
   const int64_t j_end = j_begin + p.split_len < n ? j_begin + p.split_len : n;
-  float qv[G][DPL];
+  uint32_t qw[G][DPL / 2];
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-    const uint16_t* qr = p.q + (int64_t)(kv * G + h) * p.sq + DPL * sub;
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) qv[h][e] = elem_to_f32<F16>(qr[e]);
-  }
+  for (int h = 0; h < G; ++h) load_q_pairs<DPL>(p.q + (int64_t)(kv * G + h) * p.sq + DPL * sub, qw[h]);
   float m[G], l[G];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
     m[h] = -1.0e20f;
     l[h] = 0.0f;
   }
-  for (int64_t j = j_begin + slot; j < j_end; j += SLOTS) {
-    const uint16_t* kr = p.k + (int64_t)kv * p.sk0 + j * p.sk1 + DPL * sub;
-    float kf[DPL];
+  constexpr int U = kRsKeysPerSlot;
+  const uint16_t* kbase = p.k + (int64_t)kv * p.sk0 + DPL * sub;
+  for (int64_t j0 = j_begin + slot; j0 < j_end; j0 += U * SLOTS) {
+    u32x4_t kw[U][DPL / 8];
 #pragma unroll
-    for (int e0 = 0; e0 < DPL; e0 += 8) {
-      const u32x4_t kw = ld16(kr + e0);
+    for (int u = 0; u < U; ++u) {
+      const int64_t j = j0 + u * SLOTS;
 #pragma unroll
-      for (int e = 0; e < 8 && e0 + e < DPL; ++e) kf[e0 + e] = elem_to_f32<F16>((uint16_t)(kw[e >> 1] >> (16 * (e & 1))));
-    }
-    float s[G];
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      float t = 0.0f;
-#pragma unroll
-      for (int e = 0; e < DPL; ++e) t = fmaf(qv[h][e], kf[e], t);
-      s[h] = t;
+      for (int e0 = 0; e0 < DPL / 8; ++e0) kw[u][e0] = ld16(kbase + (j < j_end ? j : j0) * p.sk1 + 8 * e0);
     }
 #pragma unroll
-    for (int off = 1; off < LPK; off <<= 1)
+    for (int u = 0; u < U; ++u) {
+      const int64_t j = j0 + u * SLOTS;
+      if (j >= j_end) break;  // the 8 lanes of a key slot agree
+      float sc[G];
 #pragma unroll
-      for (int h = 0; h < G; ++h) s[h] += __shfl_xor(s[h], off);
+      for (int h = 0; h < G; ++h) {
+        float t = 0.0f;
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      const float x = s[h] * p.c;
-      if (sub == h % LPK) p.scores[(int64_t)(kv * G + h) * p.cap + j] = x;
-      const float mn = fmaxf(m[h], x);
-      l[h] = l[h] * fast_exp2(m[h] - mn) + fast_exp2(x - mn);
-      m[h] = mn;
+        for (int w = 0; w < DPL / 2; ++w) t = dot2<F16>(qw[h][w], kw[u][w >> 2][w & 3], t);
+        sc[h] = t;
+      }
+#pragma unroll
+      for (int off = 1; off < LPK; off <<= 1)
+#pragma unroll
+        for (int h = 0; h < G; ++h) sc[h] += __shfl_xor(sc[h], off);
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const float x = sc[h] * p.c;
+        if (sub == h % LPK) p.scores[(int64_t)(kv * G + h) * p.cap + j] = x;
+        const float mn = fmaxf(m[h], x);
+        l[h] = l[h] * fast_exp2(m[h] - mn) + fast_exp2(x - mn);
+        m[h] = mn;
+      }
     }
   }
   if (sub == 0) {
@@ -266,38 +329,75 @@ __global__ __launch_bounds__(kSdThreads) void route_scores_kernel(DecodeRoutePar
   }
 }
 
-// Decode routing, pass 2 (kernels/bigger_bird_route.py:55-80): merges each head's split statistics, then per key
-// p = mean over the group of 2^(s - M) / Z; keys outside [front, n - window) get -1. Optionally also writes the
-// order-preserving 64-bit keys (fp32 bits of p, 0 for masked keys) for the top-k kernels.
-constexpr int kRpKeys = 256;
+BB_DEV float wave_max(float v) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) v = fmaxf(v, __shfl_xor(v, off));
+  return v;
+}
+BB_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+// Decode routing, pass 2 (kernels/bigger_bird_route.py:55-80): merges each head's split statistics (one wave per
+// head, lanes over the splits), then per key p = mean over the group of 2^(s - M) / Z; keys outside
+// [front, n - window) get -1. With top-k keys it also writes the order-preserving 64-bit keys (fp32 bits of p) and
+// adds the eligible keys to the KV head's top-k histogram (LDS counts, then one atomic per non-empty bin).
+constexpr int kRpThreads = 256, kRpPer = 4, kRpKeys = kRpThreads * kRpPer;
 template <int G>
-__global__ __launch_bounds__(kRpKeys) void route_pool_kernel(DecodeRouteParams p) {
+__global__ __launch_bounds__(kRpThreads) void route_pool_kernel(DecodeRouteParams p) {
   __shared__ float sm[G], sinv[G];
-  const int kv = blockIdx.y, tid = threadIdx.x;
+  __shared__ uint32_t hist[kTopBins];
+  const int kv = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t n = current_length(p.n, p.n_dev, p.cap);
-  if (tid < G) {
+  const bool top = p.keys && p.top_hist;
+  if (top)
+    for (int b = tid; b < kTopBins; b += kRpThreads) hist[b] = 0u;
+  for (int h = wave; h < G; h += kRpThreads / 64) {
+    const float* pm = p.stat_m + (int64_t)kv * p.n_splits * G + h;
+    const float* pl = p.stat_l + (int64_t)kv * p.n_splits * G + h;
     float M = -1.0e20f;
-    for (int s = 0; s < p.n_splits; ++s) M = fmaxf(M, p.stat_m[((int64_t)kv * p.n_splits + s) * G + tid]);
+    for (int s = lane; s < p.n_splits; s += 64) M = fmaxf(M, pm[(int64_t)s * G]);
+    M = wave_max(M);
     float L = 0.0f;
-    for (int s = 0; s < p.n_splits; ++s) {
-      const int64_t o = ((int64_t)kv * p.n_splits + s) * G + tid;
-      L += p.stat_l[o] * fast_exp2(p.stat_m[o] - M);
+    for (int s = lane; s < p.n_splits; s += 64) L += pl[(int64_t)s * G] * fast_exp2(pm[(int64_t)s * G] - M);
+    L = wave_sum(L);
+    if (lane == 0) {
+      sm[h] = M;
+      sinv[h] = 1.0f / fmaxf(L, 1.0e-30f);
     }
-    sm[tid] = M;
-    sinv[tid] = 1.0f / fmaxf(L, 1.0e-30f);
   }
   __syncthreads();
-  const int64_t j = (int64_t)blockIdx.x * kRpKeys + tid;
-  if (j >= p.cap) return;
-  float pr = -1.0f;
-  if (j >= p.front && j < n - p.window) {
-    float acc = 0.0f;
+  const int64_t hi = n - p.window;
 #pragma unroll
-    for (int h = 0; h < G; ++h) acc += fast_exp2(p.scores[(int64_t)(kv * G + h) * p.cap + j] - sm[h]) * sinv[h];
-    pr = acc / (float)G;
+  for (int u = 0; u < kRpPer; ++u) {
+    const int64_t j = (int64_t)blockIdx.x * kRpKeys + u * kRpThreads + tid;
+    if (j < p.cap) {
+      const bool eligible = j >= p.front && j < hi;
+      float pr = -1.0f;
+      if (eligible) {
+        float sc[G];
+#pragma unroll
+        for (int h = 0; h < G; ++h) sc[h] = p.scores[(int64_t)(kv * G + h) * p.cap + j];
+        float acc = 0.0f;
+#pragma unroll
+        for (int h = 0; h < G; ++h) acc += fast_exp2(sc[h] - sm[h]) * sinv[h];
+        pr = acc / (float)G;
+      }
+      p.probs[(int64_t)kv * p.cap + j] = pr;
+      if (p.keys) {
+        const uint64_t key = float_key(pr);
+        p.keys[(int64_t)kv * p.cap + j] = key;
+        if (top && eligible) atomicAdd(&hist[top_bin(key, true)], 1u);
+      }
+    }
   }
-  p.probs[(int64_t)kv * p.cap + j] = pr;
-  if (p.keys) p.keys[(int64_t)kv * p.cap + j] = pr > 0.0f ? (uint64_t)__float_as_uint(pr) : 0ull;
+  if (top) {
+    __syncthreads();
+    for (int b = tid; b < kTopBins; b += kRpThreads)
+      if (hist[b]) atomicAdd(&p.top_hist[(int64_t)kv * kTopBins + b], hist[b]);
+  }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -323,7 +423,7 @@ __global__ __launch_bounds__(256) void f32_keys_kernel(const float* __restrict__
   const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (j >= n) return;
   const float x = vals[(int64_t)r * sv0 + j];
-  keys[(int64_t)r * n + j] = x > 0.0f ? (uint64_t)__float_as_uint(x) : 0ull;  // NaN and x <= 0 sort last
+  keys[(int64_t)r * n + j] = float_key(x);  // NaN and x <= 0 sort last
 }
 
 template <int D, int GR, bool F16>
@@ -347,8 +447,8 @@ hipError_t launch_sparse_decode_d(const SparseDecodeParams& p, hipStream_t strea
 template <int D, int G, bool F16>
 hipError_t launch_route_t(const DecodeRouteParams& p, hipStream_t stream) {
   hipLaunchKernelGGL((route_scores_kernel<D, G, F16>), dim3(p.n_splits, p.Hkv), dim3(kSdThreads), 0, stream, p);
-  hipLaunchKernelGGL(route_pool_kernel<G>, dim3((unsigned)((p.cap + kRpKeys - 1) / kRpKeys), p.Hkv), dim3(kRpKeys), 0,
-                     stream, p);
+  hipLaunchKernelGGL(route_pool_kernel<G>, dim3((unsigned)((p.cap + kRpKeys - 1) / kRpKeys), p.Hkv), dim3(kRpThreads),
+                     0, stream, p);
   return hipGetLastError();
 }
 

@@ -48,6 +48,7 @@ struct RoutesParams {
   int32_t* out_idx;     // [B*H][budget]
   int64_t pstride;      // row stride of pooled (n for prefill routes)
   const int64_t* n_dev; // top-k range length from device memory (decode routing), or null
+  int float_keys;       // top-k keys are fp32 bits of positive values (binned by value, not by bit length)
 };
 
 size_t routes_workspace_bytes(int64_t n, int H, int Hkv, int B, int r);
@@ -105,6 +106,8 @@ struct DecodeRouteParams {
   float* stat_l;
   float* probs;          // [Hkv, cap] output
   uint64_t* keys;        // [Hkv, cap] top-k keys, or null
+  uint32_t* top_hist;    // [Hkv][top-k bins] histogram filled while the keys are written (with keys), or null
+  uint32_t* top_meta;    // [Hkv][8] top-k counters, cleared by the scores pass when top_hist is set
   int64_t sq, sk0, sk1;
   int64_t n, cap, split_len;
   int H, Hkv, D, front, window, n_splits, f16;
@@ -112,10 +115,14 @@ struct DecodeRouteParams {
 };
 hipError_t launch_decode_route_probs(const DecodeRouteParams& p, hipStream_t stream);
 // Top-`budget` of 64-bit keys per row over [front, n - window) (n from n_dev when set), ascending int32 indices;
-// rows of `stride` keys; the workspace comes from topk_workspace_bytes.
+// rows of `stride` keys; the workspace comes from topk_workspace_bytes. Flags: kTopFloatKeys when the keys are fp32
+// bits of positive values (0 for the rest), kTopHistReady when the histogram and counters in the workspace
+// (topk_hist_meta) were already filled and cleared by the producer of the keys.
+constexpr int kTopFloatKeys = 1, kTopHistReady = 2;
 size_t topk_workspace_bytes(int64_t stride, int rows);
+void topk_hist_meta(void* ws, int64_t stride, int rows, uint32_t** hist, uint32_t** meta);
 hipError_t launch_topk_rows(const uint64_t* keys, int rows, int64_t stride, int64_t n, const int64_t* n_dev,
-                            int front, int window, int budget, int32_t* out, void* ws, size_t ws_bytes,
+                            int front, int window, int budget, int32_t* out, void* ws, size_t ws_bytes, int flags,
                             hipStream_t stream);
 
 // Row gather (cache compaction) and float -> top-k key conversion.

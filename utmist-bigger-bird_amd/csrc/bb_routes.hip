@@ -26,6 +26,7 @@
 
 #include "bb_common.h"
 #include "bb_internal.h"
+#include "bb_topk.h"
 
 // Every rounding step above is part of the contract: no fused multiply-add contraction in this file.
 #pragma clang fp contract(off)
@@ -37,7 +38,6 @@ constexpr int kScoreKeys = 32;    // keys per scores_kernel block (8 key groups 
 constexpr int kScoreIters = 8;    // key blocks per scores_kernel workgroup
 constexpr int kSumKeys = 1024;    // keys per rowsum_kernel workgroup
 constexpr int kPoolKeys = 256;    // keys per pooled_kernel workgroup
-constexpr int kTopBinsPool = 2080;  // top-k histogram bins (kTopBins), cleared by pooled_kernel
 constexpr int kMaxRows = 256;     // G * r handled by one scores workgroup (rows beyond this use more row blocks)
 constexpr float kFixOne = 1099511627776.0f;  // 2^40
 
@@ -457,8 +457,8 @@ __global__ __launch_bounds__(256) void pooled_kernel(RoutesParams p, RouteGeom g
   const int64_t j = (int64_t)blockIdx.x * kPoolKeys + threadIdx.x;
   const int head = blockIdx.y;  // over B * H
   if (blockIdx.x == 0) {  // clear this head's top-k histogram and list counters (the next kernels accumulate)
-    for (int b = threadIdx.x; b < kTopBinsPool; b += kPoolKeys) top_hist[(int64_t)head * kTopBinsPool + b] = 0u;
-    if (threadIdx.x < 8) top_meta[8 * head + threadIdx.x] = 0u;
+    for (int b = threadIdx.x; b < kTopBins; b += kPoolKeys) top_hist[(int64_t)head * kTopBins + b] = 0u;
+    if (threadIdx.x < kTopMetaWords) top_meta[kTopMetaWords * head + threadIdx.x] = 0u;
   }
   if (j >= p.n) return;
   const int batch = head / p.H, hh = head % p.H;
@@ -631,25 +631,21 @@ __device__ __noinline__ void topk_radix_head(const RoutesParams& p, int head) {
   }
 }
 
-// Fast top-budget selection in four launches (all heads at once):
-//   topk_hist_kernel     many workgroups per head: 2080-bin log-linear histogram of the pooled values (bin = 32 x
-//                        bit length + the 5 bits after the leading one; 0 for zero), monotone in the value
-//   topk_pick_kernel     per head: the bin b* holding the budget-th largest value; `above` values lie in higher bins
-//   topk_compact_kernel  many workgroups per head: indices of values above b* to `sel`, (value, index) of values in
-//                        b* to the candidate list (at most kTopCand kept; the count goes on)
-//   topk_final_kernel    per head: the need = budget - above best candidates by (value desc, index asc), then all
+// Fast top-budget selection in three launches (all heads at once):
+//   topk_hist_kernel     many workgroups per head: log-linear histogram of the keys (bin = 32 x bit length + the 5
+//                        bits after the leading one, 0 for zero; for float keys 32 bins per octave of the value),
+//                        monotone in the key. Decode routing fills it in its pool kernel instead.
+//   topk_compact_kernel  many workgroups per head: each finds the bin b* holding the budget-th largest key from the
+//                        histogram (workgroup 0 records it), then writes indices of keys above b* to `sel` and
+//                        (key, index) of keys in b* to the candidate list (at most kTopCand kept; the count goes on),
+//                        one atomic per wave and list
+//   topk_final_kernel    per head: the need = budget - above best candidates by (key desc, index asc), then all
 //                        chosen keys through an LDS bitmap of the eligible range, emitted ascending; when the
 //                        candidates overflowed or the range is too long for the bitmap, topk_radix_head instead
-constexpr int kTopBins = 2080;
-constexpr int kTopChunk = 4096;       // values per histogram / compaction workgroup (256 threads x 16)
+constexpr int kTopChunk = 4096;       // keys per histogram / compaction workgroup (256 threads x 16)
 constexpr int kTopCand = 2048;        // candidates kept per head
 constexpr int kTopBitmapBits = 262144;
 
-static_assert(kTopBins == kTopBinsPool, "pooled_kernel clears the top-k histogram");
-struct TopMeta {
-  int32_t bstar, above, need, flags;
-  uint32_t nsel, ncand, pad0, pad1;
-};
 struct TopWs {
   uint32_t* hist;     // [heads][kTopBins]
   TopMeta* meta;      // [heads]
@@ -657,13 +653,6 @@ struct TopWs {
   uint64_t* candv;    // [heads][kTopCand]
   int32_t* candi;     // [heads][kTopCand]
 };
-
-BB_DEV int top_bin(uint64_t v) {
-  if (!v) return 0;
-  const int lz = __clzll((long long)v);
-  return 32 * (64 - lz) + (int)((v << lz) >> 58 & 31u);
-}
-
 
 __global__ __launch_bounds__(256) void topk_hist_kernel(RoutesParams p, TopWs w) {
   __shared__ uint32_t h[kTopBins];
@@ -673,19 +662,24 @@ __global__ __launch_bounds__(256) void topk_hist_kernel(RoutesParams p, TopWs w)
   for (int b = tid; b < kTopBins; b += 256) h[b] = 0;
   __syncthreads();
   const uint64_t* P = p.pooled + (int64_t)head * p.pstride + lo;
+  const bool fk = p.float_keys != 0;
   const int64_t t0 = (int64_t)blockIdx.x * kTopChunk;
   for (int e = tid; e < kTopChunk; e += 256)
-    if (t0 + e < cnt) atomicAdd(&h[top_bin(P[t0 + e])], 1u);
+    if (t0 + e < cnt) atomicAdd(&h[top_bin(P[t0 + e], fk)], 1u);
   __syncthreads();
   for (int b = tid; b < kTopBins; b += 256)
     if (h[b]) atomicAdd(&w.hist[(int64_t)head * kTopBins + b], h[b]);
 }
 
-__global__ __launch_bounds__(256) void topk_pick_kernel(RoutesParams p, TopWs w) {
+// The bin b* that holds the budget-th largest key of one head, from its histogram (all 256 threads of the workgroup
+// call it): above = keys in higher bins, need = budget - above. With fewer keys than the budget, b* = 0 and every
+// key is taken (need = the zero keys).
+struct TopPick {
+  int bstar, above, need;
+};
+BB_DEV TopPick top_pick(const uint32_t* __restrict__ hist, uint32_t budget, uint32_t* part, TopPick* s_pick) {
   constexpr int PER = (kTopBins + 255) / 256;  // bins per thread, taken from the top
-  __shared__ uint32_t part[256];
-  const int head = blockIdx.x, tid = threadIdx.x;
-  const uint32_t* hist = w.hist + (int64_t)head * kTopBins;
+  const int tid = threadIdx.x;
   uint32_t c[PER], sum = 0;
 #pragma unroll
   for (int k = 0; k < PER; ++k) {
@@ -694,6 +688,7 @@ __global__ __launch_bounds__(256) void topk_pick_kernel(RoutesParams p, TopWs w)
     sum += c[k];
   }
   part[tid] = sum;
+  if (tid == 0) *s_pick = TopPick{-1, 0, 0};
   __syncthreads();
   for (int off = 1; off < 256; off <<= 1) {  // inclusive scan over threads (top bins first)
     const uint32_t a = tid >= off ? part[tid - off] : 0u;
@@ -701,52 +696,83 @@ __global__ __launch_bounds__(256) void topk_pick_kernel(RoutesParams p, TopWs w)
     part[tid] += a;
     __syncthreads();
   }
-  const uint32_t before = part[tid] - sum, budget = (uint32_t)p.budget;
-  if (before < budget && part[tid] >= budget) {  // the budget-th largest value lies in this thread's bins
+  const uint32_t before = part[tid] - sum;
+  if (before < budget && part[tid] >= budget) {  // the budget-th largest key lies in this thread's bins
     uint32_t cum = before;
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
       if (cum + c[k] >= budget) {
-        TopMeta m = {};
-        m.bstar = kTopBins - 1 - (PER * tid + k);
-        m.above = (int32_t)cum;
-        m.need = (int32_t)(budget - cum);
-        w.meta[head] = m;
+        *s_pick = TopPick{kTopBins - 1 - (PER * tid + k), (int)cum, (int)(budget - cum)};
         break;
       }
       cum += c[k];
     }
   }
+  __syncthreads();
+  TopPick r = *s_pick;
+  if (r.bstar < 0) {  // fewer keys than the budget: all of them
+    const uint32_t total = part[255], zeros = hist[0];
+    r = TopPick{0, (int)(total - zeros), (int)zeros};
+  }
+  return r;
 }
 
 __global__ __launch_bounds__(256) void topk_compact_kernel(RoutesParams p, TopWs w) {
+  constexpr int PER = kTopChunk / 256;
+  __shared__ uint32_t part[256];
+  __shared__ TopPick s_pick;
   const int head = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
   int64_t lo, cnt;
   top_range(p, lo, cnt);
-  const uint64_t* P = p.pooled + (int64_t)head * p.pstride + lo;
-  TopMeta* m = w.meta + head;
-  const int bstar = m->bstar;
   const int64_t t0 = (int64_t)blockIdx.x * kTopChunk;
-  for (int e = tid; e < kTopChunk; e += 256) {
-    const int64_t t = t0 + e;
-    const uint64_t v = t < cnt ? P[t] : 0;
-    const int b = t < cnt ? top_bin(v) : -1;
-    // wave-aggregated appends: one atomic per wave and list
-    const uint64_t bs = __builtin_amdgcn_ballot_w64(b > bstar), bc = __builtin_amdgcn_ballot_w64(b == bstar);
+  if (t0 >= cnt) return;  // uniform per workgroup; workgroup 0 always stays when there is any key
+  const TopPick pk = top_pick(w.hist + (int64_t)head * kTopBins, (uint32_t)p.budget, part, &s_pick);
+  TopMeta* m = w.meta + head;
+  if (blockIdx.x == 0 && tid == 0) {
+    m->bstar = pk.bstar;
+    m->above = pk.above;
+    m->need = pk.need;
+  }
+  const bool fk = p.float_keys != 0;
+  const uint64_t* P = p.pooled + (int64_t)head * p.pstride + lo;
+  uint64_t v[PER];
+  int bin[PER];
+  uint32_t ns = 0, nc = 0;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int64_t t = t0 + 256 * k + tid;
+    v[k] = t < cnt ? P[t] : 0;
+    bin[k] = t < cnt ? top_bin(v[k], fk) : -1;
+  }
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    ns += (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(bin[k] > pk.bstar));
+    nc += (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(bin[k] == pk.bstar));
+  }
+  // one atomic per wave and list for the whole chunk
+  uint32_t base_s = 0, base_c = 0;
+  if (lane == 0) {
+    if (ns) base_s = atomicAdd(&m->nsel, ns);
+    if (nc) base_c = atomicAdd(&m->ncand, nc);
+  }
+  base_s = __shfl(base_s, 0);
+  base_c = __shfl(base_c, 0);
+  int32_t* sel = w.sel + (int64_t)head * p.pstride;
+  uint64_t* candv = w.candv + (int64_t)head * kTopCand;
+  int32_t* candi = w.candi + (int64_t)head * kTopCand;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const uint64_t bs = __builtin_amdgcn_ballot_w64(bin[k] > pk.bstar), bc = __builtin_amdgcn_ballot_w64(bin[k] == pk.bstar);
     const uint32_t below_s = __builtin_amdgcn_mbcnt_hi((uint32_t)(bs >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bs, 0u));
     const uint32_t below_c = __builtin_amdgcn_mbcnt_hi((uint32_t)(bc >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bc, 0u));
-    uint32_t base_s = 0, base_c = 0;
-    if (lane == 0) {
-      if (bs) base_s = atomicAdd(&m->nsel, (uint32_t)__builtin_popcountll(bs));
-      if (bc) base_c = atomicAdd(&m->ncand, (uint32_t)__builtin_popcountll(bc));
+    const int32_t ix = (int32_t)(lo + t0 + 256 * k + tid);
+    if (bin[k] > pk.bstar) sel[base_s + below_s] = ix;
+    if (bin[k] == pk.bstar && base_c + below_c < (uint32_t)kTopCand) {
+      candv[base_c + below_c] = v[k];
+      candi[base_c + below_c] = ix;
     }
-    base_s = __shfl(base_s, 0);
-    base_c = __shfl(base_c, 0);
-    if (b > bstar) w.sel[(int64_t)head * p.pstride + base_s + below_s] = (int32_t)(lo + t);
-    if (b == bstar && base_c + below_c < (uint32_t)kTopCand) {
-      w.candv[(int64_t)head * kTopCand + base_c + below_c] = v;
-      w.candi[(int64_t)head * kTopCand + base_c + below_c] = (int32_t)(lo + t);
-    }
+    base_s += (uint32_t)__builtin_popcountll(bs);
+    base_c += (uint32_t)__builtin_popcountll(bc);
   }
 }
 
@@ -832,7 +858,6 @@ hipError_t launch_routes_d(RoutesParams& p, const RouteGeom& g, float* pmax, uin
     const unsigned chunks = (unsigned)((cnt + kTopChunk - 1) / kTopChunk);
     const int heads = p.B * p.H;
     hipLaunchKernelGGL(topk_hist_kernel, dim3(chunks, heads), dim3(256), 0, stream, p, tw);
-    hipLaunchKernelGGL(topk_pick_kernel, dim3(heads), dim3(256), 0, stream, p, tw);
     hipLaunchKernelGGL(topk_compact_kernel, dim3(chunks, heads), dim3(256), 0, stream, p, tw);
     hipLaunchKernelGGL(topk_final_kernel, dim3(heads), dim3(kTopThreads), 0, stream, p, tw);
   }
@@ -878,8 +903,15 @@ __global__ __launch_bounds__(256) void topk_clear_kernel(TopWs w) {
 
 size_t topk_workspace_bytes(int64_t stride, int rows) { return top_ws_bytes(stride, (size_t)rows); }
 
+void topk_hist_meta(void* ws, int64_t stride, int rows, uint32_t** hist, uint32_t** meta) {
+  const TopWs tw = carve_top_ws(static_cast<char*>(ws), stride, (size_t)rows);
+  *hist = tw.hist;
+  *meta = reinterpret_cast<uint32_t*>(tw.meta);
+}
+
 hipError_t launch_topk_rows(const uint64_t* keys, int rows, int64_t stride, int64_t n, const int64_t* n_dev, int front,
-                            int window, int budget, int32_t* out, void* ws, size_t ws_bytes, hipStream_t stream) {
+                            int window, int budget, int32_t* out, void* ws, size_t ws_bytes, int flags,
+                            hipStream_t stream) {
   if (rows <= 0 || stride <= 0 || budget <= 0 || ws_bytes < topk_workspace_bytes(stride, rows))
     return hipErrorInvalidValue;
   RoutesParams p;
@@ -892,17 +924,17 @@ hipError_t launch_topk_rows(const uint64_t* keys, int rows, int64_t stride, int6
   p.window = window;
   p.budget = budget;
   p.out_idx = out;
+  p.float_keys = (flags & kTopFloatKeys) != 0;
   const TopWs tw = carve_top_ws(static_cast<char*>(ws), stride, (size_t)rows);
   // grids cover the largest range the device length can give: [front, stride)
   const int64_t lo = front > 0 ? front : 0;
   const int64_t cnt = stride > lo ? stride - lo : 0;
   const unsigned chunks = (unsigned)((cnt + kTopChunk - 1) / kTopChunk);
-  hipLaunchKernelGGL(topk_clear_kernel, dim3(rows), dim3(256), 0, stream, tw);
-  if (chunks > 0) {
-    hipLaunchKernelGGL(topk_hist_kernel, dim3(chunks, rows), dim3(256), 0, stream, p, tw);
-    hipLaunchKernelGGL(topk_pick_kernel, dim3(rows), dim3(256), 0, stream, p, tw);
-    hipLaunchKernelGGL(topk_compact_kernel, dim3(chunks, rows), dim3(256), 0, stream, p, tw);
+  if (!(flags & kTopHistReady)) {
+    hipLaunchKernelGGL(topk_clear_kernel, dim3(rows), dim3(256), 0, stream, tw);
+    if (chunks > 0) hipLaunchKernelGGL(topk_hist_kernel, dim3(chunks, rows), dim3(256), 0, stream, p, tw);
   }
+  if (chunks > 0) hipLaunchKernelGGL(topk_compact_kernel, dim3(chunks, rows), dim3(256), 0, stream, p, tw);
   hipLaunchKernelGGL(topk_final_kernel, dim3(rows), dim3(kTopThreads), 0, stream, p, tw);
   return hipGetLastError();
 }
@@ -928,6 +960,7 @@ hipError_t launch_routes(RoutesParams& p, void* ws, size_t ws_bytes, hipStream_t
   const size_t nbkv = (size_t)p.B * p.Hkv;
   p.pstride = p.n;
   p.n_dev = nullptr;
+  p.float_keys = 0;
   char* w = static_cast<char*>(ws);
   p.scores = reinterpret_cast<uint16_t*>(w); w += align256(nbkv * g.rows * (size_t)g.ns * 2);
   float* pmax = reinterpret_cast<float*>(w); w += align256(nbkv * g.n_kb1 * g.rows * 4);
