@@ -309,6 +309,37 @@ def short_arm_leg(dev, seed):
     return res
 
 
+def graph_decode_leg(model, ids, steps=32):
+    """Greedy decode after the sparse prefill (modal_rd/graph_decode.py): prefill into the decoder's buffers, then
+    one HIP graph per token (32 layers of split-K flash decoding over the whole cache + projections, MLP, lm_head,
+    argmax), timed per token; the same step run eagerly (one launch per op) beside it."""
+    import torch
+    from bigger_bird_amd.graph_decode import graph_prefill
+
+    dec, out, prefill_s = graph_prefill(model, ids, 2 * steps + 16, headroom=0)
+    del out
+    dec.capture()
+    dec.run(2)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    dec.run(steps)
+    torch.cuda.synchronize()
+    graph_ms = (time.perf_counter() - t0) / steps * 1e3
+    t0 = time.perf_counter()
+    dec.run(steps // 4, graph=False)
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) / (steps // 4) * 1e3
+    res = {"context_tokens": int(ids.shape[1]), "prefill_s": round(prefill_s, 3),
+           "graph_ms_per_token": round(graph_ms, 3), "eager_step_ms_per_token": round(eager_ms, 3),
+           "h100_reference_ms_per_token": {"eager": 25.5, "graph": 15.1, "context": "~128K, v3"}}
+    print(f"graph decode: {graph_ms:.3f} ms/token (eager step {eager_ms:.3f})", file=sys.stderr, flush=True)
+    del dec
+    from bigger_bird_amd import graph_decode as gd
+    gd._DECODERS.clear()
+    torch.cuda.empty_cache()
+    return res
+
+
 def full_model_leg(dev, seed, T=131072):
     """BASELINE configs[2] (SURVEY next step): prefill of a random-init Llama-3-8B-architecture model in bf16 (32 layers,
     hidden 4096, 32 q / 8 KV heads, FFN 14336, vocab 128256, RoPE theta 500000) at T uniform-random token ids, with
@@ -367,6 +398,7 @@ def full_model_leg(dev, seed, T=131072):
     install(model, "rd", **attn_cfg)
     run()  # warm-up: kernels loaded, allocator sized
     sparse_s, ls = timed(2, "rd sparse")
+    res["graph_decode"] = graph_decode_leg(model, ids)
     install(model, "dense_rd", **attn_cfg)
     dense_s, ld = timed(1, "dense_rd")
     cos = torch.nn.functional.cosine_similarity

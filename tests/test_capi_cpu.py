@@ -107,3 +107,13 @@ def test_attended_pairs_matches_brute_force():
         allowed[T - tail:] = kk <= q[T - tail:]
         total += int(allowed.sum())
     assert attended_pairs(T, H, sink, window, routes, tail) == total
+
+
+def test_argmax_argument_checks():
+    L = _lib.lib()
+    out = ctypes.c_void_p(16)
+    assert L.bb_argmax(ctypes.c_void_p(16), 0, 1, out, None) != 0
+    assert "row length" in L.bb_last_error().decode()
+    assert L.bb_argmax(ctypes.c_void_p(16), 10, 3, out, None) != 0
+    assert "dtype must be" in L.bb_last_error().decode()
+    assert L.bb_argmax(None, 10, 1, out, None) != 0

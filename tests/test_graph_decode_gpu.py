@@ -1,0 +1,151 @@
+"""HIP-graph greedy decode (bigger_bird_amd.graph_decode, drop-in for modal_rd/graph_decode.py) on a tiny random-init
+Llama, as the reference's GPU self-check modal_rd/graphcheck.py:22-37 runs it: for the dense_rd, rd and rd + kv_evict
+arms the captured decode must produce what eager decoding produces.
+
+* Graph replay vs the same step run eagerly (a second decoder, graph=False): token ids and logits bit-identical for
+  every step, with unrelated eager work and host synchronisation between replays (captured graphs have given wrong
+  results on replays after the first when they recorded memset nodes; the step records none).
+* Graph decode vs the model's own eager forward (HF layer stack, RDAttention's exact decode over a DynamicCache),
+  teacher-forced with the graph's tokens: logits close at every step (the attention kernels differ: split-K flash
+  decoding vs the INT8-path kernel in bf16 mode), and the same greedy token wherever the eager top-2 margin is clear.
+* generate(): stops after the block that produced an EOS, returns the tokens through it, rewinds the cache to right
+  after the EOS's input and makes the EOS the next input; the HIP argmax equals torch.argmax (incl. ties, NaN).
+"""
+import pytest
+import torch
+
+from bigger_bird_amd import install
+from bigger_bird_amd.decode import argmax_index
+from bigger_bird_amd.graph_decode import StaticDecoder, graph_prefill
+
+pytestmark = pytest.mark.gpu
+
+KW = dict(sink=8, window=96, vertical=24, n_route=16, exact_tail=24, block_m=16, block_n=16)
+EVICT = dict(kv_evict=True)
+N, STEPS = 400, 12
+
+
+def _tiny(dev):
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    # head_dim 64: the decode kernels take 64 or 128
+    cfg = LlamaConfig(vocab_size=512, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
+                      num_attention_heads=8, num_key_value_heads=2, max_position_embeddings=8192,
+                      attn_implementation="sdpa")
+    torch.manual_seed(0)
+    return LlamaForCausalLM(cfg).to(dev, torch.bfloat16).eval()
+
+
+def _ids(dev):
+    g = torch.Generator().manual_seed(4)
+    return torch.randint(0, 512, (1, N), generator=g).to(dev)
+
+
+SPARSE = dict(front=8, window=64, routed=32)
+
+
+@pytest.mark.parametrize("arm,extra,sparse", [("dense_rd", {}, None), ("rd", {}, None), ("rd", EVICT, None),
+                                              ("rd", {}, SPARSE)])
+def test_graph_matches_eager_step_bitwise(arm, extra, sparse, dev):
+    print(f"case graph_vs_eager_step {arm} evict={bool(extra)} sparse={bool(sparse)}", flush=True)
+    model = _tiny(dev)
+    install(model, arm, **KW, **extra)
+    ids = _ids(dev)
+    dec, out, _ = graph_prefill(model, ids, STEPS + 4, headroom=64, sparse_decode=sparse)
+    assert int(dec.token) == out.logits[0, -1].argmax().item()
+    assert dec.sparse == [bool(sparse)] * len(model.model.layers)
+    # a second, eager decoder over the same prefill (deterministic kernels: identical cache)
+    eager = StaticDecoder(model, dec.capacity, sparse_decode=sparse)
+    with torch.inference_mode():
+        from transformers import DynamicCache
+        cache = eager.buffer_cache() if not extra else DynamicCache(config=model.config)
+        o2 = model(input_ids=ids, position_ids=torch.arange(N, device=dev)[None], past_key_values=cache,
+                   use_cache=True, logits_to_keep=1)
+        assert torch.equal(o2.logits, out.logits)
+        eager.load(cache, N, o2.logits[0, -1].argmax().item())
+    m = int(dec.length)
+    if extra:
+        g = model.config.num_attention_heads // model.config.num_key_value_heads
+        assert m == KW["sink"] + KW["window"] + g * KW["vertical"]
+    else:
+        assert m == N
+    for i in range(STEPS):
+        dec.run(1)
+        eager.run(1, graph=False)
+        torch.cuda.synchronize()
+        assert int(dec.length) == m + i + 1 and int(dec.position) == N + i + 1
+        assert torch.equal(dec.logits, eager.logits), i
+        assert dec.generated() == eager.generated(), i
+        _ = torch.randn(1000, device=dev).sum().item()  # unrelated eager work between replays
+
+
+@pytest.mark.parametrize("arm,extra", [("dense_rd", {}), ("rd", {}), ("rd", EVICT)])
+def test_graph_matches_model_forward(arm, extra, dev):
+    print(f"case graph_vs_model {arm} evict={bool(extra)}", flush=True)
+    from transformers import DynamicCache
+
+    model = _tiny(dev)
+    install(model, arm, **KW, **extra)
+    ids = _ids(dev)
+    dec, out, _ = graph_prefill(model, ids, STEPS + 4, headroom=64)
+    cache = DynamicCache(config=model.config)
+    with torch.inference_mode():
+        ref = model(input_ids=ids, past_key_values=cache, use_cache=True, logits_to_keep=1).logits[0, -1]
+        tok = ref.argmax().item()
+        for i in range(STEPS):
+            dec.run(1)
+            got = dec.logits.float()
+            step_ids = torch.tensor([[tok]], device=dev)
+            pos = torch.tensor([[N + i]], device=dev)
+            want = model(input_ids=step_ids, position_ids=pos, past_key_values=cache, use_cache=True).logits[0, -1]
+            want = want.float()
+            err = (got - want).abs().max().item()
+            assert err <= 2e-2 * want.abs().max().item() + 1e-3, (i, err)
+            top2 = want.topk(2).values
+            nxt = dec.generated()[-1]
+            if (top2[0] - top2[1]).item() > 4 * err + 1e-3:
+                assert nxt == want.argmax().item(), i
+            tok = nxt  # teacher forcing with the graph's token
+
+
+def test_generate_eos_and_rewind(dev):
+    print("case generate_eos", flush=True)
+    model = _tiny(dev)
+    install(model, "dense_rd", **KW)
+    ids = _ids(dev)
+    dec, _, _ = graph_prefill(model, ids, 40, headroom=64)
+    first = int(dec.token)
+    toks, steps = dec.generate(10, block=4)
+    assert steps == 12 - 2 and len(toks) == 10  # max_steps caps the last block
+    # replay from the same prefill with the 6th token as EOS
+    dec2, _, _ = graph_prefill(model, ids, 40, headroom=64)
+    assert dec2 is dec and int(dec.token) == first and int(dec.length) == N
+    eos = toks[5]
+    cut = toks.index(eos) + 1
+    got, steps = dec.generate(10, eos=[eos], block=4)
+    assert got == toks[:cut] and steps == 4 * ((cut + 3) // 4)  # whole blocks, stopping after the EOS's block
+    assert int(dec.length) == N + cut and int(dec.position) == N + cut and int(dec.step_i) == cut
+    assert int(dec.token) == eos
+    # a further turn appends after the rewound point and continues as the uninterrupted run would
+    more, _ = dec.generate(10 - cut, block=4)
+    assert more == toks[cut:]
+    with pytest.raises(ValueError, match="buffer full"):
+        dec.run(dec.capacity)
+
+
+def test_argmax_matches_torch(dev):
+    g = torch.Generator().manual_seed(5)
+    for dt in (torch.float32, torch.bfloat16, torch.float16):
+        for n in (1, 7, 1000, 128256, 300001):
+            x = torch.randn(n, generator=g).to(dt).to(dev)
+            assert argmax_index(x).item() == x.argmax().item(), (dt, n)
+        x = torch.zeros(5000, dtype=dt, device=dev)
+        x[[17, 300, 4000]] = 3.0  # ties: first index
+        assert argmax_index(x).item() == 17
+        x[2500] = float("nan")
+        x[4500] = float("nan")
+        assert argmax_index(x).item() == 2500
+        x = torch.full((999,), -float("inf"), dtype=dt, device=dev)
+        assert argmax_index(x).item() == 0
+    x = torch.randn(2, 4097, generator=g).to(torch.bfloat16).to(dev)[:, 1:].reshape(-1)  # offset, unaligned start
+    assert argmax_index(x[3:]).item() == x[3:].argmax().item()

@@ -146,3 +146,21 @@ def topk_columns(vals, budget, *, front=0, tail=0):
     _lib.check(L.bb_topk_f32(_lib.ptr(v), v.stride(0), rows, n, int(front), int(tail), int(budget), _lib.ptr(out),
                              _lib.ptr(ws), ws_bytes, _lib.stream_of(v)))
     return out
+
+
+_ARGMAX_KIND = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+
+
+def argmax_index(x, out=None):
+    """Index of the largest element of a 1-D GPU tensor (fp32 / bf16 / fp16) as an int64 [1] GPU tensor (written into
+    `out` when given): torch.argmax semantics (NaN largest, first index on ties), one workgroup and no workspace, so
+    a captured decode step needs no multi-workgroup reduction (modal_rd/graph_decode.py:216-217)."""
+    if not x.is_cuda or x.ndim != 1 or x.dtype not in _ARGMAX_KIND:
+        raise ValueError("argmax_index needs a 1-D fp32/bf16/fp16 GPU tensor")
+    x = x if x.stride(0) == 1 else x.contiguous()
+    if out is None:
+        out = torch.empty(1, dtype=torch.int64, device=x.device)
+    elif out.dtype != torch.int64 or out.numel() != 1 or not out.is_cuda:
+        raise ValueError("argmax_index: out must be an int64 [1] GPU tensor")
+    _lib.check(_lib.lib().bb_argmax(_lib.ptr(x), x.shape[0], _ARGMAX_KIND[x.dtype], _lib.ptr(out), _lib.stream_of(x)))
+    return out

@@ -500,6 +500,14 @@ int bb_topk_f32(const float* vals, int64_t sv0, int rows, int64_t n, int front, 
                     "bb_topk_f32");
 }
 
+int bb_argmax(const void* x, int64_t n, int dtype, int64_t* out, void* stream) {
+  g_err[0] = 0;
+  if (!x || !out) return fail("argmax: null argument");
+  if (n <= 0 || n > 0x7ffffffe) return fail("argmax: row length %lld out of range", (long long)n);
+  if (dtype < 0 || dtype > 2) return fail("argmax: dtype must be 0 (fp32), 1 (bf16) or 2 (fp16)");
+  return hip_status(bb::launch_argmax(x, n, dtype, aligned(x, 16), out, static_cast<hipStream_t>(stream)), "bb_argmax");
+}
+
 int bb_rope_inplace(void* x, const int64_t* sx, int B, int Hh, int64_t T, int D, const void* cos, const void* sin,
                     const int64_t* sc, void* stream) {
   g_err[0] = 0;

@@ -426,6 +426,81 @@ __global__ __launch_bounds__(256) void f32_keys_kernel(const float* __restrict__
   keys[(int64_t)r * n + j] = float_key(x);  // NaN and x <= 0 sort last
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// Greedy token choice of a decode step (modal_rd/graph_decode.py:216-217): the index of the largest logit of one row,
+// torch.argmax semantics (a NaN is larger than every number, the first index wins ties). One 1024-thread workgroup,
+// so a captured decode step holds no multi-workgroup reduction (and no counters to clear between replays).
+constexpr int kAmThreads = 1024;
+
+BB_DEV bool am_better(float a, int ia, float b, int ib) {
+  const bool na = a != a, nb = b != b;
+  if (na != nb) return na;
+  if (!na && a != b) return a > b;
+  return ia < ib;
+}
+
+template <typename T, int EPU>  // element type (float, bf16 / fp16 bits), elements per load
+__global__ __launch_bounds__(kAmThreads) void argmax_kernel(const T* __restrict__ x, int64_t n, int kind,
+                                                            int64_t* __restrict__ out) {
+  __shared__ float wv[kAmThreads / 64];
+  __shared__ int wi[kAmThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  auto value = [&](T raw) -> float {
+    if constexpr (sizeof(T) == 4) return __builtin_bit_cast(float, raw);
+    else return kind == 2 ? (float)__builtin_bit_cast(_Float16, (uint16_t)raw) : bf16_to_f32((uint16_t)raw);
+  };
+  float bv = -__builtin_huge_valf();
+  int bi = 0x7fffffff;
+  const int64_t units = n / EPU;
+  for (int64_t u = tid; u < units; u += kAmThreads) {
+    T e[EPU];
+    if constexpr (EPU > 1) {
+      const u32x4_t w = *reinterpret_cast<const u32x4_t*>(x + u * EPU);
+      __builtin_memcpy(e, &w, sizeof(w));
+    } else {
+      e[0] = x[u];
+    }
+#pragma unroll
+    for (int k = 0; k < EPU; ++k) {
+      const float v = value(e[k]);
+      const int i = (int)(u * EPU + k);
+      if (am_better(v, i, bv, bi)) {
+        bv = v;
+        bi = i;
+      }
+    }
+  }
+  for (int64_t i = units * EPU + tid; i < n; i += kAmThreads) {
+    const float v = value(x[i]);
+    if (am_better(v, (int)i, bv, bi)) {
+      bv = v;
+      bi = (int)i;
+    }
+  }
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const float ov = __shfl_xor(bv, off);
+    const int oi = __shfl_xor(bi, off);
+    if (am_better(ov, oi, bv, bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if (lane == 0) {
+    wv[wave] = bv;
+    wi[wave] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < kAmThreads / 64; ++w)
+      if (am_better(wv[w], wi[w], bv, bi)) {
+        bv = wv[w];
+        bi = wi[w];
+      }
+    out[0] = bi == 0x7fffffff ? 0 : bi;
+  }
+}
+
 template <int D, int GR, bool F16>
 hipError_t launch_sparse_decode_t(const SparseDecodeParams& p, hipStream_t stream) {
   hipLaunchKernelGGL((sparse_decode_kernel<D, GR, F16>), dim3(p.n_splits, p.rows), dim3(kSdThreads), 0, stream, p);
@@ -480,6 +555,25 @@ hipError_t launch_gather_rows(const uint16_t* src, int64_t ss0, int64_t ss1, int
   if (work <= 0 || heads <= 0) return hipSuccess;
   hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)((work + 255) / 256), heads), dim3(256), 0, stream, src, ss0,
                      ss1, n_src, idx, si0, m, D, dst, sd0, sd1);
+  return hipGetLastError();
+}
+
+hipError_t launch_argmax(const void* x, int64_t n, int kind, bool vec16, int64_t* out, hipStream_t stream) {
+  if (n <= 0 || n > 0x7ffffffe) return hipErrorInvalidValue;
+  if (kind == 0) {
+    if (vec16)
+      hipLaunchKernelGGL((argmax_kernel<uint32_t, 4>), dim3(1), dim3(kAmThreads), 0, stream,
+                         static_cast<const uint32_t*>(x), n, kind, out);
+    else
+      hipLaunchKernelGGL((argmax_kernel<uint32_t, 1>), dim3(1), dim3(kAmThreads), 0, stream,
+                         static_cast<const uint32_t*>(x), n, kind, out);
+  } else if (vec16) {
+    hipLaunchKernelGGL((argmax_kernel<uint16_t, 8>), dim3(1), dim3(kAmThreads), 0, stream,
+                       static_cast<const uint16_t*>(x), n, kind, out);
+  } else {
+    hipLaunchKernelGGL((argmax_kernel<uint16_t, 1>), dim3(1), dim3(kAmThreads), 0, stream,
+                       static_cast<const uint16_t*>(x), n, kind, out);
+  }
   return hipGetLastError();
 }
 

@@ -129,6 +129,8 @@ hipError_t launch_topk_rows(const uint64_t* keys, int rows, int64_t stride, int6
 hipError_t launch_gather_rows(const uint16_t* src, int64_t ss0, int64_t ss1, int64_t n_src, int heads,
                               const int64_t* idx, int64_t si0, int m, int D, uint16_t* dst, int64_t sd0, int64_t sd1,
                               hipStream_t stream);
+// Index of the largest element of x [n] (kind 0 fp32, 1 bf16, 2 fp16; vec16: 16-byte aligned), to out[0].
+hipError_t launch_argmax(const void* x, int64_t n, int kind, bool vec16, int64_t* out, hipStream_t stream);
 hipError_t launch_f32_keys(const float* vals, int64_t sv0, int rows, int64_t n, uint64_t* keys, hipStream_t stream);
 
 // RoPE in place (HF apply_rotary_pos_emb arithmetic in bf16).
