@@ -188,69 +188,62 @@ def sparse_decode_leg(dev, seed):
     """Sparse decode after a 128K prefill (SURVEY next step: kernels/bigger_bird_decode.py + bigger_bird_route.py):
     bf16 cache of 131072 tokens (+1 per step), 32 q / 8 KV heads, d=128; a step appends the new K/V row at the
     device-side length, routes (pooled decode routing over every cached key, top 512 per KV head outside the sink
-    and the 16384-key window) and attends sink 64 + window 16384 + the 512 routed keys. Timed eagerly and as one
-    captured HIP graph replayed per step; bytes = the K rows the routing reads + its fp32 score round trip + the
-    K/V rows the sparse decode reads."""
+    and the 16384-key window) and attends sink 64 + window 16384 + the 512 routed keys. The step's inputs are fixed
+    buffers (in a model they come from the projections inside the same graph). Timed eagerly and as one captured
+    HIP graph replayed per step; bytes = the K rows the routing reads + its fp32 score round trip + the K/V rows the
+    sparse decode reads."""
     import torch
     from bigger_bird_amd import bigger_bird_decode, bigger_bird_route
 
     n0, steps, H, Hkv, d = 131072, 64, 32, 8, 128
     front, window, routed = 64, 16384, 512
-    cap = n0 + steps + 8
+    cap = n0 + 2 * steps + 8
     g = torch.Generator(device=dev).manual_seed(seed + 9)
     k = torch.randn(Hkv, cap, d, device=dev, generator=g).to(torch.bfloat16)
     v = torch.randn(Hkv, cap, d, device=dev, generator=g).to(torch.bfloat16)
-    qs = torch.randn(steps, H, d, device=dev, generator=g).to(torch.bfloat16)
-    kn = torch.randn(steps, Hkv, d, device=dev, generator=g).to(torch.bfloat16)
-    vn = torch.randn(steps, Hkv, d, device=dev, generator=g).to(torch.bfloat16)
+    qb = torch.randn(H, d, device=dev, generator=g).to(torch.bfloat16)
+    kb = torch.randn(Hkv, d, device=dev, generator=g).to(torch.bfloat16)
+    vb = torch.randn(Hkv, d, device=dev, generator=g).to(torch.bfloat16)
     scale = d ** -0.5
 
-    def step(length, q, knew, vnew):
-        k.index_copy_(1, length, knew[:, None])
-        v.index_copy_(1, length, vnew[:, None])
+    def step(length):
+        k.index_copy_(1, length, kb[:, None])
+        v.index_copy_(1, length, vb[:, None])
         length.add_(1)
-        idx = bigger_bird_route(q, k, routed, front=front, window=window, scale=scale, n=length)
-        return bigger_bird_decode(q, k, v, idx, front=front, window=window, scale=scale, n=length)
+        idx = bigger_bird_route(qb, k, routed, front=front, window=window, scale=scale, n=length)
+        return bigger_bird_decode(qb, k, v, idx, front=front, window=window, scale=scale, n=length)
+
+    def timed(fn):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        for _ in range(steps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return round(a.elapsed_time(b) * 1e3 / steps, 2)
 
     res = {"workload": "sparse decode after a 131072-token prefill: bf16 cache, 32q/8kv heads, d=128; per step append + "
                        "pooled decode routing (top 512 per KV head) + split-K decode over sink 64 + window 16384 + 512 "
                        "routed keys"}
     with torch.inference_mode():
         length = torch.tensor([n0], device=dev)
-        for i in range(4):
-            step(length, qs[i], kn[i], vn[i])
-        torch.cuda.synchronize()
+        for _ in range(4):
+            step(length)
         length.fill_(n0)
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        for i in range(steps):
-            step(length, qs[i], kn[i], vn[i])
-        b.record()
-        torch.cuda.synchronize()
-        res["eager_us_per_step"] = round(a.elapsed_time(b) * 1e3 / steps, 2)
-        # graph: one captured step, replayed with the inputs copied into static buffers
-        qb, kb, vb = qs[0].clone(), kn[0].clone(), vn[0].clone()
+        res["eager_us_per_step"] = timed(lambda: step(length))
         length.fill_(n0)
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
-            step(length, qb, kb, vb)
+            step(length)
         torch.cuda.current_stream().wait_stream(s)
         length.fill_(n0)
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            step(length, qb, kb, vb)
+            step(length)
         length.fill_(n0)
-        torch.cuda.synchronize()
-        a.record()
-        for i in range(steps):
-            qb.copy_(qs[i])
-            kb.copy_(kn[i])
-            vb.copy_(vn[i])
-            graph.replay()
-        b.record()
-        torch.cuda.synchronize()
-        res["graph_us_per_step"] = round(a.elapsed_time(b) * 1e3 / steps, 2)
+        res["graph_us_per_step"] = timed(graph.replay)
     n_mean = n0 + (steps + 1) / 2
     route_bytes = Hkv * n_mean * d * 2 + 2 * H * n_mean * 4          # K read once + fp32 scores written and read
     decode_bytes = Hkv * (front + window + routed) * d * 2 * 2        # K and V rows of the sparse key list
