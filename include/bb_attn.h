@@ -150,16 +150,15 @@ int bb_gather_rows(const void* src, const int64_t* ss, int64_t n_src, int heads,
  */
 int bb_topk_f32(const float* vals, int64_t sv0, int rows, int64_t n, int front, int tail, int budget, int32_t* out,
                 void* ws, size_t ws_bytes, void* stream);
+size_t bb_topk_f32_workspace(int rows, int64_t n);
 
 /*
  * Greedy token choice of a decode step: out[0] (int64, device) = index of the largest element of x [n] (dtype 0
  * fp32, 1 bf16, 2 fp16; contiguous); a NaN counts as larger than every number and the first index wins ties
  * (torch.argmax). One workgroup, no workspace: safe inside a captured decode graph. Replaces
- * logits[0, -1].argmax() of StaticDecoder.step (modal_rd/graph_decode.py:216-217).
+ * logits[0, -1].argmax() of StaticDecoder.step (modal_rd/graph_decode.py:201-202).
  */
 int bb_argmax(const void* x, int64_t n, int dtype, int64_t* out, void* stream);
-
-size_t bb_topk_f32_workspace(int rows, int64_t n);
 
 /*
  * In-place RoPE on x [B, Hh, T, D] (strides sx[3]) with cos/sin [B, T, D] (strides sc[2]; 0 to broadcast), with

@@ -154,7 +154,7 @@ _ARGMAX_KIND = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 def argmax_index(x, out=None):
     """Index of the largest element of a 1-D GPU tensor (fp32 / bf16 / fp16) as an int64 [1] GPU tensor (written into
     `out` when given): torch.argmax semantics (NaN largest, first index on ties), one workgroup and no workspace, so
-    a captured decode step needs no multi-workgroup reduction (modal_rd/graph_decode.py:216-217)."""
+    a captured decode step needs no multi-workgroup reduction (modal_rd/graph_decode.py:201-202)."""
     if not x.is_cuda or x.ndim != 1 or x.dtype not in _ARGMAX_KIND:
         raise ValueError("argmax_index needs a 1-D fp32/bf16/fp16 GPU tensor")
     x = x if x.stride(0) == 1 else x.contiguous()

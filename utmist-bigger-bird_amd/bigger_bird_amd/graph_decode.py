@@ -33,7 +33,7 @@ from .decode import argmax_index, bigger_bird_decode, bigger_bird_route
 
 class BufferLayer(DynamicLayer):
     """Cache layer over preallocated [Hkv, capacity, d] buffers: prefill rows are written in place and `keys` /
-    `values` are [1, Hkv, n, d] views of the filled part (modal_rd/graph_decode.py:38-57)."""
+    `values` are [1, Hkv, n, d] views of the filled part (modal_rd/graph_decode.py:40-57)."""
 
     def __init__(self, kb, vb):
         super().__init__()

@@ -427,7 +427,7 @@ __global__ __launch_bounds__(256) void f32_keys_kernel(const float* __restrict__
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Greedy token choice of a decode step (modal_rd/graph_decode.py:216-217): the index of the largest logit of one row,
+// Greedy token choice of a decode step (modal_rd/graph_decode.py:201-202): the index of the largest logit of one row,
 // torch.argmax semantics (a NaN is larger than every number, the first index wins ties). One 1024-thread workgroup,
 // so a captured decode step holds no multi-workgroup reduction (and no counters to clear between replays).
 constexpr int kAmThreads = 1024;

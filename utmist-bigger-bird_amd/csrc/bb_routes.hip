@@ -45,6 +45,7 @@ BB_DEV uint64_t fix40(float v) { return (uint64_t)(v * kFixOne); }
 
 struct RouteGeom {
   int G, rows, n_kb1, n_kb2, row_blocks;
+  int sum_rows, sum_splits;  // rowsum_kernel: rows per workgroup (a multiple of 4) and row slices
   int64_t ns;  // score row stride: n rounded up to 8 (16-byte aligned rows)
 };
 
@@ -395,25 +396,28 @@ __global__ __launch_bounds__(64) void rowmax_kernel(RoutesParams p, RouteGeom g,
   if (lane == 0) p.rowmax[(int64_t)bkv * g.rows + row] = __float_as_uint(mx);
 }
 
-// Fixed-point partial row sums: one wave per row (4 rows in flight per workgroup), 16 keys per lane.
+// Fixed-point partial row sums: one wave per row (4 rows in flight per workgroup), 16 keys per lane. The rows of a
+// key block may be cut into blockIdx.z slices of g.sum_rows rows, so short sequences still fill the chip.
 __global__ __launch_bounds__(256) void rowsum_kernel(RoutesParams p, RouteGeom g, uint64_t* __restrict__ psum) {
   const int kb = blockIdx.x, bkv = blockIdx.y;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int r_begin = blockIdx.z * g.sum_rows;
+  const int r_end = r_begin + g.sum_rows < g.rows ? r_begin + g.sum_rows : g.rows;
   const int64_t j0 = (int64_t)kb * kSumKeys + 16 * lane;
   // the next row's scores are loaded while this row's are summed
   u32x4_t na = {0, 0, 0, 0}, nb = {0, 0, 0, 0};
-  if (wave < g.rows && j0 + 16 <= p.n) {
-    const uint16_t* src = p.scores + ((int64_t)bkv * g.rows + wave) * g.ns + j0;
+  if (r_begin + wave < r_end && j0 + 16 <= p.n) {
+    const uint16_t* src = p.scores + ((int64_t)bkv * g.rows + r_begin + wave) * g.ns + j0;
     na = ld16(src);
     nb = ld16(src + 8);
   }
-  for (int row = wave; row < g.rows; row += 4) {
+  for (int row = r_begin + wave; row < r_end; row += 4) {
     const float M = __uint_as_float(p.rowmax[(int64_t)bkv * g.rows + row]);
     const uint16_t* src = p.scores + ((int64_t)bkv * g.rows + row) * g.ns + j0;
     uint64_t acc = 0;
     if (j0 + 16 <= p.n) {
       const u32x4_t a = na, b = nb;
-      if (row + 4 < g.rows) {
+      if (row + 4 < r_end) {
         na = ld16(src + 4 * g.ns);
         nb = ld16(src + 4 * g.ns + 8);
       }
@@ -848,7 +852,7 @@ hipError_t launch_routes_d(RoutesParams& p, const RouteGeom& g, float* pmax, uin
   else
     hipLaunchKernelGGL(scores_kernel<D>, dim3(g.n_kb1, g.row_blocks, nbkv), dim3(256), 0, stream, p, g, pmax);
   hipLaunchKernelGGL(rowmax_kernel, dim3(g.rows, nbkv), dim3(64), 0, stream, p, g, pmax);
-  hipLaunchKernelGGL(rowsum_kernel, dim3(g.n_kb2, nbkv), dim3(256), 0, stream, p, g, psum);
+  hipLaunchKernelGGL(rowsum_kernel, dim3(g.n_kb2, nbkv, g.sum_splits), dim3(256), 0, stream, p, g, psum);
   hipLaunchKernelGGL(invz_kernel, dim3(g.rows, nbkv), dim3(64), 0, stream, p, g, psum, invz);
   hipLaunchKernelGGL(pooled_kernel, dim3((unsigned)((p.n + kPoolKeys - 1) / kPoolKeys), p.B * p.H), dim3(kPoolKeys), 0,
                      stream, p, g, invz, tw.hist, reinterpret_cast<uint32_t*>(tw.meta));
@@ -872,6 +876,13 @@ RouteGeom geom(int64_t n, int H, int Hkv, int r) {
   g.n_kb2 = (int)((n + kSumKeys - 1) / kSumKeys);
   g.row_blocks = (g.rows + kMaxRows - 1) / kMaxRows;
   g.ns = (n + 7) & ~(int64_t)7;
+  // rowsum: about 8 workgroups per CU (2048) per KV-head set, slices of at least 16 rows (4 per wave)
+  const int blocks = g.n_kb2 * Hkv > 0 ? g.n_kb2 * Hkv : 1;
+  int splits = (2048 + blocks - 1) / blocks;
+  const int max_splits = (g.rows + 15) / 16;
+  splits = splits < 1 ? 1 : (splits > max_splits ? max_splits : splits);
+  g.sum_rows = (((g.rows + splits - 1) / splits) + 3) & ~3;
+  g.sum_splits = (g.rows + g.sum_rows - 1) / g.sum_rows;
   return g;
 }
 
