@@ -77,3 +77,36 @@ def test_helpers_match_torch(dev):
     idx = torch.randint(0, 3000, (4, 517), generator=g).to(dev)
     out = gather_rows(x, idx)
     assert torch.equal(out, x.gather(1, idx[:, :, None].expand(-1, -1, 128)))
+
+
+def _topk_ref(vals, budget, front, tail):
+    """(value desc, index asc) over [front, n - tail), ascending indices; values <= 0 / NaN rank last."""
+    out = []
+    for row in vals.double().cpu():
+        seg = row[front:row.shape[0] - tail].clone()
+        seg[~(seg > 0)] = 0.0
+        order = torch.argsort(-seg, stable=True)[:budget] + front
+        out.append(order.sort().values)
+    return torch.stack(out).to(torch.int32)
+
+
+@pytest.mark.parametrize("case", ["wide_range", "ties", "above_clamp", "below_clamp", "mixed_signs"])
+def test_topk_columns_float_bins(case, dev):
+    """The float-key histogram bins 32 per octave over [2^-40, 2^25) and clamps outside; clamped bins, heavy ties
+    (candidate overflow -> radix select) and non-positive values must still give the exact top-k."""
+    print(f"case topk_float_bins {case}", flush=True)
+    g = torch.Generator().manual_seed(11)
+    rows, n, front, tail, budget = 4, 20000, 5, 300, 700
+    if case == "wide_range":
+        vals = torch.exp2(torch.rand(rows, n, generator=g) * 110 - 65)          # 2^-65 .. 2^45
+    elif case == "ties":
+        vals = torch.randint(0, 6, (rows, n), generator=g).float() * 0.25     # six values, 3000+ ties each
+    elif case == "above_clamp":
+        vals = 2.0 ** 30 * (1 + torch.rand(rows, n, generator=g))             # one clamped bin, distinct values
+    elif case == "below_clamp":
+        vals = 2.0 ** -50 * (1 + torch.rand(rows, n, generator=g))
+    else:
+        vals = torch.randn(rows, n, generator=g)                                # half non-positive
+        vals[:, ::7] = float("nan")
+    got = topk_columns(vals.to(dev), budget, front=front, tail=tail).cpu()
+    assert torch.equal(got, _topk_ref(vals, budget, front, tail))
