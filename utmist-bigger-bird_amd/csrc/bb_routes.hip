@@ -35,7 +35,7 @@ namespace bb {
 namespace {
 
 constexpr int kScoreKeys = 32;    // keys per scores_kernel block (8 key groups of 4)
-constexpr int kScoreIters = 8;    // key blocks per scores_kernel workgroup
+constexpr int kScoreIters = 16;   // key blocks per scores_kernel workgroup
 constexpr int kSumKeys = 1024;    // keys per rowsum_kernel workgroup
 constexpr int kPoolKeys = 256;    // keys per pooled_kernel workgroup
 constexpr int kMaxRows = 256;     // G * r handled by one scores workgroup (rows beyond this use more row blocks)
