@@ -88,6 +88,14 @@ int bb_int8_quantize(const void* x, int x_is_f32, int64_t outer, int64_t row_str
                      int D, float min_scale, int8_t* q, void* scale, int scale_is_f16, void* stream);
 
 /* q [rows, D] int8 * scale [rows] -> out [rows, D] (bf16 or fp32). Replaces modal_rd/kv_int8.py:25-26. */
+/*
+ * bb_int8_quantize of a decode step's new K rows and V rows in one launch: xk and xv share the shape and strides,
+ * results to (qk, sk) and (qv, sv). Replaces the per-tensor quantize loop of Int8KVLayer.update
+ * (modal_rd/kv_int8.py:107-111).
+ */
+int bb_int8_quantize_pair(const void* xk, const void* xv, int x_is_f32, int64_t outer, int64_t row_stride, int inner,
+                          int64_t inner_stride, int D, float min_scale, int8_t* qk, void* sk, int8_t* qv, void* sv,
+                          int scale_is_f16, void* stream);
 int bb_int8_dequantize(const int8_t* q, const void* scale, int scale_is_f16, int64_t rows, int D, void* out,
                        int out_is_f32, void* stream);
 

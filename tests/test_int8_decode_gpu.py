@@ -84,3 +84,33 @@ def test_rope_inplace_bitwise(dev):
     y = x.to(dev).transpose(1, 2).contiguous().transpose(1, 2)  # strided [1, H, T, d] view like q_proj output
     rope_inplace(y, cos.to(dev), sin.to(dev))
     assert torch.equal(y.cpu(), rope_host(x, cos, sin))
+
+
+@pytest.mark.parametrize("scale_dtype,f32", [(torch.float16, False), (torch.float32, False), (torch.float32, True)])
+def test_quantize_pair_matches_oracle(scale_dtype, f32, dev):
+    """K and V rows quantised in one launch (bb_int8_quantize_pair) equal the oracle for each tensor, bitwise, into
+    slices of cache buffers; inputs that differ in strides take the two-launch path with the same results."""
+    print(f"case quantize_pair {scale_dtype} f32={f32}", flush=True)
+    from bigger_bird_amd.kv_int8 import quantize_pair
+
+    k, v = _rand((1, 8, 5, 128), 3, 3.0), _rand((1, 8, 5, 128), 4, 0.5)
+    if f32:
+        k, v = k.float(), v.float()
+    kd, vd = k.to(dev)[0].transpose(0, 1), v.to(dev)[0].transpose(0, 1)  # [t, Hkv, d] strided views
+    qk = torch.zeros(20, 8, 128, dtype=torch.int8, device=dev)
+    qv = torch.zeros_like(qk)
+    sk = torch.zeros(20, 8, 1, dtype=scale_dtype, device=dev)
+    sv = torch.zeros_like(sk)
+    rows = slice(7, 12)
+    quantize_pair(kd, vd, (qk[rows], sk[rows]), (qv[rows], sv[rows]), scale_dtype=scale_dtype)
+    for x, q8, s in ((k, qk, sk), (v, qv, sv)):
+        want_q, want16, want32 = oracle.quantize(x[0].transpose(0, 1).contiguous())
+        want_s = want16 if scale_dtype == torch.float16 else want32
+        assert torch.equal(q8[rows].cpu(), want_q)
+        assert torch.equal(s[rows].cpu().float(), want_s.float())
+        assert (q8[:7] == 0).all() and (q8[12:] == 0).all()  # nothing outside the rows
+    # different strides (V contiguous): two launches, same bytes
+    qk2, qv2 = torch.zeros_like(qk), torch.zeros_like(qv)
+    sk2, sv2 = torch.zeros_like(sk), torch.zeros_like(sv)
+    quantize_pair(kd, vd.contiguous(), (qk2[rows], sk2[rows]), (qv2[rows], sv2[rows]), scale_dtype=scale_dtype)
+    assert torch.equal(qk2, qk) and torch.equal(qv2, qv) and torch.equal(sk2, sk) and torch.equal(sv2, sv)

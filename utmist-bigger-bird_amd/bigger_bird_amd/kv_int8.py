@@ -27,22 +27,9 @@ def _scale_flag(scale_dtype):
     raise ValueError("scale dtype must be float16 or float32")
 
 
-def quantize(x, out=None, scale_dtype=torch.float16, min_scale=MIN_SCALE):
-    """[..., d] (bf16 or fp32, rows may be strided) -> int8 [..., d], scales [..., 1]; one row per leading index.
-
-    `out` = (q, s): contiguous tensors to write into (e.g. the next rows of a cache buffer)."""
-    _lib.require_gpu(x, what="quantize")
-    if x.dtype not in (torch.bfloat16, torch.float32):
-        raise ValueError("quantize: bf16 or fp32 input")
+def _rows(x):
+    """x [..., d] as (tensor, outer, inner, outer stride, inner stride) with 16-byte aligned rows (a copy otherwise)."""
     d = x.shape[-1]
-    lead = x.shape[:-1]
-    if out is None:
-        out = (torch.empty(x.shape, device=x.device, dtype=torch.int8),
-               torch.empty(*lead, 1, device=x.device, dtype=scale_dtype))
-    q, s = out
-    if not (q.is_contiguous() and s.is_contiguous()) or q.numel() != x.numel() or s.numel() * d != x.numel():
-        raise ValueError("quantize: out tensors must be contiguous and match x")
-    # rows as (outer, inner) with two strides; anything else is made contiguous first
     if x.ndim >= 3 and x.stride(-1) == 1:
         x3 = x.reshape(-1, x.shape[-2], d) if x.ndim > 3 else x
         if x.ndim > 3 and x3.data_ptr() != x.data_ptr():
@@ -56,10 +43,51 @@ def quantize(x, out=None, scale_dtype=torch.float16, min_scale=MIN_SCALE):
     if x3.data_ptr() % 16 or (so * el) % 16 or (si * el) % 16:
         x3 = x3.contiguous()
         so, si = (x3.stride(0), x3.stride(1)) if x3.ndim == 3 else (x3.stride(0), 0)
-    _lib.check(_lib.lib().bb_int8_quantize(_lib.ptr(x3), int(x.dtype == torch.float32), outer, so, inner, si, d,
-                                           float(min_scale), _lib.ptr(q), _lib.ptr(s), _scale_flag(s.dtype),
-                                           _lib.stream_of(x)))
+    return x3, outer, inner, so, si
+
+
+def _outputs(x, out, scale_dtype):
+    lead = x.shape[:-1]
+    if out is None:
+        out = (torch.empty(x.shape, device=x.device, dtype=torch.int8),
+               torch.empty(*lead, 1, device=x.device, dtype=scale_dtype))
+    q, s = out
+    if not (q.is_contiguous() and s.is_contiguous()) or q.numel() != x.numel() or s.numel() * x.shape[-1] != x.numel():
+        raise ValueError("quantize: out tensors must be contiguous and match x")
     return q, s
+
+
+def quantize(x, out=None, scale_dtype=torch.float16, min_scale=MIN_SCALE):
+    """[..., d] (bf16 or fp32, rows may be strided) -> int8 [..., d], scales [..., 1]; one row per leading index.
+
+    `out` = (q, s): contiguous tensors to write into (e.g. the next rows of a cache buffer)."""
+    _lib.require_gpu(x, what="quantize")
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("quantize: bf16 or fp32 input")
+    q, s = _outputs(x, out, scale_dtype)
+    x3, outer, inner, so, si = _rows(x)
+    _lib.check(_lib.lib().bb_int8_quantize(_lib.ptr(x3), int(x.dtype == torch.float32), outer, so, inner, si,
+                                           x.shape[-1], float(min_scale), _lib.ptr(q), _lib.ptr(s),
+                                           _scale_flag(s.dtype), _lib.stream_of(x)))
+    return q, s
+
+
+def quantize_pair(xk, xv, out_k, out_v, scale_dtype=torch.float16, min_scale=MIN_SCALE):
+    """quantize(xk, out_k) and quantize(xv, out_v) in one launch when the two inputs share shape, dtype and strides
+    (a decode step's new K and V rows); two launches otherwise."""
+    _lib.require_gpu(xk, xv, what="quantize")
+    if xk.dtype not in (torch.bfloat16, torch.float32) or xv.dtype != xk.dtype or xv.shape != xk.shape:
+        return quantize(xk, out_k, scale_dtype, min_scale), quantize(xv, out_v, scale_dtype, min_scale)
+    (qk, sk), (qv, sv) = _outputs(xk, out_k, scale_dtype), _outputs(xv, out_v, scale_dtype)
+    a, b = _rows(xk), _rows(xv)
+    if a[1:] != b[1:] or sk.dtype != sv.dtype:
+        return quantize(xk, (qk, sk), scale_dtype, min_scale), quantize(xv, (qv, sv), scale_dtype, min_scale)
+    _, outer, inner, so, si = a
+    _lib.check(_lib.lib().bb_int8_quantize_pair(
+        _lib.ptr(a[0]), _lib.ptr(b[0]), int(xk.dtype == torch.float32), outer, so, inner, si, xk.shape[-1],
+        float(min_scale), _lib.ptr(qk), _lib.ptr(sk), _lib.ptr(qv), _lib.ptr(sv), _scale_flag(sk.dtype),
+        _lib.stream_of(xk)))
+    return (qk, sk), (qv, sv)
 
 
 def dequantize(q, scale, dtype):
@@ -187,8 +215,8 @@ class Int8KVLayer(DynamicLayer):
             return key_states, value_states
         self._reserve(t)
         rows = slice(self.n, self.n + t)
-        for x, q, s in ((key_states, self.qk, self.sk), (value_states, self.qv, self.sv)):
-            quantize(x[0].transpose(0, 1), out=(q[rows], s[rows]), scale_dtype=self.scale_dtype)
+        quantize_pair(key_states[0].transpose(0, 1), value_states[0].transpose(0, 1), (self.qk[rows], self.sk[rows]),
+                      (self.qv[rows], self.sv[rows]), scale_dtype=self.scale_dtype)
         self.n += t
         if self.fused and t == 1:
             handle = Int8Handle(self, (1, self.qk.shape[1], self.n, self.qk.shape[2]))

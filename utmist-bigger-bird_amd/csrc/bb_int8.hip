@@ -20,12 +20,22 @@ BB_DEV float load_scale(const void* s, int64_t i, int is_f16) {
   return reinterpret_cast<const float*>(s)[i];
 }
 
-// One group of D/8 lanes per row, 8 elements per lane.
+// One group of D/8 lanes per row, 8 elements per lane. blockIdx.y picks one of two (input, int8, scale) sets of the
+// same shape: a decode step quantises its new K row and V row in one launch.
+struct QuantSet {
+  const void* x;
+  int8_t* q;
+  void* s;
+};
+
 template <int D>
-__global__ __launch_bounds__(256) void quantize_kernel(const void* __restrict__ x, int x_is_f32, int64_t rows,
+__global__ __launch_bounds__(256) void quantize_kernel(QuantSet set0, QuantSet set1, int x_is_f32, int64_t rows,
                                                        int64_t row_stride, int inner, int64_t inner_stride,
-                                                       float min_scale, int8_t* __restrict__ qo, void* __restrict__ so,
-                                                       int scale_is_f16) {
+                                                       float min_scale, int scale_is_f16) {
+  const QuantSet& set = blockIdx.y ? set1 : set0;
+  const void* __restrict__ x = set.x;
+  int8_t* __restrict__ qo = set.q;
+  void* __restrict__ so = set.s;
   constexpr int LPR = D / 8;
   constexpr int RPB = 256 / LPR;
   const int lane_in_row = threadIdx.x % LPR;
@@ -551,16 +561,17 @@ __global__ __launch_bounds__(256) void rope_kernel(uint16_t* __restrict__ x, int
 
 hipError_t launch_int8_quantize(const void* x, int x_is_f32, int64_t rows, int64_t row_stride, int inner,
                                 int64_t inner_stride, int D, float min_scale, int8_t* q, void* scale, int scale_is_f16,
-                                hipStream_t stream) {
+                                hipStream_t stream, const void* x1, int8_t* q1, void* scale1) {
   const int64_t total = rows * inner;
   if (total <= 0) return hipSuccess;
   const int rpb = 256 / (D / 8);
-  const unsigned blocks = (unsigned)((total + rpb - 1) / rpb);
+  const dim3 grid((unsigned)((total + rpb - 1) / rpb), x1 ? 2u : 1u);
+  const QuantSet s0{x, q, scale}, s1{x1 ? x1 : x, x1 ? q1 : q, x1 ? scale1 : scale};
   switch (D) {
-    case 32: hipLaunchKernelGGL(quantize_kernel<32>, dim3(blocks), dim3(256), 0, stream, x, x_is_f32, rows, row_stride, inner, inner_stride, min_scale, q, scale, scale_is_f16); break;
-    case 64: hipLaunchKernelGGL(quantize_kernel<64>, dim3(blocks), dim3(256), 0, stream, x, x_is_f32, rows, row_stride, inner, inner_stride, min_scale, q, scale, scale_is_f16); break;
-    case 128: hipLaunchKernelGGL(quantize_kernel<128>, dim3(blocks), dim3(256), 0, stream, x, x_is_f32, rows, row_stride, inner, inner_stride, min_scale, q, scale, scale_is_f16); break;
-    case 256: hipLaunchKernelGGL(quantize_kernel<256>, dim3(blocks), dim3(256), 0, stream, x, x_is_f32, rows, row_stride, inner, inner_stride, min_scale, q, scale, scale_is_f16); break;
+    case 32: hipLaunchKernelGGL(quantize_kernel<32>, grid, dim3(256), 0, stream, s0, s1, x_is_f32, rows, row_stride, inner, inner_stride, min_scale, scale_is_f16); break;
+    case 64: hipLaunchKernelGGL(quantize_kernel<64>, grid, dim3(256), 0, stream, s0, s1, x_is_f32, rows, row_stride, inner, inner_stride, min_scale, scale_is_f16); break;
+    case 128: hipLaunchKernelGGL(quantize_kernel<128>, grid, dim3(256), 0, stream, s0, s1, x_is_f32, rows, row_stride, inner, inner_stride, min_scale, scale_is_f16); break;
+    case 256: hipLaunchKernelGGL(quantize_kernel<256>, grid, dim3(256), 0, stream, s0, s1, x_is_f32, rows, row_stride, inner, inner_stride, min_scale, scale_is_f16); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
