@@ -169,6 +169,15 @@ size_t bb_topk_f32_workspace(int rows, int64_t n);
 int bb_argmax(const void* x, int64_t n, int dtype, int64_t* out, void* stream);
 
 /*
+ * RMSNorm of `rows` rows of x (row stride sx elements, D contiguous 16-bit values, bf16 or fp16 by is_f16) with
+ * weight w [D] into out (row stride so): the arithmetic of transformers' LlamaRMSNorm (fp32 mean of squares,
+ * rsqrt(mean + eps), round to the model dtype, times the weight, round). One launch per call, for the decode step's
+ * input / post-attention / final norms (modal_rd/graph_decode.py:185,200-201, which run the HF modules).
+ */
+int bb_rms_norm(const void* x, int64_t sx, int rows, int D, const void* w, float eps, int is_f16, void* out,
+                int64_t so, void* stream);
+
+/*
  * In-place RoPE on x [B, Hh, T, D] (strides sx[3]) with cos/sin [B, T, D] (strides sc[2]; 0 to broadcast), with
  * the arithmetic of HF apply_rotary_pos_emb on bf16 tensors (bit-identical). Replaces rope_inplace
  * (modal_rd/attention.py:51-60).

@@ -149,3 +149,24 @@ def test_argmax_matches_torch(dev):
         assert argmax_index(x).item() == 0
     x = torch.randn(2, 4097, generator=g).to(torch.bfloat16).to(dev)[:, 1:].reshape(-1)  # offset, unaligned start
     assert argmax_index(x[3:]).item() == x[3:].argmax().item()
+
+
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 4096), (torch.bfloat16, 512), (torch.float16, 4096)])
+def test_rms_norm_matches_hf(dtype, d, dev):
+    """bb_rms_norm against transformers' LlamaRMSNorm: the same arithmetic except the fp32 summation order of the
+    mean of squares, so results agree to one unit in the last place of the model dtype (and mostly bitwise)."""
+    from transformers.models.llama.modeling_llama import LlamaRMSNorm
+
+    from bigger_bird_amd.decode import rms_norm
+
+    g = torch.Generator().manual_seed(6)
+    norm = LlamaRMSNorm(d, eps=1e-5).to(dev, dtype)
+    with torch.no_grad():
+        norm.weight.copy_((1 + 0.1 * torch.randn(d, generator=g)).to(dtype))
+    x = (torch.randn(3, 5, d, generator=g) * 3).to(dtype).to(dev)
+    want = norm(x)
+    got = rms_norm(x, norm.weight, norm.variance_epsilon)
+    diff = (got.float() - want.float()).abs()
+    ulp = want.float().abs() * (2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10) + 1e-30
+    assert (diff <= ulp).all()
+    assert (diff == 0).float().mean() > 0.95

@@ -164,3 +164,19 @@ def argmax_index(x, out=None):
         raise ValueError("argmax_index: out must be an int64 [1] GPU tensor")
     _lib.check(_lib.lib().bb_argmax(_lib.ptr(x), x.shape[0], _ARGMAX_KIND[x.dtype], _lib.ptr(out), _lib.stream_of(x)))
     return out
+
+
+def rms_norm(x, weight, eps):
+    """transformers' LlamaRMSNorm on a 16-bit GPU tensor [..., D] in one launch (fp32 mean of squares,
+    rsqrt(mean + eps), round to x's dtype, times `weight`, round); D % 8 == 0, D <= 8192."""
+    if not x.is_cuda or x.dtype not in (torch.bfloat16, torch.float16) or weight.dtype != x.dtype:
+        raise ValueError("rms_norm needs bf16/fp16 GPU tensors of one dtype")
+    d = x.shape[-1]
+    x2 = x.reshape(-1, d)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    w = weight.contiguous()
+    out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    _lib.check(_lib.lib().bb_rms_norm(_lib.ptr(x2), x2.stride(0), x2.shape[0], d, _lib.ptr(w), float(eps),
+                                      int(x.dtype == torch.float16), _lib.ptr(out), d, _lib.stream_of(x)))
+    return out

@@ -11,6 +11,9 @@ live in GPU tensors, so the step is captured once as a HIP graph (torch.cuda.CUD
   fused decode routing (bigger_bird_route, pooled per KV head) + sparse decode.
 * The greedy choice is a one-workgroup HIP argmax and new K/V rows go in with index_copy_ at the device-side slot:
   the captured step holds no multi-workgroup reduction and no memset node.
+* On a bf16 model the RMSNorms (`bb_rms_norm`, HF LlamaRMSNorm arithmetic) and RoPE (`bb_rope_inplace`, bit-identical
+  to HF apply_rotary_pos_emb) run as one launch each instead of the handful of elementwise launches of the HF
+  modules, which at batch 1 cost more than their arithmetic.
 * With kv_evict the prefill runs on a DynamicCache (evicted layer by layer) and the kept rows are copied into the
   buffers afterwards; otherwise the prefill writes straight into them (BufferLayer), so there is one cache copy.
 * Not supported, as in the reference: the INT8 KV cache, batch > 1, sampling. The reference's compressed-cache
@@ -28,7 +31,8 @@ from transformers import DynamicCache
 from transformers.cache_utils import DynamicLayer
 from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
 
-from .decode import argmax_index, bigger_bird_decode, bigger_bird_route
+from .attention import rope_inplace
+from .decode import argmax_index, bigger_bird_decode, bigger_bird_route, rms_norm
 
 
 class BufferLayer(DynamicLayer):
@@ -130,6 +134,15 @@ class StaticDecoder:
         return bigger_bird_decode(q, K, V, idx, front=c["front"], window=c["window"], scale=attn.scaling,
                                   n=self.length)
 
+    @staticmethod
+    def _norm(module, x):
+        """A Llama RMSNorm module applied to x, in one launch when it is the plain bf16/fp16 module."""
+        w, eps = getattr(module, "weight", None), getattr(module, "variance_epsilon", None)
+        if type(module).__name__.endswith("RMSNorm") and w is not None and eps is not None and w.dtype == x.dtype \
+                and x.dtype in (torch.bfloat16, torch.float16) and x.shape[-1] % 8 == 0 and x.shape[-1] <= 8192:
+            return rms_norm(x, w, eps)
+        return module(x)
+
     def step(self):
         """One greedy token. Every shape is fixed and all state lives in GPU tensors (capturable)."""
         core = self.model.model
@@ -140,17 +153,21 @@ class StaticDecoder:
         for i, layer in enumerate(self.layers):
             attn = layer.self_attn
             base = getattr(attn, "_rd_base", attn)
-            x = layer.input_layernorm(hid)
+            x = self._norm(layer.input_layernorm, hid)
             q = base.q_proj(x).view(1, 1, self.h, self.d).transpose(1, 2)
             k = base.k_proj(x).view(1, 1, self.hk, self.d).transpose(1, 2)
             v = base.v_proj(x).view(1, 1, self.hk, self.d).transpose(1, 2)
-            q, k = apply_rotary_pos_emb(q, k, cos, sin)
+            if q.dtype == torch.bfloat16 and cos.dtype == torch.bfloat16:
+                rope_inplace(q, cos, sin)
+                rope_inplace(k, cos, sin)
+            else:
+                q, k = apply_rotary_pos_emb(q, k, cos, sin)
             self.k[i].index_copy_(1, slot, k[0])
             self.v[i].index_copy_(1, slot, v[0])
             o = self.attention(i, attn, q[0, :, 0])
             hid = hid + base.o_proj(o.reshape(1, 1, -1))
-            hid = hid + layer.mlp(layer.post_attention_layernorm(hid))
-        self.logits = self.model.lm_head(core.norm(hid))[0, -1]
+            hid = hid + layer.mlp(self._norm(layer.post_attention_layernorm, hid))
+        self.logits = self.model.lm_head(self._norm(core.norm, hid))[0, -1]
         nxt = argmax_index(self.logits)
         self.out.index_copy_(0, self.step_i, nxt)
         self.token.copy_(nxt.view(1, 1))

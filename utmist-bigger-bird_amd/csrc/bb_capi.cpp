@@ -520,6 +520,19 @@ int bb_topk_f32(const float* vals, int64_t sv0, int rows, int64_t n, int front, 
                     "bb_topk_f32");
 }
 
+int bb_rms_norm(const void* x, int64_t sx, int rows, int D, const void* w, float eps, int is_f16, void* out,
+                int64_t so, void* stream) {
+  g_err[0] = 0;
+  if (!x || !w || !out) return fail("rms_norm: null argument");
+  if (rows < 0 || D <= 0 || D % 8 || D > 8192) return fail("rms_norm: hidden size %d unsupported", D);
+  if (!aligned(x, 16) || !aligned(w, 16) || !aligned(out, 16) || sx % 8 || so % 8)
+    return fail("rms_norm: rows must be 16-byte aligned");
+  return hip_status(bb::launch_rms_norm(static_cast<const uint16_t*>(x), sx, rows, D, static_cast<const uint16_t*>(w),
+                                        eps, is_f16 ? 1 : 0, static_cast<uint16_t*>(out), so,
+                                        static_cast<hipStream_t>(stream)),
+                    "bb_rms_norm");
+}
+
 int bb_argmax(const void* x, int64_t n, int dtype, int64_t* out, void* stream) {
   g_err[0] = 0;
   if (!x || !out) return fail("argmax: null argument");

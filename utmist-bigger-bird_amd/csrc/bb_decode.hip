@@ -501,6 +501,59 @@ __global__ __launch_bounds__(kAmThreads) void argmax_kernel(const T* __restrict_
   }
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// RMSNorm of a decode step's hidden rows with the arithmetic of HF LlamaRMSNorm on a 16-bit model: x in fp32,
+// r = rsqrt(mean(x^2) + eps), y = round(x r) to the model dtype, out = round(w y). One 256-thread workgroup per
+// row, 8 values per 16-byte load (D % 8 == 0, D <= 8192).
+constexpr int kRnThreads = 256;
+template <bool F16>
+__global__ __launch_bounds__(kRnThreads) void rms_norm_kernel(const uint16_t* __restrict__ x, int64_t sx,
+                                                              const uint16_t* __restrict__ w, int D, float eps,
+                                                              uint16_t* __restrict__ out, int64_t so) {
+  __shared__ float red[kRnThreads / 64];
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const uint16_t* xr = x + (int64_t)row * sx;
+  constexpr int kMaxUnits = 8192 / 8 / kRnThreads;  // 16-byte units per thread at D = 8192
+  u32x4_t xv[kMaxUnits];
+  float ss = 0.0f;
+#pragma unroll
+  for (int u = 0; u < kMaxUnits; ++u) {
+    const int c = (u * kRnThreads + tid) * 8;
+    xv[u] = c < D ? ld16(xr + c) : u32x4_t{0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float f = elem_to_f32<F16>((uint16_t)(xv[u][e >> 1] >> (16 * (e & 1))));
+      ss = fmaf(f, f, ss);
+    }
+  }
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  const float total = red[0] + red[1] + red[2] + red[3];
+  const float r = rsqrtf(total * (1.0f / (float)D) + eps);
+#pragma unroll
+  for (int u = 0; u < kMaxUnits; ++u) {
+    const int c = (u * kRnThreads + tid) * 8;
+    if (c >= D) break;
+    const u32x4_t wv = ld16(w + c);
+    u32x4_t o;
+#pragma unroll
+    for (int e2 = 0; e2 < 4; ++e2) {
+      uint32_t pair = 0;
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb) {
+        const int e = 2 * e2 + hb;
+        const float f = elem_to_f32<F16>((uint16_t)(xv[u][e >> 1] >> (16 * (e & 1))));
+        const float y = elem_to_f32<F16>(f32_to_elem<F16>(f * r));
+        const float wf = elem_to_f32<F16>((uint16_t)(wv[e >> 1] >> (16 * (e & 1))));
+        pair |= (uint32_t)f32_to_elem<F16>(wf * y) << (16 * hb);
+      }
+      o[e2] = pair;
+    }
+    st16(out + (int64_t)row * so + c, o);
+  }
+}
+
 template <int D, int GR, bool F16>
 hipError_t launch_sparse_decode_t(const SparseDecodeParams& p, hipStream_t stream) {
   hipLaunchKernelGGL((sparse_decode_kernel<D, GR, F16>), dim3(p.n_splits, p.rows), dim3(kSdThreads), 0, stream, p);
@@ -574,6 +627,17 @@ hipError_t launch_argmax(const void* x, int64_t n, int kind, bool vec16, int64_t
     hipLaunchKernelGGL((argmax_kernel<uint16_t, 1>), dim3(1), dim3(kAmThreads), 0, stream,
                        static_cast<const uint16_t*>(x), n, kind, out);
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_rms_norm(const uint16_t* x, int64_t sx, int rows, int D, const uint16_t* w, float eps, int f16,
+                           uint16_t* out, int64_t so, hipStream_t stream) {
+  if (rows <= 0) return hipSuccess;
+  if (D <= 0 || D % 8 || D > 8192) return hipErrorInvalidValue;
+  if (f16)
+    hipLaunchKernelGGL(rms_norm_kernel<true>, dim3(rows), dim3(kRnThreads), 0, stream, x, sx, w, D, eps, out, so);
+  else
+    hipLaunchKernelGGL(rms_norm_kernel<false>, dim3(rows), dim3(kRnThreads), 0, stream, x, sx, w, D, eps, out, so);
   return hipGetLastError();
 }
 

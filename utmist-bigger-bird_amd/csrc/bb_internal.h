@@ -131,6 +131,9 @@ hipError_t launch_topk_rows(const uint64_t* keys, int rows, int64_t stride, int6
 hipError_t launch_gather_rows(const uint16_t* src, int64_t ss0, int64_t ss1, int64_t n_src, int heads,
                               const int64_t* idx, int64_t si0, int m, int D, uint16_t* dst, int64_t sd0, int64_t sd1,
                               hipStream_t stream);
+// HF LlamaRMSNorm arithmetic on rows of a 16-bit tensor (D % 8 == 0, D <= 8192).
+hipError_t launch_rms_norm(const uint16_t* x, int64_t sx, int rows, int D, const uint16_t* w, float eps, int f16,
+                           uint16_t* out, int64_t so, hipStream_t stream);
 // Index of the largest element of x [n] (kind 0 fp32, 1 bf16, 2 fp16; vec16: 16-byte aligned), to out[0].
 hipError_t launch_argmax(const void* x, int64_t n, int kind, bool vec16, int64_t* out, hipStream_t stream);
 hipError_t launch_f32_keys(const float* vals, int64_t sv0, int rows, int64_t n, uint64_t* keys, hipStream_t stream);
