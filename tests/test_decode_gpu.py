@@ -28,16 +28,18 @@ def _routes(rows, n, front, window, r, seed):
     return torch.stack([front + torch.randperm(n - window - front, generator=g)[:r] for _ in range(rows)])
 
 
-@pytest.mark.parametrize("n,front,window,routed,pooled,splits,dtype", [
-    (4096, 64, 1024, 256, True, None, torch.bfloat16),
-    (4096, 64, 1024, 256, False, None, torch.bfloat16),
-    (20000, 64, 4096, 512, True, 7, torch.float16),
-    (20000, 16, 333, 1000, False, 1, torch.bfloat16),
-    (70000, 64, 16384, 512, True, None, torch.bfloat16),
+@pytest.mark.parametrize("n,front,window,routed,pooled,splits,dtype,d,hk", [
+    (4096, 64, 1024, 256, True, None, torch.bfloat16, 128, 8),
+    (4096, 64, 1024, 256, False, None, torch.bfloat16, 128, 8),
+    (20000, 64, 4096, 512, True, 7, torch.float16, 128, 8),
+    (20000, 16, 333, 1000, False, 1, torch.bfloat16, 128, 8),
+    (70000, 64, 16384, 512, True, None, torch.bfloat16, 128, 8),
+    (9000, 32, 2048, 300, True, None, torch.bfloat16, 64, 4),     # head_dim 64, 8 query heads per KV head
+    (9000, 32, 2048, 300, False, 3, torch.float16, 64, 16),       # head_dim 64, 2 query heads per KV head
 ])
-def test_sparse_decode_matches_oracle(n, front, window, routed, pooled, splits, dtype, dev):
-    print(f"case sparse_decode n={n} pooled={pooled} splits={splits} {dtype}", flush=True)
-    h, hk, d = 32, 8, 128
+def test_sparse_decode_matches_oracle(n, front, window, routed, pooled, splits, dtype, d, hk, dev):
+    print(f"case sparse_decode n={n} pooled={pooled} splits={splits} {dtype} d={d} hk={hk}", flush=True)
+    h = 32
     k, v = _cache(n, hk, d, dtype, 0)
     g = torch.Generator().manual_seed(1)
     q = torch.randn(h, d, generator=g).to(dtype)
@@ -97,15 +99,17 @@ def test_rejects_short_cache(dev):
         bigger_bird_decode(q.float(), k, k, torch.zeros(8, 4, dtype=torch.long, device=dev), front=8, window=8)
 
 
-@pytest.mark.parametrize("cap,n,front,window,routed,dtype,device_n", [
-    (5000, 5000, 64, 1024, 256, torch.bfloat16, False),
-    (40000, 40000, 64, 4096, 1024, torch.bfloat16, False),
-    (40000, 33333, 16, 1000, 512, torch.float16, True),
-    (131072, 131072, 64, 1024, 1024, torch.bfloat16, False),
+@pytest.mark.parametrize("cap,n,front,window,routed,dtype,device_n,d,hk", [
+    (5000, 5000, 64, 1024, 256, torch.bfloat16, False, 128, 8),
+    (40000, 40000, 64, 4096, 1024, torch.bfloat16, False, 128, 8),
+    (40000, 33333, 16, 1000, 512, torch.float16, True, 128, 8),
+    (131072, 131072, 64, 1024, 1024, torch.bfloat16, False, 128, 8),
+    (12000, 11000, 32, 2048, 400, torch.bfloat16, True, 64, 4),   # head_dim 64, 8 query heads per KV head
+    (12000, 12000, 32, 2048, 400, torch.float16, False, 64, 32),  # one query head per KV head
 ])
-def test_route_matches_oracle(cap, n, front, window, routed, dtype, device_n, dev):
-    print(f"case route cap={cap} n={n} device_n={device_n} {dtype}", flush=True)
-    h, hk, d = 32, 8, 128
+def test_route_matches_oracle(cap, n, front, window, routed, dtype, device_n, d, hk, dev):
+    print(f"case route cap={cap} n={n} device_n={device_n} {dtype} d={d} hk={hk}", flush=True)
+    h = 32
     g = torch.Generator().manual_seed(0)
     k = (torch.randn(hk, cap, d, generator=g) * 2).to(dtype)
     k[:, n:] = 50
