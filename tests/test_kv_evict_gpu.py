@@ -110,3 +110,39 @@ def test_topk_columns_float_bins(case, dev):
         vals[:, ::7] = float("nan")
     got = topk_columns(vals.to(dev), budget, front=front, tail=tail).cpu()
     assert torch.equal(got, _topk_ref(vals, budget, front, tail))
+
+
+def test_evict_options_match_torch_topk(dev, monkeypatch):
+    """kv_evict with its tuning options (evict_keep, evict_pool / evict_pool_back span pooling, evict_obs exact
+    scoring with mean and max pooling, evict_window, evict_full_layers; modal_rd/attention.py:226-259): the kept
+    positions and the compacted caches equal those of the same policy with torch's topk + sort in place of the HIP
+    top-k and torch's gather in place of the HIP row gather."""
+    print("case kv_evict_options", flush=True)
+    from bigger_bird_amd import attention as rd
+
+    def torch_topk(vals, budget, *, front=0, tail=0):
+        seg = vals[:, front:vals.shape[1] - tail]
+        return (seg.topk(budget, dim=-1).indices + front).sort(-1).values.to(torch.int32)
+
+    def torch_gather(x, idx):
+        return x.gather(1, idx[:, :, None].expand(-1, -1, x.shape[-1]))
+
+    torch.manual_seed(5)
+    ids = torch.randint(0, 512, (1, N), device=dev)
+    model = _tiny(dev)
+    for opts in (dict(evict_keep=150, evict_pool=3, evict_pool_back=1, evict_window=128, evict_full_layers=1),
+                 dict(evict_obs=16, evict_obs_max=True, evict_pool=2),
+                 dict(evict_obs=8)):
+        install(model, "rd", kv_evict=True, **KW, **opts)
+        _, got = _prefill(model, ids)
+        kept = [layer.self_attn.kept.clone() for layer in model.model.layers]
+        with monkeypatch.context() as m:
+            m.setattr(rd, "topk_columns", torch_topk)
+            m.setattr(rd, "gather_rows", torch_gather)
+            _, want = _prefill(model, ids)
+        for i, layer in enumerate(model.model.layers):
+            assert torch.equal(kept[i], layer.self_attn.kept), (opts, i)
+            assert torch.equal(got.layers[i].keys, want.layers[i].keys), (opts, i)
+            assert torch.equal(got.layers[i].values, want.layers[i].values), (opts, i)
+        if opts.get("evict_full_layers"):
+            assert kept[0].shape[-1] == N and got.layers[0].keys.shape[-2] == N
