@@ -95,3 +95,41 @@ def test_config4_batch_sampled_rows(dev):
             err = (o[pr[:, 0], pr[:, 1]].double() - ref).abs()
             print(f"config4 b={b} {what}: max_abs={err.max().item():.3e} mean_abs={err.mean().item():.3e}", flush=True)
             assert err.max().item() < 2e-2 and err.mean().item() < 2e-3
+
+
+def test_vertical_scope_matches_oracle(dev):
+    """vertical_scope (modal_rd/attention.py:183-196): routed keys only for the query chunks of `scope_chunk` rows that
+    end inside the last `vertical_scope` rows; earlier chunks attend sink + window only. The oracle gets the same
+    per-chunk route lists ([H, groups, K], -1 for inactive chunks) and route_chunk = scope_chunk."""
+    print("case prefill vertical_scope", flush=True)
+    g = golden_routes.case("config1")
+    H, Hkv, T, d = g["H"], g["Hkv"], g["T"], g["d"]
+    cfg = dict(sink=64, window=2048, vertical=128, exact_tail=256, vertical_scope=3000, scope_chunk=1024)
+    attn = RDAttention(_base(H, Hkv, d), **cfg)
+    gen = torch.Generator().manual_seed(9)
+    v = torch.randn(1, Hkv, T, d, generator=gen).to(torch.bfloat16)
+    q, k = g["q"], g["k"]
+    with torch.inference_mode():
+        out = attn.sparse_prefill(q.to(dev), k.to(dev), v.to(dev))
+    torch.cuda.synchronize()
+    routes = attn.last_routes.cpu()
+    assert torch.equal(routes, g["routes"])
+    chunk, groups = 1024, T // 1024
+    active = [(c + 1) * chunk > T - cfg["vertical_scope"] for c in range(groups)]
+    assert active == [False] * 5 + [True] * 3
+    idx = torch.stack([routes if a else torch.full_like(routes, -1) for a in active], 1)  # [H, groups, K]
+    r = cfg["exact_tail"]
+    rows = torch.tensor([100, 2047, 2048, 4095, 4200, 5119, 5120, 5121, 6000, 7000, T - r - 1, T - r, T - 1])
+    pairs = torch.stack([torch.arange(H).repeat_interleave(rows.numel()), rows.repeat(H)], -1)
+    main, tail = pairs[pairs[:, 1] < T - r], pairs[pairs[:, 1] >= T - r]
+    G = H // Hkv
+    ref_main = oracle.attn_rows(q[0], k[0], v[0], idx, main, front=64, window=2048, num_heads=H, kv_groups=G,
+                                scale=d ** -0.5, route_chunk=chunk)
+    none = torch.full((H, 1, 1), -1, dtype=torch.int32)
+    ref_tail = oracle.attn_rows(q[0], k[0], v[0], none, tail, front=0, window=T, num_heads=H, kv_groups=G,
+                                scale=d ** -0.5)
+    o = out[0].cpu()
+    for what, pr, ref in (("main", main, ref_main), ("tail", tail, ref_tail)):
+        err = (o[pr[:, 0], pr[:, 1]].double() - ref).abs()
+        print(f"vertical_scope {what}: max_abs={err.max().item():.3e} mean_abs={err.mean().item():.3e}", flush=True)
+        assert err.max().item() < 2e-2 and err.mean().item() < 2e-3
