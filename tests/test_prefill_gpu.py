@@ -98,7 +98,7 @@ def test_config4_batch_sampled_rows(dev):
 
 
 def test_vertical_scope_matches_oracle(dev):
-    """vertical_scope (modal_rd/attention.py:183-196): routed keys only for the query chunks of `scope_chunk` rows that
+    """vertical_scope (modal_rd/attention.py:187-196): routed keys only for the query chunks of `scope_chunk` rows that
     end inside the last `vertical_scope` rows; earlier chunks attend sink + window only. The oracle gets the same
     per-chunk route lists ([H, groups, K], -1 for inactive chunks) and route_chunk = scope_chunk."""
     print("case prefill vertical_scope", flush=True)
