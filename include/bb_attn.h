@@ -112,6 +112,20 @@ int bb_decode(const void* q, int64_t sq, const int8_t* k8, const void* ks, const
 size_t bb_decode_workspace(int64_t n, int H, int Hkv, int D);
 
 /*
+ * bb_decode without a workspace argument and without any allocation: the split partials go to a static device array
+ * of bb_decode_noalloc_max_bytes() bytes (4 MiB) inside the library, one per GPU, held until the process ends. No
+ * counterpart in the reference: this is for callers that cannot allocate (code under HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc). Same arguments, kernels and results as bb_decode; a call whose partials
+ * (H * splits * (D + 2) * 4 bytes, see bb_decode_workspace) exceed the array returns BB_EINVAL. The array of the
+ * current device is used, so `stream` must belong to the current device. Calls that overlap on one GPU (two
+ * streams, or two host threads) share the array and race; calls ordered on one stream are safe.
+ */
+int bb_decode_noalloc(const void* q, int64_t sq, const int8_t* k8, const void* ks, const int8_t* v8, const void* vs,
+                      int scale_is_f16, const void* kb, const int64_t* skb, const void* vb, const int64_t* svb,
+                      int64_t n, int H, int Hkv, int D, float scale, void* out, int64_t so, void* stream);
+size_t bb_decode_noalloc_max_bytes(void);
+
+/*
  * Split-K sparse decode of one query token over a bf16 (is_f16 = 0) or fp16 KV cache. Every route row attends its
  * virtual key list front | window | routed: position j for j < front, n - window + i for the window, idx[row][i]
  * for the routed keys; positions outside [0, n) are skipped. Replaces bigger_bird_decode

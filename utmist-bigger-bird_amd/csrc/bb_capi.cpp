@@ -6,6 +6,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 #include "bb_attn.h"
 #include "bb_internal.h"
@@ -94,6 +95,34 @@ FlashSchedule flash_schedule(int BH, int64_t T, int64_t N, int num_heads, int kv
     }
   }
   return s;
+}
+
+// Static scratch of bb_decode_noalloc: the split partials [H][n_splits][D + 2] fp32 live in this array instead of a
+// caller workspace. Every GPU the library runs on holds its own copy for the life of the process; calls that overlap
+// on one GPU share it and race. Host code never passes `decode_scratch_mem` itself (that name is a host-side
+// stand-in): its device address comes from hipGetSymbolAddress, looked up once per device with that device current.
+constexpr size_t kDecodeScratchBytes = (size_t)4 << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char decode_scratch_mem[kDecodeScratchBytes];
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxDevices] = {};
+
+// Device address of the current device's scratch (looked up on the first call on that device).
+int decode_scratch(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e, "bb_decode_noalloc: hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail("decode_noalloc: device %d beyond the %d supported", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_addr[dev]) {
+    void* addr = nullptr;
+    e = hipGetSymbolAddress(&addr, HIP_SYMBOL(decode_scratch_mem));
+    if (e != hipSuccess) return hip_status(e, "bb_decode_noalloc: hipGetSymbolAddress");
+    if (!addr) return fail("decode_noalloc: no device address for the scratch array");
+    g_scratch_addr[dev] = addr;
+  }
+  *out = g_scratch_addr[dev];
+  return BB_OK;
 }
 
 }  // namespace
@@ -328,10 +357,10 @@ size_t bb_decode_workspace(int64_t n, int H, int Hkv, int D) {
   return bb::decode_workspace_bytes(H, D, decode_splits(n, Hkv));
 }
 
-int bb_decode(const void* q, int64_t sq, const int8_t* k8, const void* ks, const int8_t* v8, const void* vs,
-              int scale_is_f16, const void* kb, const int64_t* skb, const void* vb, const int64_t* svb, int64_t n,
-              int H, int Hkv, int D, float scale, void* out, int64_t so, void* ws, size_t ws_bytes, void* stream) {
-  g_err[0] = 0;
+// Argument checks and launch descriptor shared by bb_decode and bb_decode_noalloc (p.part is left to the caller).
+static int decode_params(const void* q, int64_t sq, const int8_t* k8, const void* ks, const int8_t* v8, const void* vs,
+                         int scale_is_f16, const void* kb, const int64_t* skb, const void* vb, const int64_t* svb,
+                         int64_t n, int H, int Hkv, int D, float scale, void* out, int64_t so, bb::DecodeParams& p) {
   if (!q || !out) return fail("decode: null argument");
   if (n <= 0) return fail("decode: empty cache");
   if (H <= 0 || Hkv <= 0 || H % Hkv) return fail("q [H,D] and k/v [Hkv,N,D] must match");
@@ -345,7 +374,6 @@ int bb_decode(const void* q, int64_t sq, const int8_t* k8, const void* ks, const
   if (!int8 && (!aligned(kb, 16) || !aligned(vb, 16) || skb[0] % 8 || skb[1] % 8 || svb[0] % 8 || svb[1] % 8))
     return fail("decode: misaligned cache");
   if (!(scale > 0.0f)) return fail("scale must be positive");
-  bb::DecodeParams p;
   memset(&p, 0, sizeof(p));
   p.q = static_cast<const uint16_t*>(q);
   p.sq = sq;
@@ -360,11 +388,40 @@ int bb_decode(const void* q, int64_t sq, const int8_t* k8, const void* ks, const
   p.c = (float)((double)scale * 1.4426950408889634);
   p.out = static_cast<uint16_t*>(out);
   p.so = so;
-  const size_t need = bb::decode_workspace_bytes(H, D, decode_splits(n, Hkv));
+  return BB_OK;
+}
+
+int bb_decode(const void* q, int64_t sq, const int8_t* k8, const void* ks, const int8_t* v8, const void* vs,
+              int scale_is_f16, const void* kb, const int64_t* skb, const void* vb, const int64_t* svb, int64_t n,
+              int H, int Hkv, int D, float scale, void* out, int64_t so, void* ws, size_t ws_bytes, void* stream) {
+  g_err[0] = 0;
+  bb::DecodeParams p;
+  const int rc = decode_params(q, sq, k8, ks, v8, vs, scale_is_f16, kb, skb, vb, svb, n, H, Hkv, D, scale, out, so, p);
+  if (rc != BB_OK) return rc;
+  const size_t need = bb::decode_workspace_bytes(H, D, p.n_splits);
   if (!ws || ws_bytes < need) return fail("workspace of %zu bytes required", need);
   p.part = static_cast<float*>(ws);
-  (void)G;
   return hip_status(bb::launch_decode(p, static_cast<hipStream_t>(stream)), "bb_decode");
+}
+
+size_t bb_decode_noalloc_max_bytes(void) { return kDecodeScratchBytes; }
+
+int bb_decode_noalloc(const void* q, int64_t sq, const int8_t* k8, const void* ks, const int8_t* v8, const void* vs,
+                      int scale_is_f16, const void* kb, const int64_t* skb, const void* vb, const int64_t* svb,
+                      int64_t n, int H, int Hkv, int D, float scale, void* out, int64_t so, void* stream) {
+  g_err[0] = 0;
+  bb::DecodeParams p;
+  const int rc = decode_params(q, sq, k8, ks, v8, vs, scale_is_f16, kb, skb, vb, svb, n, H, Hkv, D, scale, out, so, p);
+  if (rc != BB_OK) return rc;
+  const size_t need = bb::decode_workspace_bytes(H, D, p.n_splits);
+  if (need > kDecodeScratchBytes)
+    return fail("decode_noalloc: %zu bytes of split partials exceed the static scratch of %zu bytes (use bb_decode "
+                "with a workspace)", need, (size_t)kDecodeScratchBytes);
+  void* scratch_ptr = nullptr;
+  const int src = decode_scratch(&scratch_ptr);
+  if (src != BB_OK) return src;
+  p.part = static_cast<float*>(scratch_ptr);
+  return hip_status(bb::launch_decode(p, static_cast<hipStream_t>(stream)), "bb_decode_noalloc");
 }
 
 // Key chunks of the split-K decode kernels, as kernels/bigger_bird_decode.py:84-88 and bigger_bird_route.py:91-94
