@@ -329,8 +329,7 @@ def graph_decode_leg(model, ids, steps=32):
     print(f"graph decode: {graph_ms:.3f} ms/token (eager step {eager_ms:.3f})", file=sys.stderr, flush=True)
     del dec
     from bigger_bird_amd import graph_decode as gd
-    gd._DECODERS.clear()
-    torch.cuda.empty_cache()
+    gd.release()
     return res
 
 

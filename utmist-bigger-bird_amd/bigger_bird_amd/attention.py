@@ -121,7 +121,7 @@ class RDAttention(nn.Module):
         self.evict_full_layers, self.evict_window = evict_full_layers, evict_window
         self.evict_obs_max, self.evict_pool_back = evict_obs_max, evict_pool_back
         self.last_routes = None
-        self.kept = None            # [Hkv, m] absolute positions left in the cache after eviction
+        self.kept = None  # after kv_evict: int64 [Hkv, m], per KV head the sequence positions of the rows kept
         self._col = None
 
     def forward(self, hidden_states, position_embeddings=None, attention_mask=None, past_key_values=None, **kwargs):
@@ -133,7 +133,8 @@ class RDAttention(nn.Module):
             raise NotImplementedError("RDAttention on MI355X is inference-only (no autograd through HIP kernels)")
         q, k = rope_inplace(q, *position_embeddings), rope_inplace(k, *position_embeddings)
         if past_key_values is not None:
-            k, v = past_key_values.update(k, v, self.layer_idx)
+            # the cache kwargs tell an Int8KVLayer that this module takes fused decode handles (exact_attention)
+            k, v = past_key_values.update(k, v, self.layer_idx, {"bb_attend": True})
         n = k.shape[-2]
         if b != 1:
             raise ValueError("batch size 1 only")

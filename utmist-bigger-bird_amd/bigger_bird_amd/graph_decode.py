@@ -1,28 +1,30 @@
-"""HIP-graph greedy decode for Llama-family models at batch 1 (drop-in for modal_rd/graph_decode.py).
+"""Greedy batch-1 decode of Llama-family models as a replayed HIP graph (drop-in for modal_rd/graph_decode.py).
 
-Prefill is an ordinary eager forward through the installed attention modules. Decode is one token step assembled by
-hand (embedding -> every decoder layer -> final norm -> lm_head -> greedy choice) over fixed-capacity per-layer K/V
-buffers [Hkv, capacity, d]. The cache length, the write slot, the RoPE position, the input token and the step counter
-live in GPU tensors, so the step is captured once as a HIP graph (torch.cuda.CUDAGraph) and replayed per token.
+Public surface kept from the reference: `StaticDecoder` (buffer_cache / load / feed / step / capture / run /
+generated / rewind / generate), `BufferLayer`, `decoder_for`, `graph_prefill` and `graph_generate`, with the same
+generate / EOS / rewind / feed protocol. The design is this package's own:
 
-* Attention per layer: split-K flash decoding over the filled buffer (bigger_bird_decode with front=0,
-  window=capacity and no routes, reading the length on the GPU), as the reference does for its dense / v3 / v3 +
-  eviction arms. `sparse_decode={"front", "window", "routed"}` switches the RDAttention layers that are not dense to
-  fused decode routing (bigger_bird_route, pooled per KV head) + sparse decode.
-* The greedy choice is a one-workgroup HIP argmax and new K/V rows go in with index_copy_ at the device-side slot:
-  the captured step holds no multi-workgroup reduction and no memset node.
-* On a bf16 model the RMSNorms (`bb_rms_norm`, HF LlamaRMSNorm arithmetic) and RoPE (`bb_rope_inplace`, bit-identical
-  to HF apply_rotary_pos_emb) run as one launch each instead of the handful of elementwise launches of the HF
-  modules, which at batch 1 cost more than their arithmetic.
-* With kv_evict the prefill runs on a DynamicCache (evicted layer by layer) and the kept rows are copied into the
-  buffers afterwards; otherwise the prefill writes straight into them (BufferLayer), so there is one cache copy.
-* Not supported, as in the reference: the INT8 KV cache, batch > 1, sampling. The reference's compressed-cache
-  (turbo) and host-embedding variants are not part of this package.
-* Generation runs in blocks of `block` steps and stops after the block that produced an EOS; the cache is rewound to
-  just after the input that produced it, so a further turn can be appended (`feed` + `run`).
-* The decoder's tensors are ordinary tensors (made outside inference mode) and the step runs and is captured under
-  no_grad: a capture under inference mode would leave the CUDA generator's graph state as inference tensors, and any
-  later capture outside inference mode would then fail.
+* Memory. Every layer's K and V live in one arena [layers, 2, Hkv, capacity, d] (one allocation, sized once for the
+  prompt plus the tokens to generate). Without kv_evict the prefill writes its K/V rows straight into the arena
+  through `BufferLayer`; with kv_evict the prefill runs on a DynamicCache (each layer evicts right after its prefill)
+  and `load` copies the kept rows in.
+* State. A 5-slot int64 control block on the GPU holds (n, position, token, produced, slot): the filled cache rows,
+  the RoPE position and id of the next input token, the number of tokens produced since `load`, and the cache row
+  the next token's K/V go to. A step advances the block with two vector adds, so every launch in it has a fixed
+  shape and reads its varying values from device memory: the step is captured once and replayed per token.
+* Step (one token through the model): embedding; per layer RMSNorm -> one fused QKV projection (the q, k and v
+  weights concatenated once at construction when they are plain bias-free Linear layers of one dtype) -> RoPE on q and
+  k in place -> the new K and V row into the arena at `slot` (one index_copy_) -> attention -> o_proj, residual ->
+  RMSNorm -> MLP, residual; final norm, lm_head, greedy token by a one-workgroup HIP argmax written straight into
+  the control block.
+* Attention per layer: split-K flash decoding over the filled rows (bigger_bird_decode with front 0, window =
+  capacity, no routes, length read on the GPU). `sparse_decode={"front", "window", "routed"}` switches the
+  non-dense RDAttention layers to fused decode routing (bigger_bird_route, pooled per KV head) + sparse decode.
+* On bf16 / fp16 models the RMSNorms run as one bb_rms_norm launch each and RoPE as bb_rope_inplace (bit-identical to
+  HF apply_rotary_pos_emb): at batch 1 the HF modules' elementwise launches cost more than their arithmetic.
+* A captured step holds no memset node and no multi-workgroup reduction of torch's (those have given wrong results
+  on replays after the first on these boxes).
+* Not supported: the INT8 KV cache, batch > 1, sampling (as in the reference).
 """
 import time
 
@@ -34,276 +36,334 @@ from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
 from .attention import rope_inplace
 from .decode import argmax_index, bigger_bird_decode, bigger_bird_route, rms_norm
 
+# Control block: slot indices and the per-step / per-token increments.
+N, POS, TOK, MADE, SLOT = range(5)
+_CLAIM = (1, 0, 0, 0, 0)    # a step first grows the cache by the row it is about to write (at SLOT)
+_ADVANCE = (0, 1, 0, 1, 1)  # ... and ends one position further, with one more token produced and the next free row
+_UNDO = (1, 1, 0, 1, 1)     # one consumed token taken back (rewind)
+
 
 class BufferLayer(DynamicLayer):
-    """Cache layer over preallocated [Hkv, capacity, d] buffers: prefill rows are written in place and `keys` /
-    `values` are [1, Hkv, n, d] views of the filled part (modal_rd/graph_decode.py:40-57)."""
+    """Cache layer over decoder-owned buffers kb / vb [Hkv, capacity, d]: update writes the new rows in place and
+    keys / values are [1, Hkv, filled, d] views (modal_rd/graph_decode.py:40-57)."""
 
     def __init__(self, kb, vb):
         super().__init__()
-        self.kb, self.vb, self.n = kb, vb, 0
-        self.dtype, self.device, self.is_initialized = kb.dtype, kb.device, True
-        self._views()
+        self._kb, self._vb = kb, vb
+        self.dtype, self.device = kb.dtype, kb.device
+        self.is_initialized = True
+        self._expose(0)
 
-    def _views(self):
-        self.keys, self.values = self.kb[None, :, :self.n], self.vb[None, :, :self.n]
+    def _expose(self, filled):
+        self.filled = filled
+        self.keys = self._kb.narrow(1, 0, filled).unsqueeze(0)
+        self.values = self._vb.narrow(1, 0, filled).unsqueeze(0)
+
+    def lazy_initialization(self, key_states, value_states, *args, **kwargs):
+        pass
 
     def update(self, key_states, value_states, *args, **kwargs):
-        end = self.n + key_states.shape[-2]
-        if end > self.kb.shape[1]:
+        t = key_states.shape[-2]
+        if self.filled + t > self._kb.shape[1]:
             raise ValueError("graph decode buffer too small for the prompt")
-        self.kb[:, self.n:end].copy_(key_states[0])
-        self.vb[:, self.n:end].copy_(value_states[0])
-        self.n = end
-        self._views()
+        self._kb.narrow(1, self.filled, t).copy_(key_states[0])
+        self._vb.narrow(1, self.filled, t).copy_(value_states[0])
+        self._expose(self.filled + t)
         return self.keys, self.values
 
 
-class StaticDecoder:
-    """Fixed-shape one-token decoder over per-layer K/V buffers (modal_rd/graph_decode.py:65-269)."""
+def _plain_linear(m):
+    return isinstance(m, torch.nn.Linear) and m.bias is None
 
-    _STATE = ("length", "position", "token", "step_i")
+
+class _LayerPlan:
+    """What a decode step needs of one decoder layer, resolved once."""
+
+    def __init__(self, layer, attn, sparse):
+        base = getattr(attn, "_rd_base", attn)
+        self.layer, self.base, self.sparse = layer, base, sparse
+        self.scaling = getattr(attn, "scaling", None) or base.scaling
+        projs = (base.q_proj, base.k_proj, base.v_proj)
+        self.qkv_w = None
+        if all(_plain_linear(p) for p in projs) and len({p.weight.dtype for p in projs}) == 1:
+            with torch.inference_mode(False), torch.no_grad():
+                self.qkv_w = torch.cat([p.weight for p in projs], 0)
+
+
+class StaticDecoder:
+    """Fixed-shape one-token decoder over one K/V arena, capturable as a HIP graph (modal_rd/graph_decode.py:65-269).
+
+    Attributes: `length`, `position`, `token` ([1, 1]) and `step_i` are views of the control block; `logits` is the
+    last step's logits [vocab]; `k[i]` / `v[i]` are layer i's [Hkv, capacity, d] buffers; `sparse[i]` tells whether
+    layer i decodes sparsely."""
 
     def __init__(self, model, capacity, sparse_decode=None):
+        if sparse_decode is not None and set(sparse_decode) != {"front", "window", "routed"}:
+            raise ValueError("sparse_decode takes front, window and routed")
         cfg = model.config
         self.model, self.capacity = model, int(capacity)
-        self.layers = model.model.layers
+        self.core = model.model
         self.h, self.hk = cfg.num_attention_heads, cfg.num_key_value_heads
-        self.d = getattr(self.layers[0].self_attn, "head_dim", cfg.hidden_size // self.h)
+        first = self.core.layers[0].self_attn
+        self.d = getattr(first, "head_dim", cfg.hidden_size // self.h)
         w = model.lm_head.weight
         dev = w.device
         dt = w.dtype if w.dtype in (torch.float16, torch.bfloat16) else torch.bfloat16
-        with torch.inference_mode(False):
-            self.k = [torch.zeros(self.hk, self.capacity, self.d, device=dev, dtype=dt) for _ in self.layers]
-            self.v = [torch.zeros_like(x) for x in self.k]
-            self.length = torch.zeros(1, dtype=torch.long, device=dev)     # filled cache slots
-            self.position = torch.zeros(1, dtype=torch.long, device=dev)   # RoPE position of the next input token
-            self.token = torch.zeros(1, 1, dtype=torch.long, device=dev)   # next input token
-            self.step_i = torch.zeros(1, dtype=torch.long, device=dev)     # tokens produced since load
-            self.out = torch.zeros(self.capacity, dtype=torch.long, device=dev)
-            self.no_routes = torch.empty(self.hk, 0, dtype=torch.long, device=dev)
-        self.logits = None   # last step's logits [vocab] (inside the graph's memory once captured)
-        self.graph = None
         self.sparse_cfg = dict(sparse_decode) if sparse_decode else None
-        if self.sparse_cfg and set(self.sparse_cfg) != {"front", "window", "routed"}:
-            raise ValueError("sparse_decode takes front, window and routed")
-        self.sparse = [bool(self.sparse_cfg) and not getattr(layer.self_attn, "dense", True) for layer in self.layers]
+        layers = list(self.core.layers)
+        with torch.inference_mode(False):
+            self.arena = torch.zeros(len(layers), 2, self.hk, self.capacity, self.d, device=dev, dtype=dt)
+            self.ctl = torch.zeros(5, dtype=torch.int64, device=dev)
+            self._claim, self._advance, self._undo = (torch.tensor(v, dtype=torch.int64, device=dev)
+                                                      for v in (_CLAIM, _ADVANCE, _UNDO))
+            self.out = torch.zeros(self.capacity, dtype=torch.int64, device=dev)
+            self.no_routes = torch.empty(self.hk, 0, dtype=torch.int32, device=dev)
+            # views made here, outside inference mode, so that later in-place updates are allowed in either mode
+            self.k = [self.arena[i, 0] for i in range(len(layers))]
+            self.v = [self.arena[i, 1] for i in range(len(layers))]
+            self.length, self.position = self.ctl[N:N + 1], self.ctl[POS:POS + 1]
+            self.step_i, self._slot = self.ctl[MADE:MADE + 1], self.ctl[SLOT:SLOT + 1]
+            self.token = self.ctl[TOK:TOK + 1].view(1, 1)
+            self._token_flat = self.ctl[TOK:TOK + 1]
+        self.plans = [_LayerPlan(layer, layer.self_attn,
+                                 bool(self.sparse_cfg) and not getattr(layer.self_attn, "dense", True))
+                      for layer in layers]
+        self.sparse = [p.sparse for p in self.plans]
+        self.logits = None
+        self.graph = None
 
+    # ---- loading a prefilled cache ----
     def buffer_cache(self):
-        """A DynamicCache whose layers write the prefill's K/V straight into this decoder's buffers."""
+        """A DynamicCache whose layers write the prefill's K/V straight into this decoder's arena."""
         cache = DynamicCache(config=self.model.config)
-        cache.layers = [BufferLayer(k, v) for k, v in zip(self.k, self.v)]
+        cache.layers = [BufferLayer(kb, vb) for kb, vb in zip(self.k, self.v)]
         return cache
 
     @torch.no_grad()
     def load(self, cache, prompt_len, first_token):
-        """Take a prefilled cache (a `buffer_cache()` or a DynamicCache, e.g. after eviction) and set the first
-        input token; `prompt_len` is the RoPE position of that token."""
-        layers = getattr(cache, "layers", None)
-        if not layers or not all(isinstance(x, DynamicLayer) and torch.is_tensor(x.keys) for x in layers) \
-                or layers[0].keys.dtype != self.k[0].dtype:
+        """Take a prefilled cache (this decoder's `buffer_cache()`, or a bf16/fp16 DynamicCache, e.g. after kv_evict)
+        and make `first_token` the next input at RoPE position `prompt_len`."""
+        layers = list(getattr(cache, "layers", None) or [])
+        tensors = all(isinstance(x, DynamicLayer) and torch.is_tensor(x.keys) for x in layers)
+        if len(layers) != len(self.plans) or not tensors or layers[0].keys.dtype != self.arena.dtype:
             raise ValueError("graph decode needs a BF16/FP16 DynamicCache (INT8 KV cache is not supported)")
-        m = layers[0].keys.shape[-2]
+        rows = {x.keys.shape[-2] for x in layers}
+        if len(rows) != 1:
+            raise ValueError("all layers must hold the same number of cached keys")
+        m = rows.pop()
         if m >= self.capacity:
             raise ValueError("graph decode buffer too small")
-        for i, layer in enumerate(layers):
-            if layer.keys.shape[-2] != m:
-                raise ValueError("all layers must hold the same number of cached keys")
-            if layer.keys.data_ptr() != self.k[i].data_ptr():
-                self.k[i][:, :m].copy_(layer.keys[0])
-                self.v[i][:, :m].copy_(layer.values[0])
-        self.length.fill_(m)
-        self.position.fill_(prompt_len)
-        self.step_i.zero_()
-        self.feed(first_token)
+        for i, x in enumerate(layers):
+            if x.keys.data_ptr() == self.k[i].data_ptr() and x.values.data_ptr() == self.v[i].data_ptr():
+                continue  # already in the arena (BufferLayer)
+            self.k[i].narrow(1, 0, m).copy_(x.keys[0])
+            self.v[i].narrow(1, 0, m).copy_(x.values[0])
+        state = torch.tensor([m, int(prompt_len), int(first_token), 0, m], dtype=torch.int64)
+        self.ctl.copy_(state)
 
     @torch.no_grad()
     def feed(self, token):
-        """Set the next input token (a prompt continuation or a generated token)."""
+        """Make `token` the next input (a prompt continuation or a token already produced)."""
         self.token.fill_(int(token))
 
-    def attention(self, i, attn, q):
-        """q [H, d] of the new token, whose K/V row is already in the buffers -> [H, d]."""
+    # ---- the step ----
+    def _norm(self, module, x):
+        """An RMSNorm module on x: one bb_rms_norm launch for the plain bf16/fp16 Llama module, else the module."""
+        w, eps = getattr(module, "weight", None), getattr(module, "variance_epsilon", None)
+        fast = (type(module).__name__.endswith("RMSNorm") and w is not None and eps is not None
+                and w.dtype == x.dtype and x.dtype in (torch.bfloat16, torch.float16)
+                and x.shape[-1] % 8 == 0 and x.shape[-1] <= 8192)
+        return rms_norm(x, w, eps) if fast else module(x)
+
+    def _qkv(self, plan, x):
+        """Projections of the normed input x [1, 1, hidden]: q [1, H, 1, d], k and v [1, Hkv, 1, d], and, with the
+        fused projection, the [2, Hkv, 1, d] view of its K and V part (so RoPE on k in place also lands there)."""
+        h, hk, d = self.h, self.hk, self.d
+        if plan.qkv_w is not None:
+            y = torch.nn.functional.linear(x, plan.qkv_w)[0, 0]
+            q, k, v = y.split((h * d, hk * d, hk * d))
+            kv = y[h * d:].view(2, hk, 1, d)
+        else:
+            q, k, v = (p(x)[0, 0] for p in (plan.base.q_proj, plan.base.k_proj, plan.base.v_proj))
+            kv = None
+        return q.view(1, h, 1, d), k.view(1, hk, 1, d), v.view(1, hk, 1, d), kv
+
+    def _attend(self, i, plan, q):
+        """q [H, d] of the new token (its K/V row already in the arena) -> [H, d]."""
         K, V = self.k[i], self.v[i]
-        if not self.sparse[i]:
-            return bigger_bird_decode(q, K, V, self.no_routes, front=0, window=self.capacity, scale=attn.scaling,
+        if not plan.sparse:
+            return bigger_bird_decode(q, K, V, self.no_routes, front=0, window=self.capacity, scale=plan.scaling,
                                       n=self.length)
         c = self.sparse_cfg
-        idx = bigger_bird_route(q, K, c["routed"], front=c["front"], window=c["window"], scale=attn.scaling,
+        idx = bigger_bird_route(q, K, c["routed"], front=c["front"], window=c["window"], scale=plan.scaling,
                                 n=self.length)
-        return bigger_bird_decode(q, K, V, idx, front=c["front"], window=c["window"], scale=attn.scaling,
+        return bigger_bird_decode(q, K, V, idx, front=c["front"], window=c["window"], scale=plan.scaling,
                                   n=self.length)
 
-    @staticmethod
-    def _norm(module, x):
-        """A Llama RMSNorm module applied to x, in one launch when it is the plain bf16/fp16 module."""
-        w, eps = getattr(module, "weight", None), getattr(module, "variance_epsilon", None)
-        if type(module).__name__.endswith("RMSNorm") and w is not None and eps is not None and w.dtype == x.dtype \
-                and x.dtype in (torch.bfloat16, torch.float16) and x.shape[-1] % 8 == 0 and x.shape[-1] <= 8192:
-            return rms_norm(x, w, eps)
-        return module(x)
-
     def step(self):
-        """One greedy token. Every shape is fixed and all state lives in GPU tensors (capturable)."""
-        core = self.model.model
-        hid = core.embed_tokens(self.token)
-        cos, sin = core.rotary_emb(hid, self.position[None])
-        slot = self.length.clone()
-        self.length.add_(1)
-        for i, layer in enumerate(self.layers):
-            attn = layer.self_attn
-            base = getattr(attn, "_rd_base", attn)
-            x = self._norm(layer.input_layernorm, hid)
-            q = base.q_proj(x).view(1, 1, self.h, self.d).transpose(1, 2)
-            k = base.k_proj(x).view(1, 1, self.hk, self.d).transpose(1, 2)
-            v = base.v_proj(x).view(1, 1, self.hk, self.d).transpose(1, 2)
+        """One greedy token: fixed shapes, all varying state read from the control block (capturable)."""
+        hid = self.core.embed_tokens(self.token)
+        cos, sin = self.core.rotary_emb(hid, self.position.view(1, 1))
+        self.ctl.add_(self._claim)
+        for i, plan in enumerate(self.plans):
+            layer = plan.layer
+            q, k, v, kv = self._qkv(plan, self._norm(layer.input_layernorm, hid))
             if q.dtype == torch.bfloat16 and cos.dtype == torch.bfloat16:
                 rope_inplace(q, cos, sin)
                 rope_inplace(k, cos, sin)
             else:
                 q, k = apply_rotary_pos_emb(q, k, cos, sin)
-            self.k[i].index_copy_(1, slot, k[0])
-            self.v[i].index_copy_(1, slot, v[0])
-            o = self.attention(i, attn, q[0, :, 0])
-            hid = hid + base.o_proj(o.reshape(1, 1, -1))
+                kv = None
+            if kv is None:
+                kv = torch.stack((k[0], v[0]))
+            self.arena[i].index_copy_(2, self._slot, kv)
+            o = self._attend(i, plan, q[0, :, 0])
+            hid = hid + plan.base.o_proj(o.reshape(1, 1, -1))
             hid = hid + layer.mlp(self._norm(layer.post_attention_layernorm, hid))
-        self.logits = self.model.lm_head(self._norm(core.norm, hid))[0, -1]
-        nxt = argmax_index(self.logits)
-        self.out.index_copy_(0, self.step_i, nxt)
-        self.token.copy_(nxt.view(1, 1))
-        self.position.add_(1)
-        self.step_i.add_(1)
+        self.logits = self.model.lm_head(self._norm(self.core.norm, hid))[0, -1]
+        argmax_index(self.logits, out=self._token_flat)
+        self.out.index_copy_(0, self.step_i, self._token_flat)
+        self.ctl.add_(self._advance)
 
-    def _state(self):
-        return [getattr(self, n).clone() for n in self._STATE]
-
-    def _restore(self, saved):
-        for n, x in zip(self._STATE, saved):
-            getattr(self, n).copy_(x)
-
+    # ---- graph capture and running ----
     def capture(self):
-        """Record `step` as a HIP graph; the decoder state is restored around the warm-up and capture runs. Runs
-        outside inference mode (even when called inside it), under no_grad."""
+        """Record `step` as a HIP graph. Two warm-up steps run first on a side stream (allocator pools and library
+        handles settle outside the capture); the control block is put back after them and after the capture. Runs
+        outside inference mode, under no_grad: a capture under inference mode leaves the CUDA generator's graph
+        state as inference tensors, and every later capture outside it would fail."""
         with torch.inference_mode(False), torch.no_grad():
-            saved = self._state()
+            before = self.ctl.clone()
             side = torch.cuda.Stream()
             side.wait_stream(torch.cuda.current_stream())
             with torch.cuda.stream(side):
-                for _ in range(2):  # library handles and allocator pools warmed outside the capture
+                for _ in range(2):
                     self.step()
-                    self._restore(saved)
+                    self.ctl.copy_(before)
             torch.cuda.current_stream().wait_stream(side)
-            self.graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(self.graph):
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
                 self.step()
-            self._restore(saved)
+            self.ctl.copy_(before)
+            self.graph = graph
 
     @torch.no_grad()
     def run(self, steps, graph=True):
-        """Advance `steps` tokens, each consuming the current input token and producing the next. Raises ValueError
-        (one host read of the length) when the buffers cannot hold `steps` more rows."""
+        """Advance `steps` tokens (each consumes the next input and produces the one after). Raises ValueError (one
+        host read of the length) when the arena cannot hold `steps` more rows."""
         if int(self.length) + steps > self.capacity:
             raise ValueError("graph decode buffer full: build the decoder with a larger capacity")
         if graph and self.graph is None:
             self.capture()
+        go = self.graph.replay if graph else self.step
         for _ in range(steps):
-            if graph:
-                self.graph.replay()
-            else:
-                self.step()
+            go()
 
     def generated(self):
-        """Every token produced since `load`, as a Python list."""
+        """The tokens produced since `load`, as a list."""
         return self.out[:int(self.step_i)].tolist()
 
     @torch.no_grad()
     def rewind(self, r):
-        """Drop the last `r` consumed tokens from the cache (steps run past an EOS)."""
-        for t in (self.length, self.position, self.step_i):
-            t.sub_(r)
+        """Take back the last `r` consumed tokens (their cache rows, positions and produced tokens)."""
+        self.ctl.sub_(self._undo * int(r))
 
     @torch.no_grad()
     def generate(self, max_steps, eos=(), block=8, graph=True):
-        """Greedy steps until a produced token is in `eos` (kept) or `max_steps`; returns (tokens, steps run). The
-        cache is rewound to end right after the input that produced the EOS, which becomes the next input."""
-        eos = set(eos)
-        start, steps, toks = int(self.step_i), 0, []
-        while steps < max_steps:
-            b = min(block, max_steps - steps)
+        """Greedy steps, `block` at a time, until a produced token is in `eos` or `max_steps` ran; returns
+        (tokens through the first EOS, steps run). Steps run past that EOS are taken back, and the EOS becomes the
+        next input, so the cache ends right after the input that produced it (as eager decoding stopping on EOS)."""
+        stop = frozenset(int(t) for t in eos)
+        first = int(self.step_i)
+        ran = 0
+        while ran < max_steps:
+            b = min(block, max_steps - ran)
             self.run(b, graph)
-            new = self.out[start + steps:start + steps + b].tolist()
-            steps += b
-            toks += new
-            if eos.intersection(new):
+            ran += b
+            if stop and not stop.isdisjoint(self.out[first + ran - b:first + ran].tolist()):
                 break
-        cut = next((j + 1 for j, t in enumerate(toks) if t in eos), len(toks))
-        if steps > cut:
-            self.rewind(steps - cut)
-            self.feed(toks[cut - 1])
-        return toks[:cut], steps
+        made = self.out[first:first + ran].tolist()
+        keep = next((j + 1 for j, t in enumerate(made) if t in stop), ran)
+        if keep < ran:
+            self.rewind(ran - keep)
+            self.feed(made[keep - 1])
+        return made[:keep], ran
 
 
-_DECODERS = {}
+class _Cache:
+    """At most one live decoder, reused while the installed attention modules and the sparse config stay the same
+    and its capacity suffices (graph capture is the expensive part to keep)."""
+
+    def __init__(self):
+        self.key, self.dec = None, None
+
+    @staticmethod
+    def key_of(model, sparse_decode):
+        modules = tuple(id(layer.self_attn) for layer in model.model.layers)
+        return modules, tuple(sorted(sparse_decode.items())) if sparse_decode else ()
+
+    def release(self):
+        if self.dec is not None:
+            self.key, self.dec = None, None
+            torch.cuda.empty_cache()
+
+    def get(self, model, capacity, sparse_decode):
+        key = self.key_of(model, sparse_decode)
+        if self.dec is not None and (self.key != key or self.dec.capacity < capacity):
+            self.release()
+        if self.dec is None:
+            self.key, self.dec = key, StaticDecoder(model, capacity, sparse_decode)
+        return self.dec
+
+    def holds(self, model, sparse_decode):
+        return self.dec is not None and self.key == self.key_of(model, sparse_decode)
 
 
-def _evicting(model):
-    return any(getattr(layer.self_attn, "kv_evict", False) for layer in model.model.layers)
+_CACHE = _Cache()
 
 
-def _key(model, sparse_decode=None):
-    sd = tuple(sorted(sparse_decode.items())) if sparse_decode else ()
-    return tuple(id(layer.self_attn) for layer in model.model.layers) + (sd,)
+def release():
+    """Drop the cached decoder (its arena and graph) and return the memory to the allocator."""
+    _CACHE.release()
 
 
 def decoder_for(model, capacity, sparse_decode=None):
-    """The cached decoder of the installed attention modules, rebuilt when it is too small."""
-    key = _key(model, sparse_decode)
-    dec = _DECODERS.get(key)
-    if dec is None or dec.capacity < capacity:
-        _DECODERS.clear()
-        dec = None
-        torch.cuda.empty_cache()
-        dec = _DECODERS[key] = StaticDecoder(model, capacity, sparse_decode)
-    return dec
+    """The cached decoder for the installed attention modules, rebuilt when it is too small or for other modules."""
+    return _CACHE.get(model, int(capacity), sparse_decode)
 
 
 @torch.inference_mode()
 def graph_prefill(model, input_ids, max_new, headroom=4096, position_offset=0, sparse_decode=None):
-    """Eager prefill of input_ids [1, n], loaded into a (cached) StaticDecoder. Returns (decoder, prefill output,
-    prefill seconds); the argmax of the output's last logits is already the decoder's next input. The capacity
-    covers the kept cache plus `max_new` tokens; `headroom` extra slots let slightly longer prompts reuse the graph."""
+    """Eager prefill of input_ids [1, n] loaded into the cached decoder; returns (decoder, prefill output, prefill
+    seconds). The argmax of the output's last logits is already the decoder's next input. The decoder holds the
+    kept cache rows plus `max_new` tokens and `headroom` spare rows (so slightly longer prompts reuse the graph)."""
     n = input_ids.shape[1]
-    key = _key(model, sparse_decode)
-    if _DECODERS and key not in _DECODERS:  # another arm's buffers: free them before this prefill
-        _DECODERS.clear()
-        torch.cuda.empty_cache()
-    if _evicting(model):
+    if not _CACHE.holds(model, sparse_decode):
+        release()  # another arm's arena: free it before this prefill
+    evicting = any(getattr(layer.self_attn, "kv_evict", False) for layer in model.model.layers)
+    spare = max_new + 8 + headroom
+    if evicting:
         dec, cache = None, DynamicCache(config=model.config)
     else:
-        dec = decoder_for(model, n + max_new + 8, sparse_decode)
+        dec = decoder_for(model, n + spare, sparse_decode)
         cache = dec.buffer_cache()
     pos = torch.arange(position_offset, position_offset + n, device=input_ids.device)[None]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     out = model(input_ids=input_ids, position_ids=pos, past_key_values=cache, use_cache=True, logits_to_keep=1)
     torch.cuda.synchronize()
-    prefill_s = time.perf_counter() - t0
+    seconds = time.perf_counter() - t0
     if dec is None:
-        m = cache.layers[0].keys.shape[-2]
-        dec = _DECODERS.get(key)
-        if dec is None or dec.capacity < m + max_new + 8:
-            dec = decoder_for(model, m + max_new + 8 + headroom, sparse_decode)
+        dec = decoder_for(model, cache.layers[0].keys.shape[-2] + spare, sparse_decode)
     dec.load(cache, position_offset + n, out.logits[0, -1].argmax().item())
-    del cache
-    return dec, out, prefill_s
+    return dec, out, seconds
 
 
 @torch.inference_mode()
 def graph_generate(model, input_ids, max_new, eos=(), block=8, sparse_decode=None):
-    """Greedy generation (like model.generate(do_sample=False, max_new_tokens=max_new)) with a HIP-graph decode.
-    Returns (token ids incl. a final EOS, prefill seconds, decode seconds, decode steps run)."""
+    """Greedy generation (as model.generate(do_sample=False, max_new_tokens=max_new)) with the graph decode. Returns
+    (token ids through a final EOS, prefill seconds, decode seconds, decode steps run)."""
     dec, out, prefill_s = graph_prefill(model, input_ids, max_new, sparse_decode=sparse_decode)
-    first = out.logits[0, -1].argmax().item()
+    first = int(dec.token)
     del out
     if first in set(eos) or max_new <= 1:
         return [first], prefill_s, 0.0, 0

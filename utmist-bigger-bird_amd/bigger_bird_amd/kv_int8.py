@@ -2,12 +2,14 @@
 
 Symmetric per token and KV head: scale = max(absmax / 127, MIN_SCALE) in fp32, q = round_half_even(x / scale)
 clamped to [-127, 127], scale stored as fp16 (the reference's format; `scale_dtype=torch.float32` keeps fp32).
-Buffers are token-major [capacity, Hkv, d] (scales [capacity, Hkv, 1]) so the valid rows are one contiguous block and
-decode appends into spare capacity (GROW rows at a time).
+Rows are stored token-major [capacity, Hkv, d] (scales [capacity, Hkv, 1]), so the valid rows are one contiguous
+block that the decode kernels stream and that a new token is appended to.
 
-Decode differs from the reference in one place, by design: instead of dequantising the whole cache to bf16 and
-running SDPA each step, `update` returns handles whose `attend` runs bb_decode, which reads the int8 rows and their
-scales once (no dequantised copy). The math is the same exact attention over the dequantised values.
+Decode differs from the reference in one place, by design. A consumer that opts in (RDAttention passes
+`{"bb_attend": True}` as the cache kwargs of its update call) receives handles whose `attend` runs bb_decode over
+the int8 rows and their scales, with no dequantised copy. Every other consumer, e.g. a stock HF attention module,
+receives dequantised [1, Hkv, n, d] tensors as from the reference's layer. The math is the same exact attention
+over the dequantised values.
 """
 import torch
 from transformers import DynamicCache
@@ -149,106 +151,153 @@ class Int8Handle:
     def attend(self, q, scale):
         """q [1, H, 1, d] -> [1, H, 1, d] exact attention over the layer's whole int8 cache."""
         layer = self.turbo
-        n = layer.n
-        out = decode_int8(q[0, :, 0], layer.qk, layer.sk, layer.qv, layer.sv, n, scale)
+        k, v = layer.store_k, layer.store_v
+        out = decode_int8(q[0, :, 0], k.q, k.s, v.q, v.s, layer.n, scale)
         return out[None, :, None]
 
 
+class _Int8Rows:
+    """One cached tensor (K or V) as int8 rows [capacity, Hkv, d] plus scales [capacity, Hkv, 1]; rows [0, n) are
+    valid (n is kept by the owning layer). Capacity comes in whole GROW-row steps past what is needed."""
+
+    def __init__(self, hkv, d, rows, scale_dtype, device):
+        cap = rows + GROW
+        self.q = torch.empty(cap, hkv, d, dtype=torch.int8, device=device)
+        self.s = torch.empty(cap, hkv, 1, dtype=scale_dtype, device=device)
+
+    @property
+    def capacity(self):
+        return self.q.shape[0]
+
+    def ensure(self, n, need):
+        """Make room for rows [n, need), keeping rows [0, n)."""
+        if need <= self.capacity:
+            return
+        cap = need + GROW
+        q = torch.empty(cap, *self.q.shape[1:], dtype=self.q.dtype, device=self.q.device)
+        s = torch.empty(cap, *self.s.shape[1:], dtype=self.s.dtype, device=self.s.device)
+        q[:n].copy_(self.q[:n])
+        s[:n].copy_(self.s[:n])
+        self.q, self.s = q, s
+
+    def rows(self, a, b):
+        return self.q[a:b], self.s[a:b]
+
+    def dequantized(self, n, dtype):
+        """[1, Hkv, n, d] in `dtype` (a fresh tensor, viewed head-major like the reference's cache)."""
+        return dequantize(self.q[:n], self.s[:n], dtype).transpose(0, 1)[None]
+
+    def nbytes(self, n):
+        return n * (self.q[0].numel() * self.q.element_size() + self.s[0].numel() * self.s.element_size())
+
+
 class Int8KVLayer(DynamicLayer):
-    """HF cache layer with int8 storage (modal_rd/kv_int8.py:49-133). Batch size 1 only."""
+    """HF cache layer with int8 K/V storage (modal_rd/kv_int8.py:49-133), batch size 1.
+
+    * prefill (the first update): the K/V are quantised into fresh row stores and the full-precision inputs are
+      returned, so prefill attention is unchanged;
+    * later updates quantise the new rows (K and V in one launch) into spare capacity and return the dequantised
+      cache, or, for a one-token step whose consumer opts in, Int8Handle stand-ins for the fused decode;
+    * assigning `keys` / `values` (kv_evict compacting the cache) re-quantises the given rows;
+    * `crop(-r)` drops the last r rows.
+    """
 
     scale_dtype = torch.float16
-    fused = True
+    fused = True  # hand handles to consumers that ask for them (cache kwargs {"bb_attend": True})
+
+    def __init__(self):
+        super().__init__()
+        self.store_k = self.store_v = None
+        self.n = 0
 
     def lazy_initialization(self, key_states, value_states, *args, **kwargs):
         self.dtype, self.device = key_states.dtype, key_states.device
-        self.qk = self.qv = self.sk = self.sv = None
+        self.store_k = self.store_v = None
         self.n = 0
         self.is_initialized = True
 
-    def _quantize(self, x):  # [1, Hkv, t, d] -> [t, Hkv, d] int8, [t, Hkv, 1] scales
-        if x.shape[0] != 1:
+    @staticmethod
+    def _token_major(x):
+        """[1, Hkv, t, d] -> a [t, Hkv, d] view."""
+        if x.ndim != 4 or x.shape[0] != 1:
             raise NotImplementedError("Int8KVLayer is batch-size-1 only")
-        return quantize(x[0].transpose(0, 1), scale_dtype=self.scale_dtype)
+        return x[0].transpose(0, 1)
 
-    def _get(self, q, s):  # -> [1, Hkv, n, d] view of the dequantised rows
-        if q is None:
-            return None
-        return dequantize(q[:self.n], s[:self.n], self.dtype).transpose(0, 1)[None]
+    def _fill(self, x):
+        """A new row store holding the quantised rows of x [1, Hkv, t, d]."""
+        rows = self._token_major(x)
+        t, hkv, d = rows.shape
+        store = _Int8Rows(hkv, d, t, self.scale_dtype, x.device)
+        quantize(rows, out=store.rows(0, t), scale_dtype=self.scale_dtype)
+        return store
 
+    # keys / values read back dequantised, as the reference's layer exposes them; assignment re-quantises
     @property
     def keys(self):
-        return self._get(getattr(self, "qk", None), getattr(self, "sk", None))
+        return None if self.store_k is None else self.store_k.dequantized(self.n, self.dtype)
 
     @keys.setter
     def keys(self, x):
         if x is not None and x.numel():
-            self.qk, self.sk = self._quantize(x)
-            self.n = x.shape[-2]
+            self.store_k, self.n = self._fill(x), x.shape[-2]
 
     @property
     def values(self):
-        return self._get(getattr(self, "qv", None), getattr(self, "sv", None))
+        return None if self.store_v is None else self.store_v.dequantized(self.n, self.dtype)
 
     @values.setter
     def values(self, x):
         if x is not None and x.numel():
-            self.qv, self.sv = self._quantize(x)
-            self.n = x.shape[-2]
+            self.store_v, self.n = self._fill(x), x.shape[-2]
 
-    def _reserve(self, t):
-        if self.n + t <= self.qk.shape[0]:
-            return
-
-        def grow(x):
-            return torch.cat([x[:self.n], x.new_empty(max(t, GROW), *x.shape[1:])])
-
-        self.qk, self.sk, self.qv, self.sv = map(grow, (self.qk, self.sk, self.qv, self.sv))
-
-    def update(self, key_states, value_states, *args, **kwargs):
+    def update(self, key_states, value_states, cache_kwargs=None, *args, **kwargs):
         if not self.is_initialized:
             self.lazy_initialization(key_states, value_states)
         t = key_states.shape[-2]
-        if self.qk is None:  # prefill: store quantised, attend in full precision
-            (self.qk, self.sk), (self.qv, self.sv) = self._quantize(key_states), self._quantize(value_states)
+        if self.store_k is None:
+            self.store_k, self.store_v = self._fill(key_states), self._fill(value_states)
             self.n = t
             return key_states, value_states
-        self._reserve(t)
-        rows = slice(self.n, self.n + t)
-        quantize_pair(key_states[0].transpose(0, 1), value_states[0].transpose(0, 1), (self.qk[rows], self.sk[rows]),
-                      (self.qv[rows], self.sv[rows]), scale_dtype=self.scale_dtype)
-        self.n += t
-        if self.fused and t == 1:
-            handle = Int8Handle(self, (1, self.qk.shape[1], self.n, self.qk.shape[2]))
+        start, end = self.n, self.n + t
+        self.store_k.ensure(start, end)
+        self.store_v.ensure(start, end)
+        quantize_pair(self._token_major(key_states), self._token_major(value_states), self.store_k.rows(start, end),
+                      self.store_v.rows(start, end), scale_dtype=self.scale_dtype)
+        self.n = end
+        wants_handle = isinstance(cache_kwargs, dict) and cache_kwargs.get("bb_attend", False)
+        if self.fused and wants_handle and t == 1:
+            handle = Int8Handle(self, (1, self.store_k.q.shape[1], end, self.store_k.q.shape[2]))
             return handle, handle
         return self.keys, self.values
 
     def get_seq_length(self, *args, **kwargs):
-        return 0 if not self.is_initialized or self.qk is None else self.n
+        return self.n if self.is_initialized and self.store_k is not None else 0
 
     def crop(self, tokens_to_remove):
+        if tokens_to_remove > 0:
+            raise NotImplementedError("Int8KVLayer.crop supports negative token counts only")
         if tokens_to_remove < 0 and self.get_seq_length():
             self.n = max(0, self.n + tokens_to_remove)
-        elif tokens_to_remove:
-            raise NotImplementedError("Int8KVLayer.crop supports negative token counts only")
 
     def batch_repeat_interleave(self, repeats):
         raise NotImplementedError("Int8KVLayer is batch-size-1 only")
 
-    batch_select_indices = batch_repeat_interleave
+    def batch_select_indices(self, indices):
+        raise NotImplementedError("Int8KVLayer is batch-size-1 only")
 
     def nbytes(self):
-        """Bytes of the valid rows (spare decode capacity, at most GROW rows, is not counted)."""
-        if self.qk is None:
+        """Bytes held by the valid rows of K and V with their scales; spare capacity is not counted."""
+        if self.store_k is None:
             return 0
-        return sum(t[:self.n].numel() * t.element_size() for t in (self.qk, self.sk, self.qv, self.sv))
+        return self.store_k.nbytes(self.n) + self.store_v.nbytes(self.n)
 
 
 def make_int8_cache(config, fused=True, scale_dtype=torch.float16):
+    """A DynamicCache whose layers are Int8KVLayer (modal_rd/kv_int8.py:136-139). `fused=False` never hands out
+    decode handles, even to consumers that ask for them."""
     cache = DynamicCache(config=config)
-    n_layers = config.get_text_config(decoder=True).num_hidden_layers
     layers = []
-    for _ in range(n_layers):
+    for _ in range(config.get_text_config(decoder=True).num_hidden_layers):
         layer = Int8KVLayer()
         layer.fused, layer.scale_dtype = fused, scale_dtype
         layers.append(layer)
