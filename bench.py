@@ -47,6 +47,8 @@ def parse_args():
     ap.add_argument("--no-decode", action="store_true", help="skip the decode legs (INT8 exact decode of BASELINE configs[4], sparse decode)")
     ap.add_argument("--full-model", action="store_true",
                     help="only run the full-model prefill (BASELINE configs[2]): random-init Llama-3-8B, sparse and exact arms")
+    ap.add_argument("--no-full-model", action="store_true",
+                    help="skip the full-model leg (BASELINE configs[2]) that the default run adds after the headline")
     ap.add_argument("--no-short-arm", action="store_true",
                     help="skip the B=4, T=32768 sparse-vs-dense leg (BASELINE configs[3])")
     ap.add_argument("--copy-probe", action="store_true",
@@ -102,6 +104,16 @@ def main_traffic():
         return None
 
 
+def cpu_model():
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(q, k, v, routes, cfg, args):
     """The reference's CPU path (routes() op sequence + bigger_bird_flash_ref masked-dense semantics), restated in
     torch CPU ops by the oracle, timed on a bounded sample and scaled to one layer:
@@ -132,10 +144,65 @@ def cpu_baseline(q, k, v, routes, cfg, args):
     t_attn = t_blocks / blocks * (H / G) * (T / 64)
     ms = (t_routes + t_attn) * 1e3
     return {"value": round(ms, 1), "unit": "ms/layer", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": (f"torch CPU restatement of the reference path: routes for 1 of {Hkv} KV groups (x{Hkv}) + "
                        f"masked-dense attention for {blocks} blocks of 64 rows x {G} heads over all {T} keys, "
                        f"scaled x{(H // G) * (T // 64) / blocks:.0f}; extrapolated, measured "
                        f"{(t_routes / Hkv + t_blocks):.1f} s")}
+
+
+def config1_side_by_side(dev, seed):
+    """BASELINE configs[0] (T=8192, {64, 2048, 128, 256}, 32 q / 8 KV heads, d=128) timed in full on both sides: the
+    CPU restatement of the reference's path (oracle.routes_reference_order for every head, then the masked-dense
+    oracle.flash_ref over every row, outputs and int32 routes) on the host cores, and RDAttention.sparse_prefill on
+    the GPU, on the same inputs. The routes are compared (set-exact), and the GPU output against the CPU one."""
+    import torch
+    import oracle
+    from bigger_bird_amd import RDAttention
+    from bigger_bird_amd.synth import attended_pairs, make_inputs
+
+    T, H, Hkv, d = 8192, 32, 8, 128
+    cfg = dict(sink=64, window=2048, vertical=128, exact_tail=256)
+    inp = make_inputs(T, H, Hkv, d, seed=seed + 11, sink=cfg["sink"], window=cfg["window"], device=dev, rng="device")
+    q, k, v = inp["q"], inp["k"], inp["v"]
+    attn = RDAttention(stub_base(H, Hkv, d), **cfg)
+    with torch.inference_mode():
+        out = attn.sparse_prefill(q, k, v)
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(5):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            attn.sparse_prefill(q, k, v)
+            b.record()
+            torch.cuda.synchronize()
+            best = min(best, a.elapsed_time(b))
+    routes_gpu = attn.last_routes.cpu()
+    qc, kc, vc = q[0].cpu(), k[0].cpu(), v[0].cpu()
+    t0 = time.perf_counter()
+    routes_cpu = oracle.routes_reference_order(q.cpu(), k.cpu(), num_heads=H, num_kv_heads=Hkv, sink=cfg["sink"],
+                                               window=cfg["window"], budget=cfg["vertical"], scaling=d ** -0.5)
+    t_routes = time.perf_counter() - t0
+    r = cfg["exact_tail"]
+    t0 = time.perf_counter()
+    main = oracle.flash_ref(qc, kc, vc, routes_cpu.view(H, 1, -1), front=cfg["sink"], window=cfg["window"],
+                            num_heads=H, kv_groups=H // Hkv, scale=d ** -0.5)
+    none = torch.full((H, 1, 1), -1, dtype=torch.int32)
+    tail = oracle.flash_ref(qc[:, T - r:], kc, vc, none, front=0, window=T, num_heads=H, kv_groups=H // Hkv,
+                            scale=d ** -0.5)
+    main[:, T - r:] = tail
+    t_attn = time.perf_counter() - t0
+    err = (out[0].float().cpu() - main.float()).abs()
+    cpu_ms = (t_routes + t_attn) * 1e3
+    flop = 4 * d * attended_pairs(T, H, cfg["sink"], cfg["window"], routes_gpu, r)
+    return {"workload": "BASELINE configs[0]: T=8192, 32q/8kv heads, d=128, cfg {64, 2048, 128, 256}; routes + "
+                        "sparse attention + exact tail, whole layer on both sides",
+            "cpu_ms": round(cpu_ms, 1), "cpu_routes_ms": round(t_routes * 1e3, 1),
+            "cpu_threads": torch.get_num_threads(), "cpu_model": cpu_model(),
+            "gpu_ms": round(best, 3), "speedup": round(cpu_ms / best, 1),
+            "gpu_effective_tflops": round(flop / (best * 1e-3) / 1e12, 1),
+            "routes_equal": bool(torch.equal(routes_gpu, routes_cpu)),
+            "max_abs_gpu_vs_cpu": round(err.max().item(), 5), "mean_abs_gpu_vs_cpu": round(err.mean().item(), 6)}
 
 
 def decode_leg(dev, seed):
@@ -285,9 +352,18 @@ def short_arm_leg(dev, seed):
             best = min(best, a.elapsed_time(b))
         return best
 
+    from bigger_bird_amd.synth import attended_pairs
+
     res = {"workload": "BASELINE configs[3]: B=4, T=32768, 32q/8kv heads, d=128, cfg {64, 4096, 512, 256}"}
     with torch.inference_mode():
-        res["sparse_ms"] = round(timed(lambda: attn.sparse_prefill(q, k, v)), 3)
+        sparse_ms = timed(lambda: attn.sparse_prefill(q, k, v))
+        res["sparse_ms"] = round(sparse_ms, 3)
+        # 4 d FLOP per attended (q, k) pair, pairs counted from each batch element's actual routes
+        flop = sum(4 * d * attended_pairs(T, H, cfg["sink"], cfg["window"], attn.last_routes[b].cpu(),
+                                          cfg["exact_tail"]) for b in range(B))
+        res["flop"] = flop
+        res["effective_tflops"] = round(flop / (sparse_ms * 1e-3) / 1e12, 1)
+        res["frac"] = round(res["effective_tflops"] / PEAK_BF16_TFLOPS, 4)
         try:
             from torch.nn.attention import SDPBackend, sdpa_kernel
             kr = k.repeat_interleave(H // Hkv, dim=1)
@@ -296,6 +372,8 @@ def short_arm_leg(dev, seed):
                 res["dense_ms"] = round(timed(lambda: F.scaled_dot_product_attention(q, kr, vr, is_causal=True,
                                                                                       scale=d ** -0.5)), 3)
             res["speedup"] = round(res["dense_ms"] / res["sparse_ms"], 2)
+            dense_flop = B * 4 * d * H * T * (T + 1) // 2
+            res["dense_effective_tflops"] = round(dense_flop / (res["dense_ms"] * 1e-3) / 1e12, 1)
             res["dense"] = "torch SDPA flash backend (ROCm), causal, K/V repeated to 32 heads"
         except RuntimeError as e:  # no flash backend for this shape: report the sparse time only
             res["dense_ms"] = None
@@ -524,6 +602,11 @@ def main():
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(q, k, v, routes, cfg, args)
+        result["cpu_baseline"]["config1_full_layer"] = config1_side_by_side(dev, args.seed)
+    if not args.no_full_model:
+        del q, k, v, inp, attn
+        torch.cuda.empty_cache()
+        result["full_model"] = full_model_leg(dev, args.seed, T)
     print(json.dumps(result), flush=True)
 
 
