@@ -121,6 +121,53 @@ def test_identity_attention_is_exact(dev):
         assert torch.equal(out[head], v[head // 4]), head
 
 
+@pytest.mark.parametrize("n,masked", [(524288, False), (995993, False), (1048576, False), (1048576, True)])
+def test_identity_long_strided(n, masked, dev):
+    """modal_rd/check_long_indexing.py:32-56: identity attention (front 0, window 1) on model-strided views
+    (q [n, 32, 128], k / v [n, 8, 128] permuted to head-major) past the 2^31-byte mark of a KV head's K rows: every
+    output row must equal its V row exactly. An all-true token mask routes the call to the generic kernel
+    (flash_kernel), so both kernels' 64-bit addressing is exercised at 1048576 tokens."""
+    print(f"case identity_long n={n} masked={masked}", flush=True)
+    h, hk, d = 32, 8, 128
+    q = torch.zeros((n, h, d), device=dev, dtype=torch.bfloat16).permute(1, 0, 2)
+    k = torch.zeros((n, hk, d), device=dev, dtype=torch.bfloat16).permute(1, 0, 2)
+    pattern = (torch.arange(n, device=dev) % 97).float()[:, None] + 0.25 * torch.arange(hk, device=dev)[None, :]
+    v = pattern[:, :, None].expand(n, hk, d).to(torch.bfloat16).permute(1, 0, 2)
+    del pattern
+    idx = torch.empty(h, 1, 0, dtype=torch.int32, device=dev)
+    mask = torch.ones(1, n, dtype=torch.bool, device=dev) if masked else None
+    out = bigger_bird_flash(q, k, v, idx, front=0, window=1, num_heads=h, kv_groups=4, token_mask=mask)
+    torch.cuda.synchronize()
+    assert out.stride() == (d, h * d, 1)
+    for head in range(h):
+        assert torch.equal(out[head], v[head // 4]), (n, head)
+
+
+def test_million_token_rows_match_oracle(dev):
+    """A full sparse layer at 1048576 tokens on model-strided views ({64, 16384}, 512 routes per head): sampled rows
+    of one KV group (heads 28..31), including the last rows, against the float64 oracle."""
+    n, h, hk, d, front, window, rk = 1048576, 32, 8, 128, 64, 16384, 512
+    print(f"case million_rows n={n}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(61)
+    q = torch.randn((n, h, d), device=dev, generator=g).to(torch.bfloat16).permute(1, 0, 2)
+    k = torch.randn((n, hk, d), device=dev, generator=g).to(torch.bfloat16).permute(1, 0, 2)
+    v = torch.randn((n, hk, d), device=dev, generator=g).to(torch.bfloat16).permute(1, 0, 2)
+    gc = torch.Generator().manual_seed(62)
+    idx = torch.stack([torch.randperm(n - window - front, generator=gc)[:rk].sort().values + front
+                       for _ in range(h)]).to(torch.int32)
+    out = bigger_bird_flash(q, k, v, idx.view(h, 1, rk).to(dev), front=front, window=window, num_heads=h, kv_groups=4,
+                            scale=d ** -0.5)
+    torch.cuda.synchronize()
+    heads = slice(28, 32)
+    rows = torch.cat([torch.tensor([0, 63, 64, window - 1, window, window + 1, n // 2, n - 65, n - 64, n - 2, n - 1]),
+                      idx[28:32, ::64].reshape(-1).long() + window, torch.randint(0, n, (24,), generator=gc)])
+    pairs = torch.stack([torch.arange(4).repeat_interleave(rows.numel()), rows.repeat(4)], -1)
+    ref = oracle.attn_rows(q[heads].cpu(), k[7:8].cpu(), v[7:8].cpu(), idx[heads].view(4, 1, rk), pairs, front=front,
+                           window=window, num_heads=4, kv_groups=4, scale=d ** -0.5)
+    got = out[heads].cpu()[pairs[:, 0], pairs[:, 1]]
+    _check(got, ref, "million_rows")
+
+
 def test_route_groups_and_token_mask(dev):
     """Per-query route groups (vertical_scope layout) and a padding mask (tests/test_bigger_bird_flash.py)."""
     print("case groups_mask", flush=True)
