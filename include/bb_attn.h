@@ -55,6 +55,18 @@ size_t bb_sparse_flash_workspace(int BH, int64_t T, int64_t N, int D, int num_he
                                  int64_t window, int route_k, int64_t row_end, int have_vt);
 
 /*
+ * Non-causal exact attention: every one of the T query rows attends all N keys (T <= N), in one launch (plus a merge
+ * launch when the keys are split over workgroups). Replaces F.scaled_dot_product_attention(q, k, v,
+ * is_causal=False, enable_gqa=True) of RDAttention.exact_attention for 1 < t < n (modal_rd/attention.py:140-141).
+ * Arguments as bb_sparse_flash (same layouts, alignment rules, V^T and workspace); bb_exact_attention_workspace
+ * sizes the workspace.
+ */
+int bb_exact_attention(const void* q, const int64_t* sq, const void* k, const int64_t* sk, const void* v,
+                       const int64_t* sv, const void* vt, void* out, const int64_t* so, int BH, int64_t T, int64_t N,
+                       int D, int num_heads, int kv_groups, float scale, void* ws, size_t ws_bytes, void* stream);
+size_t bb_exact_attention_workspace(int BH, int64_t T, int64_t N, int D, int num_heads, int kv_groups, int have_vt);
+
+/*
  * V [n_kvbh, N, D] (strides sv[3]) -> V^T [n_kvbh, D, bb_transpose_v_cols(N)] with zero columns past N: the layout
  * the window tiles stream from. A caller making several bb_sparse_flash calls over the same V (prefill main pass
  * and exact tail) transposes once and passes the result as `vt`. No reference counterpart (the reference's Triton

@@ -168,6 +168,28 @@ def test_million_token_rows_match_oracle(dev):
     _check(got, ref, "million_rows")
 
 
+@pytest.mark.parametrize("t,n,H,Hkv,d", [(2, 20000, 32, 8, 128), (65, 131072, 32, 8, 128), (300, 5000, 32, 8, 128),
+                                         (7, 3000, 8, 2, 64)])
+def test_exact_attention_noncausal(t, n, H, Hkv, d, dev):
+    """bb_exact_attention: t query rows, each attending all n cached keys (the reference's SDPA with is_causal=False
+    for 1 < t < n, modal_rd/attention.py:140-141), in one call, against float64 SDPA; also through
+    RDAttention.exact_attention on [1, H, t, d] / [1, Hkv, n, d] views."""
+    print(f"case exact_noncausal t={t} n={n} H={H}/{Hkv} d={d}", flush=True)
+    from types import SimpleNamespace
+
+    from bigger_bird_amd import RDAttention, exact_attention
+
+    q, k, v = _rand((H, t, d), 71 + t), _rand((Hkv, n, d), 72), _rand((Hkv, n, d), 73)
+    ref = oracle.sdpa_ref(q, k, v, causal=False, scale=d ** -0.5, groups=H // Hkv)
+    out = exact_attention(q.to(dev), k.to(dev), v.to(dev), num_heads=H, kv_groups=H // Hkv, scale=d ** -0.5)
+    _check(out, ref, f"exact_noncausal t={t} n={n}")
+    base = SimpleNamespace(config=SimpleNamespace(num_attention_heads=H, num_key_value_heads=Hkv), layer_idx=0,
+                           head_dim=d, scaling=d ** -0.5, q_proj=None, k_proj=None, v_proj=None, o_proj=None)
+    attn = RDAttention(base, sink=64, window=1024, vertical=64)
+    out2 = attn.exact_attention(q.to(dev)[None], k.to(dev)[None], v.to(dev)[None], t, n)
+    assert torch.equal(out2[0], out)
+
+
 def test_route_groups_and_token_mask(dev):
     """Per-query route groups (vertical_scope layout) and a padding mask (tests/test_bigger_bird_flash.py)."""
     print("case groups_mask", flush=True)

@@ -9,11 +9,11 @@ Public surface (mirrors the reference's modal_rd.attention / kernels.bigger_bird
 """
 from .attention import RDAttention, install, rope_inplace, routes, vertical_budget
 from .decode import bigger_bird_decode, bigger_bird_route, pooled_probs
-from .flash import bigger_bird_flash, transpose_v
+from .flash import bigger_bird_flash, exact_attention, transpose_v
 from .graph_decode import StaticDecoder, graph_generate, graph_prefill
 from .kv_int8 import Int8KVLayer, decode_bf16, decode_int8, dequantize, make_int8_cache, quantize
 
-__all__ = ["RDAttention", "install", "rope_inplace", "routes", "vertical_budget", "bigger_bird_flash", "transpose_v",
+__all__ = ["RDAttention", "install", "rope_inplace", "routes", "vertical_budget", "bigger_bird_flash", "exact_attention", "transpose_v",
            "Int8KVLayer", "decode_bf16", "decode_int8", "dequantize", "make_int8_cache", "quantize",
            "bigger_bird_decode", "bigger_bird_route", "pooled_probs", "StaticDecoder", "graph_prefill",
            "graph_generate"]

@@ -18,7 +18,7 @@ import torch.nn as nn
 
 from . import _lib
 from .decode import gather_rows, topk_columns
-from .flash import bigger_bird_flash, transpose_v
+from .flash import bigger_bird_flash, exact_attention, transpose_v
 
 ROPE_CHUNK = 8192
 
@@ -158,11 +158,9 @@ class RDAttention(nn.Module):
         if t == 1:
             from .kv_int8 import decode_bf16
             return decode_bf16(q[0, :, 0], k[0], v[0], self.scaling)[None, :, None]
-        # 1 < t < n: the reference attends every cached key from every query (non-causal SDPA)
-        none = torch.full((self.num_heads, 1, 1), -1, dtype=torch.int32, device=q.device)
-        outs = [bigger_bird_flash(q[0, :, i:i + 1], k[0], v[0], none, front=0, window=n, num_heads=self.num_heads,
-                                  kv_groups=self.groups, scale=self.scaling) for i in range(t)]
-        return torch.cat(outs, 1)[None]
+        # 1 < t < n: every query attends every cached key (the reference's non-causal SDPA), one launch
+        return exact_attention(q[0], k[0], v[0], num_heads=self.num_heads, kv_groups=self.groups,
+                               scale=self.scaling)[None]
 
     def routes(self, q, k):
         """Per-head top-V key columns by mean (or max) softmax prob of the route queries (HIP, deterministic)."""

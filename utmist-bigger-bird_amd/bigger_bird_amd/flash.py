@@ -84,3 +84,33 @@ def bigger_bird_flash(q, k, v, indices, *, front=64, window=256, token_mask=None
         _lib.ptr(out), _lib.i64s(*out.stride()), bh, t, n, d, num_heads, kv_groups, min(front, n), window,
         route_chunk, float(scale), re, _lib.ptr(ws), ws_bytes, _lib.stream_of(q)))
     return out
+
+
+def exact_attention(q, k, v, *, num_heads, kv_groups=1, scale=1.0, vt=None, out=None):
+    """Non-causal exact attention in one launch: every row of Q [BH, T, D] attends all N keys of K/V [BH/kv_groups, N,
+    D] (T <= N). The operator behind RDAttention.exact_attention for 1 < t < n, where the reference calls
+    F.scaled_dot_product_attention(q, k, v, is_causal=False, enable_gqa=True) (modal_rd/attention.py:140-141). Returns
+    a [BH, T, D] view of a [T, BH, D] buffer (or writes `out`); `vt` may pass a precomputed transpose_v(v)."""
+    if not q.is_cuda or q.dtype != torch.bfloat16:
+        raise ValueError("HIP Bigger Bird requires ROCm BF16")
+    if (k.shape != v.shape or q.ndim != 3 or q.shape[0] != k.shape[0] * kv_groups
+            or q.shape[-1] != k.shape[-1] or num_heads % kv_groups):
+        raise ValueError("Q [BH,T,D] and K/V [BH/kv_groups,N,D] must have matching heads and dimensions")
+    bh, t, d = q.shape
+    n = k.shape[1]
+    if n - t < 0:
+        raise ValueError("Key sequence must be at least as long as query sequence")
+    _lib.require_gpu(k, v, vt, what="exact_attention")
+    if out is None:
+        out = torch.empty((t, bh, d), dtype=q.dtype, device=q.device).permute(1, 0, 2)
+    if t == 0:
+        return out
+    q, k, v = _operand(q), _operand(k), _operand(v)
+    L = _lib.lib()
+    ws_bytes = L.bb_exact_attention_workspace(bh, t, n, d, num_heads, kv_groups, int(vt is not None))
+    ws = _lib.workspace(ws_bytes, q.device) if ws_bytes else None
+    _lib.check(L.bb_exact_attention(
+        _lib.ptr(q), _lib.i64s(*q.stride()), _lib.ptr(k), _lib.i64s(*k.stride()), _lib.ptr(v), _lib.i64s(*v.stride()),
+        _lib.ptr(vt), _lib.ptr(out), _lib.i64s(*out.stride()), bh, t, n, d, num_heads, kv_groups, float(scale),
+        _lib.ptr(ws), ws_bytes, _lib.stream_of(q)))
+    return out

@@ -161,11 +161,14 @@ int bb_transpose_v(const void* v, const int64_t* sv, int n_kvbh, int64_t N, int 
                     "bb_transpose_v");
 }
 
-int bb_sparse_flash(const void* q, const int64_t* sq, const void* k, const int64_t* sk, const void* v,
-                    const int64_t* sv, const void* vt, const int32_t* idx, const int64_t* si, int n_groups,
-                    int route_k, const uint8_t* key_mask, int64_t smb, void* out, const int64_t* so, int BH, int64_t T,
-                    int64_t N, int D, int num_heads, int kv_groups, int64_t front, int64_t window,
-                    int64_t route_chunk, float scale, int64_t row_end, void* ws, size_t ws_bytes, void* stream) {
+// bb_sparse_flash, and with `noncausal` the exact attention of every query row over all N keys (bb_exact_attention:
+// front 0, window N, no routes, every row placed at position N - 1).
+static int sparse_flash_impl(const void* q, const int64_t* sq, const void* k, const int64_t* sk, const void* v,
+                             const int64_t* sv, const void* vt, const int32_t* idx, const int64_t* si, int n_groups,
+                             int route_k, const uint8_t* key_mask, int64_t smb, void* out, const int64_t* so, int BH,
+                             int64_t T, int64_t N, int D, int num_heads, int kv_groups, int64_t front, int64_t window,
+                             int64_t route_chunk, float scale, int64_t row_end, void* ws, size_t ws_bytes,
+                             void* stream, bool noncausal) {
   g_err[0] = 0;
   if (!q || !k || !v || !out || !sq || !sk || !sv || !so)
     return fail("Q [BH,T,D] and K/V [BH/kv_groups,N,D] must have matching heads and dimensions");
@@ -207,7 +210,9 @@ int bb_sparse_flash(const void* q, const int64_t* sq, const void* k, const int64
   if (si) { p.si0 = si[0]; p.si1 = si[1]; p.si2 = si[2]; }
   p.smb = smb;
   p.so0 = so[0]; p.so1 = so[1];
-  p.N = N; p.T = T; p.offset = N - T; p.row_end = row_end;
+  p.N = N; p.T = T; p.row_end = row_end;
+  p.offset = noncausal ? N - 1 : N - T;
+  p.pos_step = noncausal ? 0 : 1;
   p.route_chunk = route_chunk;
   p.key_chunk = s.key_chunk;
   p.BH = BH; p.H = num_heads; p.G = kv_groups; p.Hkv_pb = num_heads / kv_groups; p.n_kvbh = BH / kv_groups;
@@ -249,6 +254,28 @@ int bb_sparse_flash(const void* q, const int64_t* sq, const void* k, const int64
   if (flash_pipe_enabled() && s.hpw == 4 && bb::flash_pipe_supported(p, D))
     return hip_status(bb::launch_flash_pipe(p, st), "bb_sparse_flash pipelined kernel");
   return hip_status(bb::launch_flash(p, D, s.hpw, false, st), "bb_sparse_flash kernel");
+}
+
+int bb_sparse_flash(const void* q, const int64_t* sq, const void* k, const int64_t* sk, const void* v,
+                    const int64_t* sv, const void* vt, const int32_t* idx, const int64_t* si, int n_groups,
+                    int route_k, const uint8_t* key_mask, int64_t smb, void* out, const int64_t* so, int BH, int64_t T,
+                    int64_t N, int D, int num_heads, int kv_groups, int64_t front, int64_t window,
+                    int64_t route_chunk, float scale, int64_t row_end, void* ws, size_t ws_bytes, void* stream) {
+  return sparse_flash_impl(q, sq, k, sk, v, sv, vt, idx, si, n_groups, route_k, key_mask, smb, out, so, BH, T, N, D,
+                           num_heads, kv_groups, front, window, route_chunk, scale, row_end, ws, ws_bytes, stream,
+                           false);
+}
+
+size_t bb_exact_attention_workspace(int BH, int64_t T, int64_t N, int D, int num_heads, int kv_groups, int have_vt) {
+  return bb_sparse_flash_workspace(BH, T, N, D, num_heads, kv_groups, 0, N, 0, T, have_vt);
+}
+
+int bb_exact_attention(const void* q, const int64_t* sq, const void* k, const int64_t* sk, const void* v,
+                       const int64_t* sv, const void* vt, void* out, const int64_t* so, int BH, int64_t T, int64_t N,
+                       int D, int num_heads, int kv_groups, float scale, void* ws, size_t ws_bytes, void* stream) {
+  const int64_t si[3] = {0, 0, 0};
+  return sparse_flash_impl(q, sq, k, sk, v, sv, vt, nullptr, si, 1, 0, nullptr, 0, out, so, BH, T, N, D, num_heads,
+                           kv_groups, 0, N, N, scale, T, ws, ws_bytes, stream, true);
 }
 
 size_t bb_routes_workspace(int64_t n, int H, int Hkv, int B, int r) {

@@ -35,7 +35,7 @@ namespace {
 // One 64-key tile for one wave: S^T = K Q^T, online softmax, O^T += V^T P^T.
 template <int D, int QB, bool MASKED, typename Mask>
 BB_DEV void tile_step(WaveState<D, QB>& st, const uint16_t* kl, const uint16_t* vt, int lane, float c, int64_t qabs0,
-                      const Mask& mask) {
+                      int64_t step, const Mask& mask) {
   const int h = lane >> 5, li = lane & 31;
   f32x16_t s[QB][2];
 #pragma unroll
@@ -56,7 +56,7 @@ BB_DEV void tile_step(WaveState<D, QB>& st, const uint16_t* kl, const uint16_t* 
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     if constexpr (MASKED) {
-      const auto mrow = mask.row(qabs0 + 32 * qb + li);
+      const auto mrow = mask.row(qabs0 + (32 * qb + li) * step);
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -155,14 +155,14 @@ __global__ __launch_bounds__(64 * NW, 1) void flash_kernel(FlashParams p) {
   const int64_t T_eff = p.row_end < p.T ? p.row_end : p.T;
   const int64_t r0 = (int64_t)rt * R;
   const int64_t r1 = (r0 + R < T_eff ? r0 + R : T_eff) - 1;
-  const int64_t qlo = r0 + p.offset, qhi = r1 + p.offset;
+  const int64_t qlo = p.offset + r0 * p.pos_step, qhi = p.offset + r1 * p.pos_step;
 
   const int slot = wave / WPH, rb = wave % WPH;
   const int bh = bh_base + slot;
   const int64_t rw = r0 + (int64_t)RW * rb;
   const bool wave_active = rw <= r1;
-  const int64_t qw0 = rw + p.offset;
-  const int64_t qw1 = (rw + RW - 1 < r1 ? rw + RW - 1 : r1) + p.offset;
+  const int64_t qw0 = p.offset + rw * p.pos_step;
+  const int64_t qw1 = p.offset + (rw + RW - 1 < r1 ? rw + RW - 1 : r1) * p.pos_step;
   const uint8_t* km = HAS_MASK ? p.key_mask + (int64_t)batch * p.smb : nullptr;
 
   WaveState<D, QB> st;
@@ -229,9 +229,9 @@ __global__ __launch_bounds__(64 * NW, 1) void flash_kernel(FlashParams p) {
           const bool full = !HAS_MASK && k1 <= qw0 && k1 < p.N && (k1 < p.front || k0 >= qw1 - p.window + 1);
           const WindowMask wm{k0, p.N, p.front, p.window, km};
           if (full)
-            tile_step<D, QB, false>(st, tile_k(cur), tile_v(cur), lane, p.c, qw0, wm);
+            tile_step<D, QB, false>(st, tile_k(cur), tile_v(cur), lane, p.c, qw0, p.pos_step, wm);
           else
-            tile_step<D, QB, true>(st, tile_k(cur), tile_v(cur), lane, p.c, qw0, wm);
+            tile_step<D, QB, true>(st, tile_k(cur), tile_v(cur), lane, p.c, qw0, p.pos_step, wm);
         }
       }
       wait_vm();
@@ -311,7 +311,7 @@ __global__ __launch_bounds__(64 * NW, 1) void flash_kernel(FlashParams p) {
         __syncthreads();
         if (head_work && bi < my_batches) {
           const RoutedMask rm{route_keys[slot], p.window, p.route_chunk, g, km};
-          tile_step<D, QB, true>(st, kl, vt, lane, p.c, qw0, rm);
+          tile_step<D, QB, true>(st, kl, vt, lane, p.c, qw0, p.pos_step, rm);
         }
         __syncthreads();
       }

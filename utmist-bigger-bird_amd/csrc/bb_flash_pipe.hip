@@ -319,11 +319,11 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
   const int64_t T_eff = p.row_end < p.T ? p.row_end : p.T;
   const int64_t r0 = (int64_t)rt * PROWS;
   const int64_t r1 = (r0 + PROWS < T_eff ? r0 + PROWS : T_eff) - 1;
-  const int64_t qlo = r0 + p.offset, qhi = r1 + p.offset;
+  const int64_t qlo = p.offset + r0 * p.pos_step, qhi = p.offset + r1 * p.pos_step;
   const int64_t rw = r0 + 32 * rbk;            // first row of this wave
   const bool wave_live = rw <= r1;
-  const int64_t qw0 = rw + p.offset, qw1 = (rw + 31 < r1 ? rw + 31 : r1) + p.offset;
-  const int64_t qme = qw0 + li;                // this lane's query position
+  const int64_t qw0 = p.offset + rw * p.pos_step, qw1 = p.offset + (rw + 31 < r1 ? rw + 31 : r1) * p.pos_step;
+  const int64_t qme = qw0 + li * p.pos_step;   // this lane's query position
 
   PingState st;
   {

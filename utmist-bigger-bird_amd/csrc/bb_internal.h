@@ -18,6 +18,7 @@ struct FlashParams {
   float* part_ml;           // split mode: [n_chunks][BH][T][2] (running max in log2 units, denominator)
   int64_t sq0, sq1, sk0, sk1, sv0, sv1, si0, si1, si2, smb, so0, so1;
   int64_t N, T, offset, row_end, route_chunk, key_chunk, np;
+  int64_t pos_step;         // absolute position of query row t = offset + t * pos_step (0: every row at offset)
   int BH, H, G, Hkv_pb, n_kvbh, front, window, route_k, n_groups;
   int row_tiles, head_splits, n_chunks, remap, waves;
   float c;  // scale * log2(e)
