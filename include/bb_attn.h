@@ -50,9 +50,11 @@ int bb_sparse_flash(const void* q, const int64_t* sq, const void* k, const int64
                     int64_t N, int D, int num_heads, int kv_groups, int64_t front, int64_t window,
                     int64_t route_chunk, float scale, int64_t row_end, void* ws, size_t ws_bytes, void* stream);
 
-/* Workspace bytes for bb_sparse_flash; have_vt != 0 when the caller passes a precomputed V^T. */
+/* Workspace bytes for bb_sparse_flash (n_groups and route_k as passed to it); have_vt != 0 when the caller passes a
+ * precomputed V^T. Besides V^T and the split partials it holds the routed K/V^T tiles pre-gathered per query head
+ * (32 KB per 64 route slots per head and group) for head_dim 128 with a multiple of 4 query heads per KV head. */
 size_t bb_sparse_flash_workspace(int BH, int64_t T, int64_t N, int D, int num_heads, int kv_groups, int64_t front,
-                                 int64_t window, int route_k, int64_t row_end, int have_vt);
+                                 int64_t window, int route_k, int n_groups, int64_t row_end, int have_vt);
 
 /*
  * Non-causal exact attention: every one of the T query rows attends all N keys (T <= N), in one launch (plus a merge

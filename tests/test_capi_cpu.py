@@ -35,9 +35,10 @@ def test_version_and_sizes():
     assert L.bb_routes_workspace(131072, 32, 8, 1, 64) > 32 * 131072 * 8
     assert L.bb_decode_workspace(131072, 32, 8, 128) > 0
     # tail shape: few row tiles, no routes -> the split-key schedule asks for partials
-    tail = L.bb_sparse_flash_workspace(32, 256, 131072, 128, 32, 4, 0, 131072, 0, 256, 1)
-    main = L.bb_sparse_flash_workspace(32, 131072, 131072, 128, 32, 4, 64, 16384, 512, 131072 - 256, 1)
-    assert tail > 0 and main == 0
+    tail = L.bb_sparse_flash_workspace(32, 256, 131072, 128, 32, 4, 0, 131072, 0, 1, 256, 1)
+    main = L.bb_sparse_flash_workspace(32, 131072, 131072, 128, 32, 4, 64, 16384, 512, 1, 131072 - 256, 1)
+    # main pass: only the routed tiles pre-gathered per head (512 slots = 8 batches of a 16 KB K and V^T tile each)
+    assert tail > 0 and main == 32 * 8 * 2 * 64 * 128 * 2
 
 
 def _flash_call(**over):

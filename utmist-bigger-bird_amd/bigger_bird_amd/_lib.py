@@ -21,7 +21,7 @@ SIGNATURES = {
     "bb_sparse_flash": (_i32, [_vp, c_i64p, _vp, c_i64p, _vp, c_i64p, _vp, _vp, c_i64p, _i32, _i32, _vp, _i64,
                                _vp, c_i64p, _i32, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _i64, _f32, _i64,
                                _vp, _sz, _vp]),
-    "bb_sparse_flash_workspace": (_sz, [_i32, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _i32, _i64, _i32]),
+    "bb_sparse_flash_workspace": (_sz, [_i32, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _i32, _i32, _i64, _i32]),
     "bb_exact_attention": (_i32, [_vp, c_i64p, _vp, c_i64p, _vp, c_i64p, _vp, _vp, c_i64p, _i32, _i64, _i64, _i32, _i32,
                                   _i32, _f32, _vp, _sz, _vp]),
     "bb_exact_attention_workspace": (_sz, [_i32, _i64, _i64, _i32, _i32, _i32, _i32]),

@@ -137,14 +137,18 @@ int64_t bb_transpose_v_cols(int64_t N) { return cdiv(N > 0 ? N : 1, 64) * 64; }
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Routed tiles are pre-gathered for the pipelined kernel (head_dim 128, query heads per KV head a multiple of 4).
+static bool routed_tiles_wanted(int D, int kv_groups, int route_k) { return route_k > 0 && D == 128 && kv_groups % 4 == 0; }
+
 size_t bb_sparse_flash_workspace(int BH, int64_t T, int64_t N, int D, int num_heads, int kv_groups, int64_t front,
-                                 int64_t window, int route_k, int64_t row_end, int have_vt) {
+                                 int64_t window, int route_k, int n_groups, int64_t row_end, int have_vt) {
   if (BH <= 0 || T <= 0 || N <= 0 || kv_groups <= 0 || BH % kv_groups) return 0;
   if (window >= N) route_k = 0;
   if (row_end <= 0 || row_end > T) row_end = T;
   FlashSchedule s = flash_schedule(BH, T, N, num_heads, kv_groups, front, window, route_k, row_end);
   size_t bytes = 0;
   if (!have_vt) bytes += align256((size_t)(BH / kv_groups) * D * bb_transpose_v_cols(N) * 2);
+  if (routed_tiles_wanted(D, kv_groups, route_k)) bytes += align256(bb::route_tiles_bytes(BH, n_groups, route_k));
   if (s.split) bytes += (size_t)s.n_chunks * BH * T * (size_t)(D + 2) * sizeof(float);
   return bytes;
 }
@@ -228,8 +232,8 @@ static int sparse_flash_impl(const void* q, const int64_t* sq, const void* k, co
   p.np = bb_transpose_v_cols(N);
   p.c = (float)((double)scale * 1.4426950408889634);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const size_t need = bb_sparse_flash_workspace(BH, T, N, D, num_heads, kv_groups, front, window, route_k, row_end,
-                                                vt != nullptr);
+  const size_t need = bb_sparse_flash_workspace(BH, T, N, D, num_heads, kv_groups, front, window, route_k, p.n_groups,
+                                                row_end, vt != nullptr);
   if (need && (!ws || ws_bytes < need)) return fail("workspace of %zu bytes required", need);
   char* wsp = static_cast<char*>(ws);
   if (vt) {
@@ -242,17 +246,25 @@ static int sparse_flash_impl(const void* q, const int64_t* sq, const void* k, co
     if (e != hipSuccess) return hip_status(e, "bb_sparse_flash transpose");
     p.vt = vt_ws;
   }
+  const bool pipe = flash_pipe_enabled() && s.hpw == 4 && bb::flash_pipe_supported(p, D);
+  if (routed_tiles_wanted(D, kv_groups, route_k)) {
+    uint16_t* rt = reinterpret_cast<uint16_t*>(wsp);
+    wsp += align256(bb::route_tiles_bytes(BH, p.n_groups, route_k));
+    if (pipe) {
+      p.rtiles = rt;
+      p.rt_batches = (int)cdiv(route_k, 64);
+      hipError_t e = bb::launch_route_tiles(p, rt, st);
+      if (e != hipSuccess) return hip_status(e, "bb_sparse_flash routed tiles");
+    }
+  }
   if (s.split) {
     p.part_o = reinterpret_cast<float*>(wsp);
     p.part_ml = p.part_o + (size_t)s.n_chunks * BH * T * D;
-    hipError_t e = (flash_pipe_enabled() && s.hpw == 4 && bb::flash_pipe_supported(p, D))
-                       ? bb::launch_flash_pipe(p, st)
-                       : bb::launch_flash(p, D, s.hpw, true, st);
+    hipError_t e = pipe ? bb::launch_flash_pipe(p, st) : bb::launch_flash(p, D, s.hpw, true, st);
     if (e != hipSuccess) return hip_status(e, "bb_sparse_flash split kernel");
     return hip_status(bb::launch_flash_merge(p, D, st), "bb_sparse_flash merge kernel");
   }
-  if (flash_pipe_enabled() && s.hpw == 4 && bb::flash_pipe_supported(p, D))
-    return hip_status(bb::launch_flash_pipe(p, st), "bb_sparse_flash pipelined kernel");
+  if (pipe) return hip_status(bb::launch_flash_pipe(p, st), "bb_sparse_flash pipelined kernel");
   return hip_status(bb::launch_flash(p, D, s.hpw, false, st), "bb_sparse_flash kernel");
 }
 
@@ -267,7 +279,7 @@ int bb_sparse_flash(const void* q, const int64_t* sq, const void* k, const int64
 }
 
 size_t bb_exact_attention_workspace(int BH, int64_t T, int64_t N, int D, int num_heads, int kv_groups, int have_vt) {
-  return bb_sparse_flash_workspace(BH, T, N, D, num_heads, kv_groups, 0, N, 0, T, have_vt);
+  return bb_sparse_flash_workspace(BH, T, N, D, num_heads, kv_groups, 0, N, 0, 1, T, have_vt);
 }
 
 int bb_exact_attention(const void* q, const int64_t* sq, const void* k, const int64_t* sk, const void* v,

@@ -463,18 +463,34 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
     if (rbk == 0) ring_barrier();  // realign the two groups
   }
 
-  // ---- routed keys: per-head gathered tiles; the two waves of a head share the gather ----
+  // ---- routed keys: per-head tiles pre-gathered by route_tiles_kernel; the two waves of a head share the loads ----
   if (p.route_k > 0) {
     __syncthreads();  // every wave is done with the ring
     uint16_t* kl = smem + hd * 2 * PTE;
     uint16_t* vt = kl + PTE;
     int64_t g_first = qlo / p.route_chunk, g_last = qhi / p.route_chunk;
     if (g_last >= p.n_groups) g_last = p.n_groups - 1;
+    const uint32_t loff = 16u * (uint32_t)lane;
     for (int64_t g = g_first; g <= g_last; ++g) {
       const int32_t* irow = p.idx + (int64_t)bh * p.si0 + g * p.si1;
+      // This head's pre-gathered batches of group g: batch b is a K tile at b * 2 PTE and its V^T tile after it.
+      // Each of the head's two waves loads blocks rbk + 2 i (i < 8) of a tile straight into LDS.
+      const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint16_t*>(p.rtiles + ((int64_t)bh * p.n_groups + g) * p.rt_batches * 2 * PTE), 0,
+          p.rt_batches * 2 * PTE * 2, 0x00020000);
+      auto load_tile = [&](int b, uint16_t* dst, int part) {
+#pragma unroll
+        for (int i = 0; i < PBLK / 2; ++i) {
+          const int blk = rbk + 2 * i;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rrs, reinterpret_cast<__attribute__((address_space(3))) void*>(
+                       reinterpret_cast<uintptr_t>(dst + blk * 512)),
+              16, loff, (b * 2 * PTE + part * PTE + blk * 512) * 2, 0, 0);
+        }
+      };
       // The head's route slots, kRouteCache at a time, go to LDS in one pass (usable keys, -1 elsewhere: a key some
-      // row of the workgroup attends is >= front, < N and <= qhi - window), so that the gathers below do not wait
-      // on index loads. Batches of 64 slots run up to the last one holding a usable key.
+      // row of the workgroup attends is >= front, < N and <= qhi - window). Batches of 64 slots run up to the last
+      // one holding a usable key.
       for (int sb = 0; sb < p.route_k; sb += kRouteCache) {
         const int nslots = p.route_k - sb < kRouteCache ? p.route_k - sb : kRouteCache;
         int nbh = 0;
@@ -497,38 +513,13 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
             if (x == hd) my_nb = my_nb > v ? my_nb : v;
           }
         __syncthreads();  // head_batches and route_keys are rewritten only after every wave has read them
+        const int b0 = sb / kTileKeys;
         for (int bi = 0; bi < nb; ++bi) {
           const bool work = bi < my_nb;
           const int32_t* keys = route_keys[hd] + kTileKeys * bi;
           if (work) {
-            // K rows by direct loads (the head's two waves split the 16 blocks)
-            for (int b = rbk; b < PBLK; b += 2) {
-              const int e = b * 512 + 8 * lane;
-              const int row = e / PD, sl2 = (e % PD) / 8;
-              const int chk = sl2 ^ (row & (PD / 8 - 1));
-              const int32_t kr = keys[row];
-              lds_dma16(kbase + (int64_t)(kr >= 0 ? kr : 0) * p.sk1 + 8 * chk, kl + b * 512);
-            }
-            // V rows -> V^T through registers: units of 4 keys x 8 d
-            for (int u = lane + 64 * rbk; u < (kTileKeys / 4) * (PD / 8); u += 128) {
-              const int bq = u % (PD / 8), a4 = u / (PD / 8);
-              u32x4_t vr[4];
-#pragma unroll
-              for (int s2 = 0; s2 < 4; ++s2) {
-                const int32_t kr = keys[4 * a4 + s2];
-                vr[s2] = kr >= 0 ? ld16(vbase + (int64_t)kr * p.sv1 + 8 * bq) : u32x4_t{0, 0, 0, 0};
-              }
-#pragma unroll
-              for (int e = 0; e < 8; ++e) {
-                const int w = e >> 1;
-                const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-                const uint32_t lo = __builtin_amdgcn_perm(vr[1][w], vr[0][w], sel);
-                const uint32_t hi = __builtin_amdgcn_perm(vr[3][w], vr[2][w], sel);
-                const int d = 8 * bq + e;
-                *reinterpret_cast<u32x2_t*>(vt + vt_off(d, 2 * (a4 >> 2) + (a4 & 1)) + 4 * ((a4 >> 1) & 1)) =
-                    u32x2_t{lo, hi};
-              }
-            }
+            load_tile(b0 + bi, kl, 0);
+            load_tile(b0 + bi, vt, 1);
           }
           vm_wait_tile(false);
           __syncthreads();
@@ -577,6 +568,51 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
     }
 }
 
+// Pre-gathers, per query head and route group, the routed K rows and V^T columns of every 64-slot batch into the
+// LDS tile layouts of the main pass (K tile: row r, 16-byte chunk c at r * D + 8 (c ^ (r % 16)); V^T tile: vt_off),
+// so that the routed phase streams them with direct loads like window tiles. Empty slots (-1, or outside [0, N))
+// are zero rows. Grid (batches, n_groups, BH), 256 threads.
+__global__ __launch_bounds__(256) void route_tiles_kernel(FlashParams p, uint16_t* __restrict__ rt) {
+  const int b = blockIdx.x, g = blockIdx.y, bh = blockIdx.z, t = threadIdx.x;
+  const int batch = bh / p.H;
+  const int kvbh = batch * p.Hkv_pb + (bh % p.H) / p.G;
+  const uint16_t* kbase = p.k + (int64_t)kvbh * p.sk0;
+  const uint16_t* vbase = p.v + (int64_t)kvbh * p.sv0;
+  const int32_t* irow = p.idx + (int64_t)bh * p.si0 + (int64_t)g * p.si1;
+  uint16_t* kt = rt + (((int64_t)bh * p.n_groups + g) * p.rt_batches + b) * 2 * PTE;
+  uint16_t* vtt = kt + PTE;
+  auto key_of = [&](int r) -> int64_t {
+    const int slot = b * kTileKeys + r;
+    const int64_t key = slot < p.route_k ? irow[(int64_t)slot * p.si2] : -1;
+    return key >= 0 && key < p.N ? key : -1;
+  };
+  // K tile: 64 rows x 16 chunks of 16 bytes, 4 per thread
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int u = t + 256 * i, row = u / 16, chunk = u % 16;
+    const int64_t key = key_of(row);
+    const u32x4_t v = key >= 0 ? ld16(kbase + key * p.sk1 + 8 * chunk) : u32x4_t{0, 0, 0, 0};
+    st16(kt + row * PD + 8 * (chunk ^ (row & 15)), v);
+  }
+  // V^T tile: unit (4 keys x 8 d) per thread, transposed into the permuted key order of vt_off
+  const int bq = t % (PD / 8), a4 = t / (PD / 8);
+  u32x4_t vr[4];
+#pragma unroll
+  for (int s2 = 0; s2 < 4; ++s2) {
+    const int64_t key = key_of(4 * a4 + s2);
+    vr[s2] = key >= 0 ? ld16(vbase + key * p.sv1 + 8 * bq) : u32x4_t{0, 0, 0, 0};
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int w = e >> 1;
+    const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+    const uint32_t lo = __builtin_amdgcn_perm(vr[1][w], vr[0][w], sel);
+    const uint32_t hi = __builtin_amdgcn_perm(vr[3][w], vr[2][w], sel);
+    const int d = 8 * bq + e;
+    *reinterpret_cast<u32x2_t*>(vtt + vt_off(d, 2 * (a4 >> 2) + (a4 & 1)) + 4 * ((a4 >> 1) & 1)) = u32x2_t{lo, hi};
+  }
+}
+
 }  // namespace
 
 bool flash_pipe_supported(const FlashParams& p, int D) {
@@ -584,6 +620,18 @@ bool flash_pipe_supported(const FlashParams& p, int D) {
   const bool fits = p.N * p.sk1 * 2 < ((int64_t)1 << 31) && (int64_t)PD * p.np * 2 < ((int64_t)1 << 31);
   const bool chunks_ok = p.n_chunks == 1 || (p.key_chunk % kTileKeys == 0 && p.route_k == 0);
   return D == PD && p.G % PHEADS == 0 && p.key_mask == nullptr && fits && chunks_ok;
+}
+
+size_t route_tiles_bytes(int BH, int n_groups, int route_k) {
+  if (BH <= 0 || n_groups <= 0 || route_k <= 0) return 0;
+  return (size_t)BH * n_groups * ((route_k + kTileKeys - 1) / kTileKeys) * 2 * PTE * sizeof(uint16_t);
+}
+
+hipError_t launch_route_tiles(const FlashParams& p, uint16_t* rt, hipStream_t stream) {
+  if (p.route_k <= 0) return hipSuccess;
+  hipLaunchKernelGGL(route_tiles_kernel, dim3((unsigned)p.rt_batches, (unsigned)p.n_groups, (unsigned)p.BH), dim3(256),
+                     0, stream, p, rt);
+  return hipGetLastError();
 }
 
 hipError_t launch_flash_pipe(const FlashParams& p, hipStream_t stream) {

@@ -19,6 +19,8 @@ struct FlashParams {
   int64_t sq0, sq1, sk0, sk1, sv0, sv1, si0, si1, si2, smb, so0, so1;
   int64_t N, T, offset, row_end, route_chunk, key_chunk, np;
   int64_t pos_step;         // absolute position of query row t = offset + t * pos_step (0: every row at offset)
+  const uint16_t* rtiles;   // pre-gathered routed tiles [BH][n_groups][rt_batches][K tile | V^T tile], or null
+  int rt_batches;           // 64-slot batches of one route list (route_k rounded up to 64)
   int BH, H, G, Hkv_pb, n_kvbh, front, window, route_k, n_groups;
   int row_tiles, head_splits, n_chunks, remap, waves;
   float c;  // scale * log2(e)
@@ -29,6 +31,9 @@ hipError_t launch_flash_merge(const FlashParams& p, int D, hipStream_t stream);
 // Software-pipelined main-pass kernel (head_dim 128, kv_groups % 4 == 0, no token mask, 64-aligned route groups).
 bool flash_pipe_supported(const FlashParams& p, int D);
 hipError_t launch_flash_pipe(const FlashParams& p, hipStream_t stream);
+// Bytes of the pre-gathered routed tiles of one call, and the kernel that writes them (p.rtiles) for the main pass.
+size_t route_tiles_bytes(int BH, int n_groups, int route_k);
+hipError_t launch_route_tiles(const FlashParams& p, uint16_t* rt, hipStream_t stream);
 hipError_t launch_transpose_v(const uint16_t* v, int64_t sv0, int64_t sv1, int n_kvbh, int64_t N, int64_t np, int D,
                               uint16_t* vt, hipStream_t stream);
 
