@@ -56,28 +56,41 @@ def route_positions(n, r, mode, sink, window, device):
     return torch.arange(n - r, n, device=device)
 
 
+def _flat_heads(x):
+    """[B, Hh, T, d] -> a [B * Hh, T, d] view when the batch stride is Hh head strides (always for B = 1), else
+    None."""
+    b, hh, t, d = x.shape
+    if b > 1 and x.stride(0) != hh * x.stride(1):
+        return None
+    return x.as_strided((b * hh, t, d), (x.stride(1), x.stride(2), x.stride(3)), x.storage_offset())
+
+
 def routes(q, k, *, num_heads, num_kv_heads, sink, window, budget, n_route=64, route_pool="mean",
            route_queries="last", scaling, return_pooled=False):
     """Per-head top-`budget` key columns by pooled softmax probability of the route queries.
 
-    q [1, H, n, d], k [1, Hkv, n, d] (strided views are fine). Returns int32 [H, budget], ascending per head
-    (and the pooled scores [H, n] as float probabilities when `return_pooled`)."""
+    q [B, H, n, d], k [B, Hkv, n, d] (strided views are fine; for B > 1 the batch stride must be H head strides).
+    Returns int32 [B * H, budget], ascending per head (and the pooled scores [B * H, n] as float probabilities
+    when `return_pooled`)."""
     _lib.require_gpu(q, k, what="routes")
+    bsz = q.shape[0]
     n, d = k.shape[-2], k.shape[-1]
     r = min(n_route, n)
     qpos = route_positions(n, r, route_queries, sink, window, q.device).to(torch.int64).contiguous()
-    Q, K = q[0], k[0]
+    Q, K = _flat_heads(q), _flat_heads(k)
+    if Q is None or K is None:
+        raise ValueError("routes: batched q / k need a batch stride of H head strides")
     if Q.stride(-1) != 1 or Q.stride(0) % 8 or Q.stride(1) % 8 or Q.data_ptr() % 16:
         Q = Q.contiguous()
     if K.stride(-1) != 1 or K.stride(0) % 8 or K.stride(1) % 8 or K.data_ptr() % 16:
         K = K.contiguous()
-    idx = torch.empty(num_heads, budget, dtype=torch.int32, device=q.device)
-    pooled = torch.empty(num_heads, n, dtype=torch.int64, device=q.device) if return_pooled else None
+    idx = torch.empty(bsz * num_heads, budget, dtype=torch.int32, device=q.device)
+    pooled = torch.empty(bsz * num_heads, n, dtype=torch.int64, device=q.device) if return_pooled else None
     L = _lib.lib()
-    ws_bytes = L.bb_routes_workspace(n, num_heads, num_kv_heads, 1, r)
+    ws_bytes = L.bb_routes_workspace(n, num_heads, num_kv_heads, bsz, r)
     ws = _lib.workspace(ws_bytes, q.device)
     _lib.check(L.bb_routes(_lib.ptr(Q), _lib.i64s(Q.stride(0), Q.stride(1)), _lib.ptr(K),
-                           _lib.i64s(K.stride(0), K.stride(1)), _lib.ptr(qpos), r, 1, num_heads, num_kv_heads, n, d,
+                           _lib.i64s(K.stride(0), K.stride(1)), _lib.ptr(qpos), r, bsz, num_heads, num_kv_heads, n, d,
                            sink, window, budget, float(scaling), int(route_pool == "max"),
                            _lib.ptr(idx) if budget else None, _lib.ptr(pooled), _lib.ptr(ws), ws_bytes,
                            _lib.stream_of(q)))
@@ -178,20 +191,23 @@ class RDAttention(nn.Module):
         return res
 
     def sparse_prefill(self, q, k, v):
-        if q.shape[0] != 1:
-            # B > 1 (BASELINE's short-context arm): every batch element is its own layer call; the reference's
-            # sparse_prefill reads q[0] only, so parity is per element. last_routes stacks to [B, H, budget].
+        """Routes, then the sink + window + routed pass over rows < n - exact_tail and the exact tail written in
+        place (modal_rd/attention.py:176-206). B > 1 (BASELINE's short-context arm; the reference reads q[0] only) runs
+        as one batch of B * H heads per launch when the batch strides allow it, else one call per element; parity is
+        per element, and last_routes is then [B, H, budget]."""
+        bsz = q.shape[0]
+        Q, K, V = _flat_heads(q), _flat_heads(k), _flat_heads(v)
+        if bsz > 1 and (Q is None or K is None or V is None or self.kv_evict):
             outs, routes = [], []
-            for i in range(q.shape[0]):
+            for i in range(bsz):
                 outs.append(self.sparse_prefill(q[i:i + 1], k[i:i + 1], v[i:i + 1]))
                 routes.append(self.last_routes)
             self.last_routes = torch.stack(routes)
             return torch.cat(outs)
         n = k.shape[-2]
         idx = self.routes(q, k)
-        self.last_routes = idx
-        bh = self.num_heads
-        Q, K, V = q[0], k[0], v[0]
+        self.last_routes = idx if bsz == 1 else idx.view(bsz, self.num_heads, -1)
+        bh = bsz * self.num_heads
         vt = transpose_v(V)
         flash = dict(num_heads=self.num_heads, kv_groups=self.groups, scale=self.scaling,
                      block_m=self.block_m, block_n=self.block_n, num_warps=self.num_warps, num_stages=self.num_stages)
@@ -211,7 +227,7 @@ class RDAttention(nn.Module):
             none = torch.full((bh, 1, 1), -1, dtype=torch.int32, device=q.device)
             bigger_bird_flash(Q[:, n - r:], K, V, none, front=0, window=n, token_mask=None, route_chunk=None, vt=vt,
                               out=out[:, n - r:], **flash)
-        return out[None]
+        return out.unflatten(0, (bsz, self.num_heads))
 
     def evict_scores(self, q, k):
         """[Hkv, n] importance of every key for the last `evict_obs` queries (modal_rd/attention.py:209-224): exact
