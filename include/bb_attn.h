@@ -39,7 +39,8 @@ const char* bb_last_error(void);
  *   key_mask [B, N] uint8 (B = BH / num_heads, row stride smb) or NULL        (token_mask)
  *   out  [BH, T, D]   strides so[3]          (e.g. a permuted view of a [T, BH, D] buffer)
  *   Query row t sits at absolute position t + N - T. Rows >= row_end are not written (row_end = T for all rows).
- *   D in {32, 64, 128}; bf16 only; scale > 0.
+ *   D in {32, 64, 128}; 16-bit elements: bf16 (is_f16 = 0) or fp16 (is_f16 = 1) for q, k, v, V^T and out alike
+ *   (fp32 accumulation and softmax either way); scale > 0.
  *   vt   optional V^T from bb_transpose_v (NULL: transposed into the workspace).
  *   ws/ws_bytes: workspace of at least bb_sparse_flash_workspace(...) bytes (V^T unless given, plus the (O, m, l)
  *   partials of the split-key schedule used for long windows without routes).
@@ -47,7 +48,7 @@ const char* bb_last_error(void);
 int bb_sparse_flash(const void* q, const int64_t* sq, const void* k, const int64_t* sk, const void* v,
                     const int64_t* sv, const void* vt, const int32_t* idx, const int64_t* si, int n_groups,
                     int route_k, const uint8_t* key_mask, int64_t smb, void* out, const int64_t* so, int BH, int64_t T,
-                    int64_t N, int D, int num_heads, int kv_groups, int64_t front, int64_t window,
+                    int64_t N, int D, int is_f16, int num_heads, int kv_groups, int64_t front, int64_t window,
                     int64_t route_chunk, float scale, int64_t row_end, void* ws, size_t ws_bytes, void* stream);
 
 /* Workspace bytes for bb_sparse_flash (n_groups and route_k as passed to it); have_vt != 0 when the caller passes a
@@ -65,7 +66,8 @@ size_t bb_sparse_flash_workspace(int BH, int64_t T, int64_t N, int D, int num_he
  */
 int bb_exact_attention(const void* q, const int64_t* sq, const void* k, const int64_t* sk, const void* v,
                        const int64_t* sv, const void* vt, void* out, const int64_t* so, int BH, int64_t T, int64_t N,
-                       int D, int num_heads, int kv_groups, float scale, void* ws, size_t ws_bytes, void* stream);
+                       int D, int is_f16, int num_heads, int kv_groups, float scale, void* ws, size_t ws_bytes,
+                       void* stream);
 size_t bb_exact_attention_workspace(int BH, int64_t T, int64_t N, int D, int num_heads, int kv_groups, int have_vt);
 
 /*
@@ -207,11 +209,11 @@ int bb_rms_norm(const void* x, int64_t sx, int rows, int D, const void* w, float
 
 /*
  * In-place RoPE on x [B, Hh, T, D] (strides sx[3]) with cos/sin [B, T, D] (strides sc[2]; 0 to broadcast), with
- * the arithmetic of HF apply_rotary_pos_emb on bf16 tensors (bit-identical). Replaces rope_inplace
- * (modal_rd/attention.py:51-60).
+ * the arithmetic of HF apply_rotary_pos_emb on bf16 (is_f16 = 0) or fp16 (is_f16 = 1) tensors (bit-identical).
+ * Replaces rope_inplace (modal_rd/attention.py:51-60).
  */
 int bb_rope_inplace(void* x, const int64_t* sx, int B, int Hh, int64_t T, int D, const void* cos, const void* sin,
-                    const int64_t* sc, void* stream);
+                    const int64_t* sc, int is_f16, void* stream);
 
 #ifdef __cplusplus
 }

@@ -9,7 +9,8 @@
  *                   contract below, which the HIP router reproduces bit for bit.
  *   orc_attn_rows   kernels/bigger_bird_flash_ref.py:10-52 and kernels/bigger_bird_flash.py:56-96 (union mask
  *                   front | causal window | routed, GQA head map, OFFSET = N - T), one query row at a time in
- *                   float64 so that 128K-token shapes can be checked on sampled rows.
+ *                   float64 so that 128K-token shapes can be checked on sampled rows; bf16 or fp16 elements
+ *                   (kernels/bigger_bird_flash.py:110 accepts both).
  *   orc_quantize    modal_rd/kv_int8.py:19-22 (per-row symmetric int8, fp32 scale clamp_min 1e-4, RNE).
  *   orc_dequantize  modal_rd/kv_int8.py:25-26.
  *   orc_decode      modal_rd/attention.py:137-141 over the dequantised cache (exact attention of one token).
@@ -299,8 +300,9 @@ int orc_attn_rows(const uint16_t* q, int64_t sq0, int64_t sq1, const uint16_t* k
                   const uint16_t* v, int64_t sv0, int64_t sv1, const int32_t* idx, int64_t si0, int64_t si1,
                   int64_t si2, int NG, int KR, const uint8_t* key_mask, int64_t smb, int BH, int T, int N, int D,
                   int num_heads, int kv_groups, int front, int window, int64_t route_chunk, double scale,
-                  const int64_t* rows, int nrows, double* out, int nthreads) {
+                  const int64_t* rows, int nrows, double* out, int nthreads, int f16) {
   if (T > N || num_heads % kv_groups || BH % num_heads) return -1;
+  float (*const elem)(uint16_t) = f16 ? f16_to_f32 : bf16_to_f32; /* q, k, v element type */
   if (front > N) front = N;
   int64_t offset = (int64_t)N - T;
 #ifdef _OPENMP
@@ -343,7 +345,7 @@ int orc_attn_rows(const uint16_t* q, int64_t sq0, int64_t sq1, const uint16_t* k
         if (!use[j]) continue;
         double acc = 0;
         const uint16_t* kr = k + kvh * sk0 + j * sk1;
-        for (int c = 0; c < D; ++c) acc += (double)bf16_to_f32(qr[c]) * (double)bf16_to_f32(kr[c]);
+        for (int c = 0; c < D; ++c) acc += (double)elem(qr[c]) * (double)elem(kr[c]);
         s[j] = acc * scale;
         if (s[j] > mx) mx = s[j];
       }
@@ -356,7 +358,7 @@ int orc_attn_rows(const uint16_t* q, int64_t sq0, int64_t sq1, const uint16_t* k
         double p = exp(s[j] - mx);
         den += p;
         const uint16_t* vr = v + kvh * sv0 + j * sv1;
-        for (int c = 0; c < D; ++c) o[c] += p * (double)bf16_to_f32(vr[c]);
+        for (int c = 0; c < D; ++c) o[c] += p * (double)elem(vr[c]);
       }
       for (int c = 0; c < D; ++c) o[c] /= den;
       if (key_mask && !key_mask[b * smb + qabs])

@@ -46,7 +46,7 @@ def _flash_call(**over):
     s3 = _lib.i64s(4096, 128, 1)
     a = dict(q=ctypes.c_void_p(16), sq=s3, k=ctypes.c_void_p(16), sk=s3, v=ctypes.c_void_p(16), sv=s3, vt=None,
              idx=None, si=_lib.i64s(1, 1, 1), n_groups=1, route_k=0, key_mask=None, smb=0, out=ctypes.c_void_p(16),
-             so=s3, BH=32, T=64, N=64, D=128, num_heads=32, kv_groups=4, front=0, window=8, route_chunk=64,
+             so=s3, BH=32, T=64, N=64, D=128, is_f16=0, num_heads=32, kv_groups=4, front=0, window=8, route_chunk=64,
              scale=1.0, row_end=64, ws=None, ws_bytes=0, stream=None)
     a.update(over)
     rc = L.bb_sparse_flash(*a.values())
@@ -88,7 +88,7 @@ def test_python_surface_errors_without_gpu():
     with pytest.raises(ValueError, match="scope_chunk"):
         RDAttention(base, scope_chunk=96)
     q = torch.zeros(8, 64, 32, dtype=torch.bfloat16)
-    with pytest.raises(ValueError, match="ROCm BF16"):  # no silent CPU path
+    with pytest.raises(ValueError, match="ROCm FP16/BF16"):  # no silent CPU path
         bigger_bird_flash(q, q[:2], q[:2], torch.zeros(8, 1, 4, dtype=torch.int32), num_heads=8, kv_groups=4)
 
 

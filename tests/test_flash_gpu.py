@@ -1,6 +1,7 @@
 """bb_sparse_flash (through the C ABI via bigger_bird_flash) against the float64 CPU oracle.
 
-Tolerance: max-abs 2e-2 and mean-abs 2e-3 against the float64 masked-dense oracle for bf16.
+Tolerance: max-abs 2e-2 and mean-abs 2e-3 against the float64 masked-dense oracle for bf16;
+fp16 inputs (the reference kernel accepts both, kernels/bigger_bird_flash.py:110) are held to the same bound.
 Cases mirror the reference's own checks: tests/test_rd_attention_gqa.py (grouped == repeated, tail == masked SDPA),
 modal_rd/selfcheck.py (full budget == dense causal), modal_rd/check_long_indexing.py (identity attention is exact),
 tests/test_bigger_bird_flash.py (route chunks, token masks, odd lengths).
@@ -16,9 +17,9 @@ pytestmark = pytest.mark.gpu
 MAX_ABS, MEAN_ABS = 2e-2, 2e-3
 
 
-def _rand(shape, seed):
+def _rand(shape, seed, dtype=torch.bfloat16):
     g = torch.Generator().manual_seed(seed)
-    return torch.randn(*shape, generator=g).to(torch.bfloat16)
+    return torch.randn(*shape, generator=g).to(dtype)
 
 
 def _routes(h, n, front, window, k, seed, groups=1, chunk=None):
@@ -50,16 +51,17 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
-def test_matches_oracle(case, dev):
+def test_matches_oracle(case, dtype, dev):
     name, H, Hkv, T, N, d, front, window, rk, scale = case
-    print(f"case {name}", flush=True)
-    q, k, v = _rand((H, T, d), 1), _rand((Hkv, N, d), 2), _rand((Hkv, N, d), 3)
+    print(f"case {name} {dtype}", flush=True)
+    q, k, v = _rand((H, T, d), 1, dtype), _rand((Hkv, N, d), 2, dtype), _rand((Hkv, N, d), 3, dtype)
     idx = _routes(H, N, front, window, rk, 4)
     out = bigger_bird_flash(q.to(dev), k.to(dev), v.to(dev), idx.to(dev), front=front, window=window, num_heads=H,
                             kv_groups=H // Hkv, scale=scale)
     torch.cuda.synchronize()
-    assert out.shape == (H, T, d) and out.stride() == (d, H * d, 1)
+    assert out.shape == (H, T, d) and out.stride() == (d, H * d, 1) and out.dtype == dtype
     ref = oracle.attn_all(q, k, v, idx, front=front, window=window, num_heads=H, kv_groups=H // Hkv, scale=scale)
     _check(out, ref, name)
 
@@ -76,11 +78,12 @@ def test_grouped_equals_repeated(dev):
     torch.testing.assert_close(grouped, repeated, atol=2e-2, rtol=1e-3)
 
 
-def test_tail_window_n_is_dense_causal_rows(dev):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_tail_window_n_is_dense_causal_rows(dtype, dev):
     """Exact tail: front=0, window=N, no routes == dense causal rows (split-key schedule + merge)."""
-    print("case tail_split", flush=True)
+    print(f"case tail_split {dtype}", flush=True)
     H, Hkv, N, r, d = 32, 8, 4096, 256, 128
-    q, k, v = _rand((H, N, d), 21), _rand((Hkv, N, d), 22), _rand((Hkv, N, d), 23)
+    q, k, v = _rand((H, N, d), 21, dtype), _rand((Hkv, N, d), 22, dtype), _rand((Hkv, N, d), 23, dtype)
     none = torch.full((H, 1, 1), -1, dtype=torch.int32)
     Q = q.to(dev)
     out = bigger_bird_flash(Q[:, N - r:], k.to(dev), v.to(dev), none.to(dev), front=0, window=N, num_heads=H,
@@ -91,6 +94,7 @@ def test_tail_window_n_is_dense_causal_rows(dev):
     ref = torch.nn.functional.scaled_dot_product_attention(
         q[:, N - r:].double()[None], k.double().repeat_interleave(H // Hkv, 0)[None],
         v.double().repeat_interleave(H // Hkv, 0)[None], attn_mask=mask, scale=d ** -0.5)[0]
+    assert out.dtype == dtype
     _check(out, ref, "tail_split")
 
 
@@ -168,18 +172,22 @@ def test_million_token_rows_match_oracle(dev):
     _check(got, ref, "million_rows")
 
 
-@pytest.mark.parametrize("t,n,H,Hkv,d", [(2, 20000, 32, 8, 128), (65, 131072, 32, 8, 128), (300, 5000, 32, 8, 128),
-                                         (7, 3000, 8, 2, 64)])
-def test_exact_attention_noncausal(t, n, H, Hkv, d, dev):
+@pytest.mark.parametrize("t,n,H,Hkv,d,dtype", [(2, 20000, 32, 8, 128, torch.bfloat16),
+                                               (65, 131072, 32, 8, 128, torch.bfloat16),
+                                               (300, 5000, 32, 8, 128, torch.bfloat16),
+                                               (7, 3000, 8, 2, 64, torch.bfloat16),
+                                               (300, 5000, 32, 8, 128, torch.float16),
+                                               (7, 3000, 8, 2, 64, torch.float16)])
+def test_exact_attention_noncausal(t, n, H, Hkv, d, dtype, dev):
     """bb_exact_attention: t query rows, each attending all n cached keys (the reference's SDPA with is_causal=False
     for 1 < t < n, modal_rd/attention.py:140-141), in one call, against float64 SDPA; also through
     RDAttention.exact_attention on [1, H, t, d] / [1, Hkv, n, d] views."""
-    print(f"case exact_noncausal t={t} n={n} H={H}/{Hkv} d={d}", flush=True)
+    print(f"case exact_noncausal t={t} n={n} H={H}/{Hkv} d={d} {dtype}", flush=True)
     from types import SimpleNamespace
 
     from bigger_bird_amd import RDAttention, exact_attention
 
-    q, k, v = _rand((H, t, d), 71 + t), _rand((Hkv, n, d), 72), _rand((Hkv, n, d), 73)
+    q, k, v = _rand((H, t, d), 71 + t, dtype), _rand((Hkv, n, d), 72, dtype), _rand((Hkv, n, d), 73, dtype)
     ref = oracle.sdpa_ref(q, k, v, causal=False, scale=d ** -0.5, groups=H // Hkv)
     out = exact_attention(q.to(dev), k.to(dev), v.to(dev), num_heads=H, kv_groups=H // Hkv, scale=d ** -0.5)
     _check(out, ref, f"exact_noncausal t={t} n={n}")

@@ -76,11 +76,12 @@ def test_decode_bf16_matches_sdpa(dev):
     _check(out, ref, "decode_bf16")
 
 
-def test_rope_inplace_bitwise(dev):
-    print("case rope", flush=True)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_rope_inplace_bitwise(dtype, dev):
+    print(f"case rope {dtype}", flush=True)
     T, d = 5000, 128
-    cos, sin = rope_cos_sin(T, d)
-    x = _rand((1, 8, T, d), 6, 3.0)
+    cos, sin = rope_cos_sin(T, d, dtype=dtype)
+    x = _rand((1, 8, T, d), 6, 3.0).to(dtype)
     y = x.to(dev).transpose(1, 2).contiguous().transpose(1, 2)  # strided [1, H, T, d] view like q_proj output
     rope_inplace(y, cos.to(dev), sin.to(dev))
     assert torch.equal(y.cpu(), rope_host(x, cos, sin))

@@ -36,6 +36,34 @@ def test_full_budget_equals_dense_causal_sdpa():
     assert (got - want).abs().max().item() < 1e-12
 
 
+def test_fp16_decode_matches_torch_on_every_bit_pattern():
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.float16)
+    want = bits.float()
+    got = torch.tensor([oracle.lib().orc_f16_to_f32(i) for i in range(65536)], dtype=torch.float32)
+    nan = want.isnan()
+    assert torch.equal(got.isnan(), nan)
+    assert torch.equal(got[~nan].view(torch.int32), want[~nan].view(torch.int32))
+
+
+@pytest.mark.parametrize("groups", [1, 4])
+def test_fp16_full_budget_equals_dense_causal_sdpa(groups):
+    H, n, d, sink, window = 8, 260, 64, 16, 64
+    g = torch.Generator().manual_seed(21)
+    q = torch.randn(H, n, d, generator=g).half()
+    k = torch.randn(H // groups, n, d, generator=g).half()
+    v = torch.randn(H // groups, n, d, generator=g).half()
+    full = torch.arange(sink, n - window, dtype=torch.int32).expand(H, -1).contiguous()
+    got = oracle.attn_all(q, k, v, full, front=sink, window=window, num_heads=H, kv_groups=groups, scale=d ** -0.5)
+    want = oracle.sdpa_ref(q, k, v, causal=True, scale=d ** -0.5, groups=groups)
+    assert (got - want).abs().max().item() < 1e-12
+    # The same bits read as bf16 are different numbers: the element type is not ignored.
+    wrong = oracle.attn_all(q.view(torch.bfloat16), k.view(torch.bfloat16), v.view(torch.bfloat16), full, front=sink,
+                            window=window, num_heads=H, kv_groups=groups, scale=d ** -0.5)
+    assert not torch.allclose(wrong, want, atol=1e-3)
+    with pytest.raises(ValueError):
+        oracle.attn_all(q, k.view(torch.bfloat16), v, full, front=sink, window=window, num_heads=H, kv_groups=groups)
+
+
 def test_tail_window_n_equals_causal_rows():
     H, Hkv, N, r, d = 8, 2, 400, 37, 64
     q, k, v = _rand((H, N, d), 4), _rand((Hkv, N, d), 5), _rand((Hkv, N, d), 6)

@@ -6,6 +6,7 @@
   * RoPE: synth.rope_cos_sin / rope_host bit-identical to transformers' LlamaRotaryEmbedding and
     apply_rotary_pos_emb (the functions the reference's rope_inplace wraps, modal_rd/attention.py:51-60).
 """
+import pytest
 import torch
 
 import oracle
@@ -70,7 +71,8 @@ def test_decode_matches_sdpa_over_dequantised_cache():
         assert (got - want).abs().max().item() < 1e-12
 
 
-def test_rope_matches_transformers_bitwise():
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_rope_matches_transformers_bitwise(dtype):
     from transformers import LlamaConfig
     from transformers.models.llama.modeling_llama import LlamaRotaryEmbedding, apply_rotary_pos_emb
 
@@ -78,11 +80,11 @@ def test_rope_matches_transformers_bitwise():
     cfg = LlamaConfig(hidden_size=32 * d, num_attention_heads=32, num_key_value_heads=8, head_dim=d,
                       rope_theta=500000.0, max_position_embeddings=131072)
     rot = LlamaRotaryEmbedding(cfg)
-    cos, sin = rot(torch.zeros(1, T, 8, dtype=torch.bfloat16), torch.arange(T)[None])
-    c2, s2 = rope_cos_sin(T, d)
+    cos, sin = rot(torch.zeros(1, T, 8, dtype=dtype), torch.arange(T)[None])
+    c2, s2 = rope_cos_sin(T, d, dtype=dtype)
     assert torch.equal(cos[0], c2) and torch.equal(sin[0], s2)
     g = torch.Generator().manual_seed(3)
-    q = torch.randn(1, 4, T, d, generator=g).to(torch.bfloat16)
-    k = torch.randn(1, 2, T, d, generator=g).to(torch.bfloat16)
+    q = (torch.randn(1, 4, T, d, generator=g) * 3).to(dtype)
+    k = (torch.randn(1, 2, T, d, generator=g) * 3).to(dtype)
     hq, hk = apply_rotary_pos_emb(q, k, cos, sin)
     assert torch.equal(rope_host(q, c2, s2), hq) and torch.equal(rope_host(k, c2, s2), hk)

@@ -19,11 +19,11 @@ SIGNATURES = {
     "bb_version": (_i32, []),
     "bb_last_error": (ctypes.c_char_p, []),
     "bb_sparse_flash": (_i32, [_vp, c_i64p, _vp, c_i64p, _vp, c_i64p, _vp, _vp, c_i64p, _i32, _i32, _vp, _i64,
-                               _vp, c_i64p, _i32, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _i64, _f32, _i64,
+                               _vp, c_i64p, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _f32, _i64,
                                _vp, _sz, _vp]),
     "bb_sparse_flash_workspace": (_sz, [_i32, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _i32, _i32, _i64, _i32]),
     "bb_exact_attention": (_i32, [_vp, c_i64p, _vp, c_i64p, _vp, c_i64p, _vp, _vp, c_i64p, _i32, _i64, _i64, _i32, _i32,
-                                  _i32, _f32, _vp, _sz, _vp]),
+                                  _i32, _i32, _f32, _vp, _sz, _vp]),
     "bb_exact_attention_workspace": (_sz, [_i32, _i64, _i64, _i32, _i32, _i32, _i32]),
     "bb_transpose_v": (_i32, [_vp, c_i64p, _i32, _i64, _i32, _vp, _vp]),
     "bb_transpose_v_cols": (_i64, [_i64]),
@@ -38,7 +38,7 @@ SIGNATURES = {
     "bb_decode_noalloc": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp, _i32, _vp, c_i64p, _vp, c_i64p, _i64, _i32, _i32, _i32,
                                  _f32, _vp, _i64, _vp]),
     "bb_decode_noalloc_max_bytes": (_sz, []),
-    "bb_rope_inplace": (_i32, [_vp, c_i64p, _i32, _i32, _i64, _i32, _vp, _vp, c_i64p, _vp]),
+    "bb_rope_inplace": (_i32, [_vp, c_i64p, _i32, _i32, _i64, _i32, _vp, _vp, c_i64p, _i32, _vp]),
     "bb_sparse_decode": (_i32, [_vp, _i64, _vp, c_i64p, _vp, c_i64p, _vp, c_i64p, _i32, _i32, _i64, _vp, _i64, _i32,
                                 _i32, _i32, _i32, _i32, _f32, _i32, _i32, _vp, _i64, _vp, _sz, _vp]),
     "bb_sparse_decode_workspace": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32]),

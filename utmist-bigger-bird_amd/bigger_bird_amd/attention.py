@@ -27,10 +27,10 @@ def rope_inplace(x, cos, sin, chunk=ROPE_CHUNK):
     """HF `apply_rotary_pos_emb` on x [b, h, t, d] in place, bit-identical (modal_rd/attention.py:51-60).
 
     One HIP launch over the whole tensor; `chunk` is accepted for signature compatibility (the kernel needs no
-    transient buffers). cos/sin are [b, t, d] (or [t, d]) in x's dtype."""
+    transient buffers). cos/sin are [b, t, d] (or [t, d]) in x's dtype, bf16 or fp16."""
     _lib.require_gpu(x, cos, sin, what="rope_inplace")
-    if x.dtype != torch.bfloat16 or cos.dtype != torch.bfloat16 or sin.dtype != torch.bfloat16:
-        raise ValueError("rope_inplace: bf16 tensors required")
+    if x.dtype not in (torch.bfloat16, torch.float16) or cos.dtype != x.dtype or sin.dtype != x.dtype:
+        raise ValueError("rope_inplace: bf16 or fp16 tensors of one dtype required")
     b, h, t, d = x.shape
     if cos.ndim == 2:
         cos, sin = cos[None], sin[None]
@@ -38,7 +38,8 @@ def rope_inplace(x, cos, sin, chunk=ROPE_CHUNK):
     if cos.stride(-1) != 1 or sin.stride(-1) != 1 or cos.stride() != sin.stride():
         cos, sin = cos.contiguous(), sin.contiguous()
     _lib.check(_lib.lib().bb_rope_inplace(_lib.ptr(x), _lib.i64s(*x.stride()[:3]), b, h, t, d, _lib.ptr(cos),
-                                          _lib.ptr(sin), _lib.i64s(cos.stride(0), cos.stride(1)), _lib.stream_of(x)))
+                                          _lib.ptr(sin), _lib.i64s(cos.stride(0), cos.stride(1)),
+                                          int(x.dtype == torch.float16), _lib.stream_of(x)))
     return x
 
 
@@ -73,6 +74,9 @@ def routes(q, k, *, num_heads, num_kv_heads, sink, window, budget, n_route=64, r
     Returns int32 [B * H, budget], ascending per head (and the pooled scores [B * H, n] as float probabilities
     when `return_pooled`)."""
     _lib.require_gpu(q, k, what="routes")
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16:
+        # The score contract (bf16 scores in the reference's accumulation order) is defined for bf16 only.
+        raise ValueError("routes: bf16 q and k required")
     bsz = q.shape[0]
     n, d = k.shape[-2], k.shape[-1]
     r = min(n_route, n)
@@ -168,7 +172,7 @@ class RDAttention(nn.Module):
             none = torch.full((self.num_heads, 1, 1), -1, dtype=torch.int32, device=q.device)
             return bigger_bird_flash(q[0], k[0], v[0], none, front=0, window=n, num_heads=self.num_heads,
                                      kv_groups=self.groups, scale=self.scaling)[None]
-        if t == 1:
+        if t == 1 and q.dtype == torch.bfloat16:
             from .kv_int8 import decode_bf16
             return decode_bf16(q[0, :, 0], k[0], v[0], self.scaling)[None, :, None]
         # 1 < t < n: every query attends every cached key (the reference's non-causal SDPA), one launch

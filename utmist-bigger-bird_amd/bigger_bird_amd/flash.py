@@ -1,6 +1,7 @@
 """`bigger_bird_flash`: the sparse attention operator, HIP-backed (drop-in for kernels/bigger_bird_flash.py:99-138).
 
-Same arguments, shapes, output layout and ValueError conditions as the reference. One joint softmax over front
+Same arguments, shapes, output layout and ValueError conditions as the reference; fp16 and bf16 inputs, as the
+reference's kernel takes (kernels/bigger_bird_flash.py:110). One joint softmax over front
 anchors, a causal local window and routed key columns; Q [BH, T, D], K/V [BH / kv_groups, N, D] (any strides with a
 contiguous head_dim), indices [BH, G, K] int32 with -1 for empty slots; the output is a [BH, T, D] view of a
 [T, BH, D] buffer. Query row t sits at absolute position t + N - T.
@@ -16,6 +17,12 @@ from . import _lib
 
 def _next_pow2(n: int) -> int:
     return 1 << max(0, (int(n) - 1).bit_length())
+
+
+def _same_dtype(q, *others):
+    """q, k, v (and V^T / out when given) share one 16-bit dtype: the kernels read and write that type."""
+    if any(x is not None and x.dtype != q.dtype for x in others):
+        raise ValueError("q, k and v must share a dtype")
 
 
 def _operand(x: torch.Tensor) -> torch.Tensor:
@@ -44,11 +51,12 @@ def bigger_bird_flash(q, k, v, indices, *, front=64, window=256, token_mask=None
     Extensions over the reference signature (all optional): `row_end` leaves rows >= row_end unwritten (the exact
     tail overwrites them), `vt` passes a precomputed `transpose_v(v)`, `out` a preallocated [BH,T,D] destination.
     """
-    if not q.is_cuda or q.dtype != torch.bfloat16:
-        raise ValueError("HIP Bigger Bird requires ROCm BF16")
+    if not q.is_cuda or q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("HIP Bigger Bird requires ROCm FP16/BF16")
     if (k.shape != v.shape or q.ndim != 3 or q.shape[0] != k.shape[0] * kv_groups
             or q.shape[-1] != k.shape[-1] or num_heads % kv_groups):
         raise ValueError("Q [BH,T,D] and K/V [BH/kv_groups,N,D] must have matching heads and dimensions")
+    _same_dtype(q, k, v, vt, out)
     if front < 0 or window < 1:
         raise ValueError("front >= 0 and window >= 1 required")
     bh, t, d = q.shape
@@ -81,8 +89,8 @@ def bigger_bird_flash(q, k, v, indices, *, front=64, window=256, token_mask=None
         _lib.ptr(q), _lib.i64s(*q.stride()), _lib.ptr(k), _lib.i64s(*k.stride()), _lib.ptr(v), _lib.i64s(*v.stride()),
         _lib.ptr(vt), _lib.ptr(indices) if route_k else None, _lib.i64s(*indices.stride()), indices.shape[1], route_k,
         _lib.ptr(mask), mask.stride(0) if mask is not None else 0,
-        _lib.ptr(out), _lib.i64s(*out.stride()), bh, t, n, d, num_heads, kv_groups, min(front, n), window,
-        route_chunk, float(scale), re, _lib.ptr(ws), ws_bytes, _lib.stream_of(q)))
+        _lib.ptr(out), _lib.i64s(*out.stride()), bh, t, n, d, int(q.dtype == torch.float16), num_heads, kv_groups,
+        min(front, n), window, route_chunk, float(scale), re, _lib.ptr(ws), ws_bytes, _lib.stream_of(q)))
     return out
 
 
@@ -91,11 +99,12 @@ def exact_attention(q, k, v, *, num_heads, kv_groups=1, scale=1.0, vt=None, out=
     D] (T <= N). The operator behind RDAttention.exact_attention for 1 < t < n, where the reference calls
     F.scaled_dot_product_attention(q, k, v, is_causal=False, enable_gqa=True) (modal_rd/attention.py:140-141). Returns
     a [BH, T, D] view of a [T, BH, D] buffer (or writes `out`); `vt` may pass a precomputed transpose_v(v)."""
-    if not q.is_cuda or q.dtype != torch.bfloat16:
-        raise ValueError("HIP Bigger Bird requires ROCm BF16")
+    if not q.is_cuda or q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("HIP Bigger Bird requires ROCm FP16/BF16")
     if (k.shape != v.shape or q.ndim != 3 or q.shape[0] != k.shape[0] * kv_groups
             or q.shape[-1] != k.shape[-1] or num_heads % kv_groups):
         raise ValueError("Q [BH,T,D] and K/V [BH/kv_groups,N,D] must have matching heads and dimensions")
+    _same_dtype(q, k, v, vt, out)
     bh, t, d = q.shape
     n = k.shape[1]
     if n - t < 0:
@@ -111,6 +120,6 @@ def exact_attention(q, k, v, *, num_heads, kv_groups=1, scale=1.0, vt=None, out=
     ws = _lib.workspace(ws_bytes, q.device) if ws_bytes else None
     _lib.check(L.bb_exact_attention(
         _lib.ptr(q), _lib.i64s(*q.stride()), _lib.ptr(k), _lib.i64s(*k.stride()), _lib.ptr(v), _lib.i64s(*v.stride()),
-        _lib.ptr(vt), _lib.ptr(out), _lib.i64s(*out.stride()), bh, t, n, d, num_heads, kv_groups, float(scale),
-        _lib.ptr(ws), ws_bytes, _lib.stream_of(q)))
+        _lib.ptr(vt), _lib.ptr(out), _lib.i64s(*out.stride()), bh, t, n, d, int(q.dtype == torch.float16), num_heads,
+        kv_groups, float(scale), _lib.ptr(ws), ws_bytes, _lib.stream_of(q)))
     return out

@@ -135,6 +135,8 @@ def decode_int8(q, k8, ks, v8, vs, n, scale):
 def decode_bf16(q, k, v, scale):
     """q [H, d] bf16 over k/v [Hkv, n, d] (strided views of a bf16 cache)."""
     _lib.require_gpu(k, v, what="decode_bf16")
+    if k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise ValueError("decode_bf16: bf16 cache required")
     for x in (k, v):
         if x.stride(-1) != 1 or x.stride(0) % 8 or x.stride(1) % 8 or x.data_ptr() % 16:
             raise ValueError("decode_bf16: cache rows must be 16-byte aligned with a contiguous head_dim")

@@ -18,7 +18,8 @@ def rope_cos_sin(T, d, theta=500000.0, dtype=torch.bfloat16):
 
 
 def rope_host(x, cos, sin):
-    """HF apply_rotary_pos_emb arithmetic on bf16 host tensors: x*cos + rotate_half(x)*sin, rounding per op."""
+    """HF apply_rotary_pos_emb arithmetic on bf16 or fp16 host tensors: x*cos + rotate_half(x)*sin, rounding per
+    op."""
     half = x.shape[-1] // 2
     rot = torch.cat((-x[..., half:], x[..., :half]), dim=-1)
     return x * cos + rot * sin

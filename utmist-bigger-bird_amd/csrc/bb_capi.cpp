@@ -170,9 +170,9 @@ int bb_transpose_v(const void* v, const int64_t* sv, int n_kvbh, int64_t N, int 
 static int sparse_flash_impl(const void* q, const int64_t* sq, const void* k, const int64_t* sk, const void* v,
                              const int64_t* sv, const void* vt, const int32_t* idx, const int64_t* si, int n_groups,
                              int route_k, const uint8_t* key_mask, int64_t smb, void* out, const int64_t* so, int BH,
-                             int64_t T, int64_t N, int D, int num_heads, int kv_groups, int64_t front, int64_t window,
-                             int64_t route_chunk, float scale, int64_t row_end, void* ws, size_t ws_bytes,
-                             void* stream, bool noncausal) {
+                             int64_t T, int64_t N, int D, int is_f16, int num_heads, int kv_groups, int64_t front,
+                             int64_t window, int64_t route_chunk, float scale, int64_t row_end, void* ws,
+                             size_t ws_bytes, void* stream, bool noncausal) {
   g_err[0] = 0;
   if (!q || !k || !v || !out || !sq || !sk || !sv || !so)
     return fail("Q [BH,T,D] and K/V [BH/kv_groups,N,D] must have matching heads and dimensions");
@@ -215,6 +215,7 @@ static int sparse_flash_impl(const void* q, const int64_t* sq, const void* k, co
   p.smb = smb;
   p.so0 = so[0]; p.so1 = so[1];
   p.N = N; p.T = T; p.row_end = row_end;
+  p.f16 = is_f16 ? 1 : 0;
   p.offset = noncausal ? N - 1 : N - T;
   p.pos_step = noncausal ? 0 : 1;
   p.route_chunk = route_chunk;
@@ -271,11 +272,11 @@ static int sparse_flash_impl(const void* q, const int64_t* sq, const void* k, co
 int bb_sparse_flash(const void* q, const int64_t* sq, const void* k, const int64_t* sk, const void* v,
                     const int64_t* sv, const void* vt, const int32_t* idx, const int64_t* si, int n_groups,
                     int route_k, const uint8_t* key_mask, int64_t smb, void* out, const int64_t* so, int BH, int64_t T,
-                    int64_t N, int D, int num_heads, int kv_groups, int64_t front, int64_t window,
+                    int64_t N, int D, int is_f16, int num_heads, int kv_groups, int64_t front, int64_t window,
                     int64_t route_chunk, float scale, int64_t row_end, void* ws, size_t ws_bytes, void* stream) {
   return sparse_flash_impl(q, sq, k, sk, v, sv, vt, idx, si, n_groups, route_k, key_mask, smb, out, so, BH, T, N, D,
-                           num_heads, kv_groups, front, window, route_chunk, scale, row_end, ws, ws_bytes, stream,
-                           false);
+                           is_f16, num_heads, kv_groups, front, window, route_chunk, scale, row_end, ws, ws_bytes,
+                           stream, false);
 }
 
 size_t bb_exact_attention_workspace(int BH, int64_t T, int64_t N, int D, int num_heads, int kv_groups, int have_vt) {
@@ -284,10 +285,11 @@ size_t bb_exact_attention_workspace(int BH, int64_t T, int64_t N, int D, int num
 
 int bb_exact_attention(const void* q, const int64_t* sq, const void* k, const int64_t* sk, const void* v,
                        const int64_t* sv, const void* vt, void* out, const int64_t* so, int BH, int64_t T, int64_t N,
-                       int D, int num_heads, int kv_groups, float scale, void* ws, size_t ws_bytes, void* stream) {
+                       int D, int is_f16, int num_heads, int kv_groups, float scale, void* ws, size_t ws_bytes,
+                       void* stream) {
   const int64_t si[3] = {0, 0, 0};
-  return sparse_flash_impl(q, sq, k, sk, v, sv, vt, nullptr, si, 1, 0, nullptr, 0, out, so, BH, T, N, D, num_heads,
-                           kv_groups, 0, N, N, scale, T, ws, ws_bytes, stream, true);
+  return sparse_flash_impl(q, sq, k, sk, v, sv, vt, nullptr, si, 1, 0, nullptr, 0, out, so, BH, T, N, D, is_f16,
+                           num_heads, kv_groups, 0, N, N, scale, T, ws, ws_bytes, stream, true);
 }
 
 size_t bb_routes_workspace(int64_t n, int H, int Hkv, int B, int r) {
@@ -638,7 +640,7 @@ int bb_argmax(const void* x, int64_t n, int dtype, int64_t* out, void* stream) {
 }
 
 int bb_rope_inplace(void* x, const int64_t* sx, int B, int Hh, int64_t T, int D, const void* cos, const void* sin,
-                    const int64_t* sc, void* stream) {
+                    const int64_t* sc, int is_f16, void* stream) {
   g_err[0] = 0;
   if (!x || !cos || !sin || !sx || !sc) return fail("rope: null argument");
   if (D % 16) return fail("rope: head_dim must be a multiple of 16");
@@ -647,7 +649,7 @@ int bb_rope_inplace(void* x, const int64_t* sx, int B, int Hh, int64_t T, int D,
     return fail("rope: rows must be 16-byte aligned");
   return hip_status(bb::launch_rope(static_cast<uint16_t*>(x), sx[0], sx[1], sx[2], B, Hh, T, D,
                                     static_cast<const uint16_t*>(cos), static_cast<const uint16_t*>(sin), sc[0], sc[1],
-                                    static_cast<hipStream_t>(stream)),
+                                    is_f16 ? 1 : 0, static_cast<hipStream_t>(stream)),
                     "bb_rope_inplace");
 }
 

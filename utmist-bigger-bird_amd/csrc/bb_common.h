@@ -39,6 +39,36 @@ BB_DEV f32x16_t mfma32(bf16x8_t a, bf16x8_t b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// The 16-bit element type of a kernel instantiation: bf16, or fp16 when F16. Fragments travel as 16-byte bit
+// patterns (bf16x8_t); the MFMA and the float -> 16-bit conversions (round to nearest even) follow the type.
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8_t;
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+template <bool F16>
+BB_DEV f32x16_t mma32(bf16x8_t a, bf16x8_t b, f32x16_t c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                  0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+template <bool F16>
+BB_DEV uint32_t pack2(float a, float b) {
+  if constexpr (F16) {
+    const f16x2_t v = {(_Float16)a, (_Float16)b};
+    return __builtin_bit_cast(uint32_t, v);
+  } else {
+    return pack_bf16x2(a, b);
+  }
+}
+
+template <bool F16>
+BB_DEV uint16_t to16(float f) {
+  if constexpr (F16) return __builtin_bit_cast(uint16_t, (_Float16)f);
+  else return f32_to_bf16(f);
+}
+
 // Value of the partner lane l ^ 32 combined with this lane's value.
 BB_DEV float xhalf_max(float v) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);

@@ -33,7 +33,7 @@ namespace bb {
 namespace {
 
 // One 64-key tile for one wave: S^T = K Q^T, online softmax, O^T += V^T P^T.
-template <int D, int QB, bool MASKED, typename Mask>
+template <bool F16, int D, int QB, bool MASKED, typename Mask>
 BB_DEV void tile_step(WaveState<D, QB>& st, const uint16_t* kl, const uint16_t* vt, int lane, float c, int64_t qabs0,
                       int64_t step, const Mask& mask) {
   const int h = lane >> 5, li = lane & 31;
@@ -48,7 +48,7 @@ BB_DEV void tile_step(WaveState<D, QB>& st, const uint16_t* kl, const uint16_t* 
     for (int dk = 0; dk < D / 16; ++dk) {
       const bf16x8_t a = as_bf16x8(*reinterpret_cast<const u32x4_t*>(kl + k_off<D>(32 * kb + li, 2 * dk + h)));
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) s[qb][kb] = mfma32(a, st.qf[qb][dk], s[qb][kb]);
+      for (int qb = 0; qb < QB; ++qb) s[qb][kb] = mma32<F16>(a, st.qf[qb][dk], s[qb][kb]);
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -92,8 +92,8 @@ BB_DEV void tile_step(WaveState<D, QB>& st, const uint16_t* kl, const uint16_t* 
           p[e] = fast_exp2(fmaf(s[qb][kb][8 * u + e], c, nm));
           sum += p[e];
         }
-        pk[qb][kb][u] = as_bf16x8(u32x4_t{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
-                                          pack_bf16x2(p[6], p[7])});
+        pk[qb][kb][u] = as_bf16x8(u32x4_t{pack2<F16>(p[0], p[1]), pack2<F16>(p[2], p[3]), pack2<F16>(p[4], p[5]),
+                                          pack2<F16>(p[6], p[7])});
       }
     }
     st.l[qb] += sum;
@@ -109,13 +109,13 @@ BB_DEV void tile_step(WaveState<D, QB>& st, const uint16_t* kl, const uint16_t* 
         const int d = 32 * dv + li;
         const bf16x8_t a = as_bf16x8(*reinterpret_cast<const u32x4_t*>(vt + vt_off(d, unit)));
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) st.o[qb][dv] = mfma32(a, pk[qb][kb][u], st.o[qb][dv]);
+        for (int qb = 0; qb < QB; ++qb) st.o[qb][dv] = mma32<F16>(a, pk[qb][kb][u], st.o[qb][dv]);
       }
     }
   }
 }
 
-template <int D, int NW, int HPW, bool SPLIT, bool HAS_MASK>
+template <bool F16, int D, int NW, int HPW, bool SPLIT, bool HAS_MASK>
 __global__ __launch_bounds__(64 * NW, 1) void flash_kernel(FlashParams p) {
   constexpr int QB = 256 / 32 / NW;  // 32-row query blocks per wave (256 query rows per workgroup)
   constexpr int WPH = NW / HPW;      // waves per head
@@ -229,9 +229,9 @@ __global__ __launch_bounds__(64 * NW, 1) void flash_kernel(FlashParams p) {
           const bool full = !HAS_MASK && k1 <= qw0 && k1 < p.N && (k1 < p.front || k0 >= qw1 - p.window + 1);
           const WindowMask wm{k0, p.N, p.front, p.window, km};
           if (full)
-            tile_step<D, QB, false>(st, tile_k(cur), tile_v(cur), lane, p.c, qw0, p.pos_step, wm);
+            tile_step<F16, D, QB, false>(st, tile_k(cur), tile_v(cur), lane, p.c, qw0, p.pos_step, wm);
           else
-            tile_step<D, QB, true>(st, tile_k(cur), tile_v(cur), lane, p.c, qw0, p.pos_step, wm);
+            tile_step<F16, D, QB, true>(st, tile_k(cur), tile_v(cur), lane, p.c, qw0, p.pos_step, wm);
         }
       }
       wait_vm();
@@ -311,7 +311,7 @@ __global__ __launch_bounds__(64 * NW, 1) void flash_kernel(FlashParams p) {
         __syncthreads();
         if (head_work && bi < my_batches) {
           const RoutedMask rm{route_keys[slot], p.window, p.route_chunk, g, km};
-          tile_step<D, QB, true>(st, kl, vt, lane, p.c, qw0, p.pos_step, rm);
+          tile_step<F16, D, QB, true>(st, kl, vt, lane, p.c, qw0, p.pos_step, rm);
         }
         __syncthreads();
       }
@@ -350,8 +350,8 @@ __global__ __launch_bounds__(64 * NW, 1) void flash_kernel(FlashParams p) {
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
           const int d0 = 32 * dv + 8 * g4 + 4 * h;
-          const u32x2_t w = {pack_bf16x2(st.o[qb][dv][4 * g4] * inv, st.o[qb][dv][4 * g4 + 1] * inv),
-                             pack_bf16x2(st.o[qb][dv][4 * g4 + 2] * inv, st.o[qb][dv][4 * g4 + 3] * inv)};
+          const u32x2_t w = {pack2<F16>(st.o[qb][dv][4 * g4] * inv, st.o[qb][dv][4 * g4 + 1] * inv),
+                             pack2<F16>(st.o[qb][dv][4 * g4 + 2] * inv, st.o[qb][dv][4 * g4 + 3] * inv)};
           *reinterpret_cast<u32x2_t*>(orow + d0) = w;
         }
     }
@@ -359,7 +359,7 @@ __global__ __launch_bounds__(64 * NW, 1) void flash_kernel(FlashParams p) {
 }
 
 // Combine split partials: one wave per (head, row); lanes cover D.
-template <int D>
+template <bool F16, int D>
 __global__ __launch_bounds__(256) void flash_merge_kernel(FlashParams p) {
   const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -394,7 +394,7 @@ __global__ __launch_bounds__(256) void flash_merge_kernel(FlashParams p) {
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int d = lane + 64 * i;
-    if (d < D) orow[d] = f32_to_bf16(acc[i] * inv);
+    if (d < D) orow[d] = to16<F16>(acc[i] * inv);
   }
 }
 
@@ -437,10 +437,14 @@ hipError_t launch_dhs(const FlashParams& p, hipStream_t stream) {
   const int64_t items = (int64_t)p.n_kvbh * p.head_splits * p.row_tiles * p.n_chunks;
   if (items <= 0) return hipSuccess;
   if (items > 0x7fffffff) return hipErrorInvalidValue;
-  if (p.key_mask)
-    hipLaunchKernelGGL((flash_kernel<D, NW, HPW, SPLIT, true>), dim3((unsigned)items), dim3(64 * NW), 0, stream, p);
-  else
-    hipLaunchKernelGGL((flash_kernel<D, NW, HPW, SPLIT, false>), dim3((unsigned)items), dim3(64 * NW), 0, stream, p);
+  const dim3 grid((unsigned)items), block(64 * NW);
+  if (p.f16) {
+    if (p.key_mask) hipLaunchKernelGGL((flash_kernel<true, D, NW, HPW, SPLIT, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((flash_kernel<true, D, NW, HPW, SPLIT, false>), grid, block, 0, stream, p);
+  } else {
+    if (p.key_mask) hipLaunchKernelGGL((flash_kernel<false, D, NW, HPW, SPLIT, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((flash_kernel<false, D, NW, HPW, SPLIT, false>), grid, block, 0, stream, p);
+  }
   return hipGetLastError();
 }
 
@@ -476,9 +480,9 @@ hipError_t launch_flash_merge(const FlashParams& p, int D, hipStream_t stream) {
   if (items <= 0) return hipSuccess;
   const unsigned blocks = (unsigned)((items + 3) / 4);
   switch (D) {
-    case 32: hipLaunchKernelGGL(flash_merge_kernel<32>, dim3(blocks), dim3(256), 0, stream, p); break;
-    case 64: hipLaunchKernelGGL(flash_merge_kernel<64>, dim3(blocks), dim3(256), 0, stream, p); break;
-    case 128: hipLaunchKernelGGL(flash_merge_kernel<128>, dim3(blocks), dim3(256), 0, stream, p); break;
+    case 32: if (p.f16) hipLaunchKernelGGL((flash_merge_kernel<true, 32>), dim3(blocks), dim3(256), 0, stream, p); else hipLaunchKernelGGL((flash_merge_kernel<false, 32>), dim3(blocks), dim3(256), 0, stream, p); break;
+    case 64: if (p.f16) hipLaunchKernelGGL((flash_merge_kernel<true, 64>), dim3(blocks), dim3(256), 0, stream, p); else hipLaunchKernelGGL((flash_merge_kernel<false, 64>), dim3(blocks), dim3(256), 0, stream, p); break;
+    case 128: if (p.f16) hipLaunchKernelGGL((flash_merge_kernel<true, 128>), dim3(blocks), dim3(256), 0, stream, p); else hipLaunchKernelGGL((flash_merge_kernel<false, 128>), dim3(blocks), dim3(256), 0, stream, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

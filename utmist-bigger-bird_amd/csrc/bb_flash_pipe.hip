@@ -149,6 +149,7 @@ struct PingState {
 };
 
 // S(t) = K Q^T (16 MFMAs).
+template <bool F16>
 BB_DEV void ping_qk(PingState& st, const uint16_t* kl, int li, int h) {
   st.s[0] = f32x16_t{};
   st.s[1] = f32x16_t{};
@@ -157,11 +158,12 @@ BB_DEV void ping_qk(PingState& st, const uint16_t* kl, int li, int h) {
 #pragma unroll
     for (int dk = 0; dk < PD / 16; ++dk) {
       const bf16x8_t a = as_bf16x8(*reinterpret_cast<const u32x4_t*>(kl + k_off<PD>(32 * kb + li, 2 * dk + h)));
-      st.s[kb] = mfma32(a, st.qf[dk], st.s[kb]);
+      st.s[kb] = mma32<F16>(a, st.qf[dk], st.s[kb]);
     }
 }
 
 // O^T += V^T P^T (16 MFMAs).
+template <bool F16>
 BB_DEV void ping_pv(PingState& st, const uint16_t* vt, int li, int h) {
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
@@ -171,7 +173,7 @@ BB_DEV void ping_pv(PingState& st, const uint16_t* vt, int li, int h) {
 #pragma unroll
       for (int dv = 0; dv < PD / 32; ++dv) {
         const int d = 32 * dv + li;
-        st.o[dv] = mfma32(as_bf16x8(*reinterpret_cast<const u32x4_t*>(vt + vt_off(d, unit))), st.pk[kb][u], st.o[dv]);
+        st.o[dv] = mma32<F16>(as_bf16x8(*reinterpret_cast<const u32x4_t*>(vt + vt_off(d, unit))), st.pk[kb][u], st.o[dv]);
       }
     }
 }
@@ -190,6 +192,7 @@ BB_DEV const u32x4_t* ping_frag(const uint16_t* kl, const uint16_t* vt, int i, i
   return reinterpret_cast<const u32x4_t*>(kl + k_off<PD>(32 * kb + li, 2 * dk + h));
 }
 
+template <bool F16>
 BB_DEV void ping_mfma_phase(PingState& st, const uint16_t* kl, const uint16_t* vt, int li, int h) {
   u32x4_t ring[kRing];
 #pragma unroll
@@ -201,10 +204,10 @@ BB_DEV void ping_mfma_phase(PingState& st, const uint16_t* kl, const uint16_t* v
     const bf16x8_t a = as_bf16x8(ring[i % kRing]);
     if (i < 16) {
       const int kb = i / 8, u = (i / 4) % 2, dv = i % 4;
-      st.o[dv] = mfma32(a, st.pk[kb][u], st.o[dv]);
+      st.o[dv] = mma32<F16>(a, st.pk[kb][u], st.o[dv]);
     } else {
       const int j = i - 16, kb = j / 8, dk = j % 8;
-      st.s[kb] = mfma32(a, st.qf[dk], st.s[kb]);
+      st.s[kb] = mma32<F16>(a, st.qf[dk], st.s[kb]);
     }
     if (i + kRing < 32) ring[i % kRing] = *ping_frag(kl, vt, i + kRing, li, h);
     __builtin_amdgcn_sched_barrier(0);
@@ -212,6 +215,7 @@ BB_DEV void ping_mfma_phase(PingState& st, const uint16_t* kl, const uint16_t* v
 }
 
 // P(t) = 2^(S(t) c - m) as bf16 MFMA fragments; returns this lane's sum of the fp32 values.
+template <bool F16>
 BB_DEV float ping_exp(PingState& st, float c) {
   const float nm = -st.m;
   float sum = 0.0f;
@@ -225,8 +229,8 @@ BB_DEV float ping_exp(PingState& st, float c) {
         pe[e] = fast_exp2(fmaf(st.s[kb][8 * u + e], c, nm));
         sum += pe[e];
       }
-      st.pk[kb][u] = as_bf16x8(u32x4_t{pack_bf16x2(pe[0], pe[1]), pack_bf16x2(pe[2], pe[3]),
-                                       pack_bf16x2(pe[4], pe[5]), pack_bf16x2(pe[6], pe[7])});
+      st.pk[kb][u] = as_bf16x8(u32x4_t{pack2<F16>(pe[0], pe[1]), pack2<F16>(pe[2], pe[3]),
+                                       pack2<F16>(pe[4], pe[5]), pack2<F16>(pe[6], pe[7])});
     }
   return sum;
 }
@@ -253,7 +257,7 @@ BB_DEV void ping_rescale(PingState& st, bool need, float mt) {
 
 // Online softmax of a masked tile S(t) into P(t): running offset m (log2 units), sum l, O rescaled when the tile
 // maximum exceeds m by more than kRescaleThreshold.
-template <typename Mask>
+template <bool F16, typename Mask>
 BB_DEV void ping_softmax_masked(PingState& st, float c, int64_t q, const Mask& mask, int h) {
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
@@ -265,15 +269,16 @@ BB_DEV void ping_softmax_masked(PingState& st, float c, int64_t q, const Mask& m
   const float mt = ping_tile_max(st, c);
   const bool need = mt > st.m + kRescaleThreshold;
   if (__builtin_amdgcn_ballot_w64(need)) ping_rescale(st, need, mt);
-  st.l += ping_exp(st, c);
+  st.l += ping_exp<F16>(st, c);
 }
 
 // Online softmax of a tile with no masked element. The tile is exponentiated against the current offset first;
 // only when a probability may exceed 2^kRescaleThreshold (this lane's or the partner lane's sum does: every term is
 // at most the sum; an infinite or NaN sum counts too) is the tile maximum taken, the offset moved and the tile
 // exponentiated again. Same bound on P as the masked form, without a maximum per tile in the common case.
+template <bool F16>
 BB_DEV void ping_softmax_open(PingState& st, float c) {
-  float sum = ping_exp(st, c);
+  float sum = ping_exp<F16>(st, c);
   const float lim = __builtin_amdgcn_exp2f(kRescaleThreshold);
   const bool over = !(sum <= lim);
   const auto sw = __builtin_amdgcn_permlane32_swap((uint32_t)over, (uint32_t)over, false, false);
@@ -282,11 +287,12 @@ BB_DEV void ping_softmax_open(PingState& st, float c) {
     const float mt = ping_tile_max(st, c);
     // the new offset never goes below the old one, so rows that do not need it keep theirs
     ping_rescale(st, need, __builtin_elementwise_maximum(mt, st.m));
-    sum = ping_exp(st, c);
+    sum = ping_exp<F16>(st, c);
   }
   st.l += sum;
 }
 
+template <bool F16>
 __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) {
   __shared__ __attribute__((aligned(1024))) uint16_t smem[PLDS];
   __shared__ __attribute__((aligned(16))) int32_t route_keys[PHEADS][kRouteCache];
@@ -405,11 +411,11 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
   // VALU phase of tile t: the lazy softmax for unmasked tiles, the masked one (front | causal window) otherwise
   auto softmax = [&](int t) {
     if (t < nu) {
-      ping_softmax_open(st, p.c);
+      ping_softmax_open<F16>(st, p.c);
     } else {
       const int64_t k0 = upos(t), k1 = k0 + kTileKeys - 1;
       const bool live = wave_live && k0 <= qw1 && !(k0 >= p.front && k1 <= qw0 - p.window);
-      ping_softmax_masked(st, p.c, qme, PipeWindowMask{k0, p.front, p.window, live}, h);
+      ping_softmax_masked<F16>(st, p.c, qme, PipeWindowMask{k0, p.front, p.window, live}, h);
     }
   };
 
@@ -427,7 +433,7 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
     if (rbk == 1) ring_barrier();  // waves 4..7 run one phase behind
     // tile 0: QK only
     if (ntot > 2) ld.tile(kst(2), vst(2), upos(2));
-    ping_qk(st, kst(0), li, h);
+    ping_qk<F16>(st, kst(0), li, h);
     vm_wait_tile(ntot > 2);
     ring_barrier();
     softmax(0);
@@ -437,21 +443,21 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
     for (int t = 1; t < nu; ++t) {
       // MFMA phase: PV of tile t-1, QK of tile t
       __builtin_amdgcn_s_setprio(1);
-      ping_mfma_phase(st, kst(t), vst(t - 1), li, h);
+      ping_mfma_phase<F16>(st, kst(t), vst(t - 1), li, h);
       __builtin_amdgcn_s_setprio(0);
       vm_wait_tile(false);  // tile t+1 has landed
       ring_barrier();
       // VALU phase: softmax of tile t, then tile t+2 starts loading into the stage tile t-2 used (every wave is past
       // the MFMA phase that last read it). The loads come after the exponentials: issuing a direct load stalls the
       // wave for as long as the CU's address unit is busy with the other waves' loads.
-      ping_softmax_open(st, p.c);
+      ping_softmax_open<F16>(st, p.c);
       if (t + 2 < ntot) ld.tile(kst(t + 2), vst(t + 2), upos(t + 2));
       ring_barrier();
     }
 #pragma unroll 1
     for (int t = nu > 1 ? nu : 1; t < ntot; ++t) {
       __builtin_amdgcn_s_setprio(1);
-      ping_mfma_phase(st, kst(t), vst(t - 1), li, h);
+      ping_mfma_phase<F16>(st, kst(t), vst(t - 1), li, h);
       __builtin_amdgcn_s_setprio(0);
       vm_wait_tile(false);
       ring_barrier();
@@ -459,7 +465,7 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
       if (t + 2 < ntot) ld.tile(kst(t + 2), vst(t + 2), upos(t + 2));
       ring_barrier();
     }
-    ping_pv(st, vst(ntot - 1), li, h);
+    ping_pv<F16>(st, vst(ntot - 1), li, h);
     if (rbk == 0) ring_barrier();  // realign the two groups
   }
 
@@ -525,9 +531,9 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
           __syncthreads();
           if (work && wave_live) {
             const PipeRoutedMask rm{keys, p.window, p.route_chunk, g};
-            ping_qk(st, kl, li, h);
-            ping_softmax_masked(st, p.c, qme, rm, h);
-            ping_pv(st, vt, li, h);
+            ping_qk<F16>(st, kl, li, h);
+            ping_softmax_masked<F16>(st, p.c, qme, rm, h);
+            ping_pv<F16>(st, vt, li, h);
           }
           __syncthreads();
         }
@@ -562,8 +568,8 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
       const int d0 = 32 * dv + 8 * g4 + 4 * h;
-      const u32x2_t w = {pack_bf16x2(st.o[dv][4 * g4] * inv, st.o[dv][4 * g4 + 1] * inv),
-                         pack_bf16x2(st.o[dv][4 * g4 + 2] * inv, st.o[dv][4 * g4 + 3] * inv)};
+      const u32x2_t w = {pack2<F16>(st.o[dv][4 * g4] * inv, st.o[dv][4 * g4 + 1] * inv),
+                         pack2<F16>(st.o[dv][4 * g4 + 2] * inv, st.o[dv][4 * g4 + 3] * inv)};
       *reinterpret_cast<u32x2_t*>(orow + d0) = w;
     }
 }
@@ -638,7 +644,8 @@ hipError_t launch_flash_pipe(const FlashParams& p, hipStream_t stream) {
   const int64_t items = (int64_t)p.n_kvbh * p.head_splits * p.row_tiles * p.n_chunks;
   if (items <= 0) return hipSuccess;
   if (items > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(flash_ping_kernel, dim3((unsigned)items), dim3(64 * PNW), 0, stream, p);
+  if (p.f16) hipLaunchKernelGGL(flash_ping_kernel<true>, dim3((unsigned)items), dim3(64 * PNW), 0, stream, p);
+  else hipLaunchKernelGGL(flash_ping_kernel<false>, dim3((unsigned)items), dim3(64 * PNW), 0, stream, p);
   return hipGetLastError();
 }
 

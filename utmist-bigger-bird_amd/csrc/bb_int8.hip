@@ -510,8 +510,26 @@ hipError_t launch_decode_d(const DecodeParams& p, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// RoPE: x' = bf16(bf16(x * cos) + bf16(rotate_half(x) * sin)), rotate_half(x) = cat(-x2, x1): the arithmetic of
-// HF apply_rotary_pos_emb on bf16 tensors (each torch op rounds to bf16), so results are bit-identical.
+// RoPE: x' = r(r(x * cos) + r(rotate_half(x) * sin)), rotate_half(x) = cat(-x2, x1), r = rounding to the tensor
+// dtype (bf16, or fp16 when F16): the arithmetic of HF apply_rotary_pos_emb on 16-bit tensors (each torch op computes
+// in fp32 and rounds to the tensor dtype), so results are bit-identical.
+template <bool F16>
+BB_DEV float from16(uint16_t h) {
+  if constexpr (F16) return (float)__builtin_bit_cast(_Float16, h);
+  else return bf16_to_f32(h);
+}
+
+// x rounded to the element type and back, as one materialised value. HF rounds each product before the add; for fp16
+// the compiler would otherwise shrink the rounding into a half-precision multiply and fuse it with the add (one fma,
+// one rounding), so the rounded bits pass through an empty asm it cannot see into.
+template <bool F16>
+BB_DEV float round16(float x) {
+  uint32_t h = to16<F16>(x);
+  asm volatile("" : "+v"(h));
+  return from16<F16>((uint16_t)h);
+}
+
+template <bool F16>
 __global__ __launch_bounds__(256) void rope_kernel(uint16_t* __restrict__ x, int64_t sx0, int64_t sx1, int64_t sx2,
                                                    int B, int Hh, int64_t T, int D, const uint16_t* __restrict__ cs,
                                                    const uint16_t* __restrict__ sn, int64_t sc0, int64_t sc1) {
@@ -539,16 +557,16 @@ __global__ __launch_bounds__(256) void rope_kernel(uint16_t* __restrict__ x, int
 #pragma unroll
     for (int hw = 0; hw < 2; ++hw) {
       const int sh = 16 * hw;
-      const float a1 = bf16_to_f32((uint16_t)(x1[w] >> sh)), a2 = bf16_to_f32((uint16_t)(x2[w] >> sh));
-      const float fc1 = bf16_to_f32((uint16_t)(c1[w] >> sh)), fc2 = bf16_to_f32((uint16_t)(c2[w] >> sh));
-      const float fs1 = bf16_to_f32((uint16_t)(s1[w] >> sh)), fs2 = bf16_to_f32((uint16_t)(s2[w] >> sh));
+      const float a1 = from16<F16>((uint16_t)(x1[w] >> sh)), a2 = from16<F16>((uint16_t)(x2[w] >> sh));
+      const float fc1 = from16<F16>((uint16_t)(c1[w] >> sh)), fc2 = from16<F16>((uint16_t)(c2[w] >> sh));
+      const float fs1 = from16<F16>((uint16_t)(s1[w] >> sh)), fs2 = from16<F16>((uint16_t)(s2[w] >> sh));
       // first half: x1*cos1 + (-x2)*sin1 ; second half: x2*cos2 + x1*sin2
-      const float p1 = bf16_to_f32(f32_to_bf16(a1 * fc1));
-      const float q1 = bf16_to_f32(f32_to_bf16(-a2 * fs1));
-      const float p2 = bf16_to_f32(f32_to_bf16(a2 * fc2));
-      const float q2 = bf16_to_f32(f32_to_bf16(a1 * fs2));
-      r1 |= (uint32_t)f32_to_bf16(p1 + q1) << sh;
-      r2 |= (uint32_t)f32_to_bf16(p2 + q2) << sh;
+      const float p1 = round16<F16>(a1 * fc1);
+      const float q1 = round16<F16>(-a2 * fs1);
+      const float p2 = round16<F16>(a2 * fc2);
+      const float q2 = round16<F16>(a1 * fs2);
+      r1 |= (uint32_t)to16<F16>(p1 + q1) << sh;
+      r2 |= (uint32_t)to16<F16>(p2 + q2) << sh;
     }
     o1[w] = r1;
     o2[w] = r2;
@@ -604,11 +622,14 @@ hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
 }
 
 hipError_t launch_rope(uint16_t* x, int64_t sx0, int64_t sx1, int64_t sx2, int B, int Hh, int64_t T, int D,
-                       const uint16_t* cos, const uint16_t* sin, int64_t sc0, int64_t sc1, hipStream_t stream) {
+                       const uint16_t* cos, const uint16_t* sin, int64_t sc0, int64_t sc1, int f16, hipStream_t stream) {
   const int64_t total = (int64_t)B * Hh * T * (D / 16);
   if (total <= 0) return hipSuccess;
-  hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, x, sx0, sx1, sx2, B, Hh,
-                     T, D, cos, sin, sc0, sc1);
+  const dim3 grid((unsigned)((total + 255) / 256));
+  if (f16)
+    hipLaunchKernelGGL(rope_kernel<true>, grid, dim3(256), 0, stream, x, sx0, sx1, sx2, B, Hh, T, D, cos, sin, sc0, sc1);
+  else
+    hipLaunchKernelGGL(rope_kernel<false>, grid, dim3(256), 0, stream, x, sx0, sx1, sx2, B, Hh, T, D, cos, sin, sc0, sc1);
   return hipGetLastError();
 }
 

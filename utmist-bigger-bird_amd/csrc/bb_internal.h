@@ -21,6 +21,7 @@ struct FlashParams {
   int64_t pos_step;         // absolute position of query row t = offset + t * pos_step (0: every row at offset)
   const uint16_t* rtiles;   // pre-gathered routed tiles [BH][n_groups][rt_batches][K tile | V^T tile], or null
   int rt_batches;           // 64-slot batches of one route list (route_k rounded up to 64)
+  int f16;                  // 16-bit element type: 0 bf16, 1 fp16
   int BH, H, G, Hkv_pb, n_kvbh, front, window, route_k, n_groups;
   int row_tiles, head_splits, n_chunks, remap, waves;
   float c;  // scale * log2(e)
@@ -144,8 +145,8 @@ hipError_t launch_rms_norm(const uint16_t* x, int64_t sx, int rows, int D, const
 hipError_t launch_argmax(const void* x, int64_t n, int kind, bool vec16, int64_t* out, hipStream_t stream);
 hipError_t launch_f32_keys(const float* vals, int64_t sv0, int rows, int64_t n, uint64_t* keys, hipStream_t stream);
 
-// RoPE in place (HF apply_rotary_pos_emb arithmetic in bf16).
+// RoPE in place (HF apply_rotary_pos_emb arithmetic in bf16, or fp16 when f16).
 hipError_t launch_rope(uint16_t* x, int64_t sx0, int64_t sx1, int64_t sx2, int B, int Hh, int64_t T, int D,
-                       const uint16_t* cos, const uint16_t* sin, int64_t sc0, int64_t sc1, hipStream_t stream);
+                       const uint16_t* cos, const uint16_t* sin, int64_t sc0, int64_t sc1, int f16, hipStream_t stream);
 
 }  // namespace bb
