@@ -49,6 +49,8 @@ def parse_args():
                     help="only run the full-model prefill (BASELINE configs[2]): random-init Llama-3-8B, sparse and exact arms")
     ap.add_argument("--no-full-model", action="store_true",
                     help="skip the full-model leg (BASELINE configs[2]) that the default run adds after the headline")
+    ap.add_argument("--no-length-sweep", action="store_true",
+                    help="skip the per-layer sparse time at 32K..1M tokens (the reference's attn_bench sweep)")
     ap.add_argument("--no-short-arm", action="store_true",
                     help="skip the B=4, T=32768 sparse-vs-dense leg (BASELINE configs[3])")
     ap.add_argument("--copy-probe", action="store_true",
@@ -381,6 +383,62 @@ def short_arm_leg(dev, seed):
     return res
 
 
+# The reference's attention-only per-layer sparse cost on H100 (modal_rd/RESULTS.md:56-62), in ms.
+H100_SWEEP_MS = {32768: 30, 65536: 61, 131072: 125, 262144: 251, 524288: 508, 1048576: 1038}
+
+
+def length_sweep_leg(dev, seed, cfg, dense_max=131072):
+    """The reference's attn_bench sweep (modal_rd/attn_bench.py:31-54): one RDAttention layer with cfg
+    {64, 16384, 512, 256} on N(0, 1) bf16 Q/K/V (32q/8kv heads, d=128, no RoPE) at 32K..1M tokens, best of 3 after
+    a warm-up call, routes + V^T + main + tail. Dense causal attention (torch SDPA, flash backend, K/V repeated) is
+    timed up to `dense_max` tokens only: past that it costs seconds per call."""
+    import torch
+    import torch.nn.functional as F
+    from bigger_bird_amd import RDAttention
+
+    H, Hkv, d = 32, 8, 128
+    attn = RDAttention(stub_base(H, Hkv, d), **cfg)
+
+    def timed(fn, reps=3):
+        fn()
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            best = min(best, a.elapsed_time(b))
+        return best
+
+    rows = []
+    for n in sorted(H100_SWEEP_MS):
+        print(f"bench: length sweep T={n}", file=sys.stderr, flush=True)
+        g = torch.Generator(device=dev).manual_seed(seed + n)
+        q = torch.randn(1, H, n, d, device=dev, dtype=torch.bfloat16, generator=g)
+        k = torch.randn(1, Hkv, n, d, device=dev, dtype=torch.bfloat16, generator=g)
+        v = torch.randn(1, Hkv, n, d, device=dev, dtype=torch.bfloat16, generator=g)
+        row = {"tokens": n}
+        with torch.inference_mode():
+            row["sparse_ms"] = round(timed(lambda: attn.sparse_prefill(q, k, v)), 3)
+            if n <= dense_max:
+                from torch.nn.attention import SDPBackend, sdpa_kernel
+                kr, vr = k.repeat_interleave(H // Hkv, dim=1), v.repeat_interleave(H // Hkv, dim=1)
+                with sdpa_kernel(SDPBackend.FLASH_ATTENTION):
+                    row["dense_ms"] = round(timed(lambda: F.scaled_dot_product_attention(
+                        q, kr, vr, is_causal=True, scale=d ** -0.5)), 3)
+                row["speedup"] = round(row["dense_ms"] / row["sparse_ms"], 2)
+                del kr, vr
+        row["h100_sparse_ms"] = H100_SWEEP_MS[n]
+        row["vs_h100"] = round(row["sparse_ms"] / H100_SWEEP_MS[n], 4)
+        rows.append(row)
+        del q, k, v
+        torch.cuda.empty_cache()
+    return {"workload": "modal_rd/attn_bench.py sweep: 1 layer, B=1, 32q/8kv, d=128, cfg {64, 16384, 512, 256}, "
+                        "N(0,1) bf16 Q/K/V, best of 3", "rows": rows}
+
+
 def graph_decode_leg(model, ids, steps=32):
     """Greedy decode after the sparse prefill (modal_rd/graph_decode.py): prefill into the decoder's buffers, then
     one HIP graph per token (32 layers of split-K flash decoding over the whole cache + projections, MLP, lm_head,
@@ -600,6 +658,8 @@ def main():
         "short_arm": None if args.no_short_arm else short_arm_leg(dev, args.seed),
         "cpu_baseline": None,
     }
+    if not args.no_length_sweep:
+        result["length_sweep"] = length_sweep_leg(dev, args.seed, cfg)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(q, k, v, routes, cfg, args)
         result["cpu_baseline"]["config1_full_layer"] = config1_side_by_side(dev, args.seed)

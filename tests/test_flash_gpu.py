@@ -125,12 +125,14 @@ def test_identity_attention_is_exact(dev):
         assert torch.equal(out[head], v[head // 4]), head
 
 
-@pytest.mark.parametrize("n,masked", [(524288, False), (995993, False), (1048576, False), (1048576, True)])
+@pytest.mark.parametrize("n,masked", [(524288, False), (995993, False), (1048576, False), (1048576, True),
+                                      (2097152, False)])
 def test_identity_long_strided(n, masked, dev):
     """modal_rd/check_long_indexing.py:32-56: identity attention (front 0, window 1) on model-strided views
     (q [n, 32, 128], k / v [n, 8, 128] permuted to head-major) past the 2^31-byte mark of a KV head's K rows: every
-    output row must equal its V row exactly. An all-true token mask routes the call to the generic kernel
-    (flash_kernel), so both kernels' 64-bit addressing is exercised at 1048576 tokens."""
+    output row must equal its V row exactly. The pipelined kernel takes up to 2^32 bytes of one head's K rows
+    (2097088 tokens at this stride); an all-true token mask (at 1048576) and the 2097152-token case route the call to
+    the generic kernel (flash_kernel), so both kernels' addressing is exercised past 2^31 bytes."""
     print(f"case identity_long n={n} masked={masked}", flush=True)
     h, hk, d = 32, 8, 128
     q = torch.zeros((n, h, d), device=dev, dtype=torch.bfloat16).permute(1, 0, 2)

@@ -92,8 +92,9 @@ struct TileLoader {
                    int lane) {
     wave = w;
     krow_bytes = (uint32_t)(sk1 * 2);
-    krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kbase), 0, (int)(N * sk1 * 2), 0x00020000);
-    vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vtbase), 0, (int)(PD * np * 2), 0x00020000);
+    // num_records is an unsigned 32-bit byte count (passed through int): sizes up to 4 GiB
+    krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kbase), 0, (int)(uint32_t)(N * sk1 * 2), 0x00020000);
+    vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vtbase), 0, (int)(uint32_t)(PD * np * 2), 0x00020000);
     // K block b = w + 8i: rows 4b + lane/16, 16-byte chunk (lane%16) ^ (row%16); row%16 does not depend on i
     const int krow = 4 * w + lane / 16;
     kvoff = (uint32_t)krow * krow_bytes + 16u * (uint32_t)((lane % 16) ^ (krow & 15));
@@ -622,8 +623,11 @@ __global__ __launch_bounds__(256) void route_tiles_kernel(FlashParams p, uint16_
 }  // namespace
 
 bool flash_pipe_supported(const FlashParams& p, int D) {
-  // buffer offsets are 32-bit: one KV head's K rows and V^T must each span < 2 GiB; split mode needs whole tiles
-  const bool fits = p.N * p.sk1 * 2 < ((int64_t)1 << 31) && (int64_t)PD * p.np * 2 < ((int64_t)1 << 31);
+  // Buffer offsets are unsigned 32-bit: every K offset up to the end of the last tile (row N + 63, which reads as
+  // zero) and every V^T offset of one KV head must stay below 4 GiB, so that no offset wraps back into the
+  // tensor. Split mode needs whole tiles.
+  const int64_t lim = (int64_t)1 << 32;
+  const bool fits = (p.N + kTileKeys) * p.sk1 * 2 < lim && (int64_t)PD * p.np * 2 < lim;
   const bool chunks_ok = p.n_chunks == 1 || (p.key_chunk % kTileKeys == 0 && p.route_k == 0);
   return D == PD && p.G % PHEADS == 0 && p.key_mask == nullptr && fits && chunks_ok;
 }
