@@ -293,6 +293,45 @@ BB_DEV void ping_softmax_open(PingState& st, float c) {
   st.l += sum;
 }
 
+// Work item of a workgroup and the rows of one wave: (KV head, 64-row tile, key chunk), XCD-aware as in flash_kernel.
+struct PipeItem {
+  int bh, kvbh, chunk;
+  int64_t T_eff, r1, qlo, qhi, rw, qw0, qw1, qme;
+  bool wave_live;
+};
+
+BB_DEV PipeItem pipe_item(const FlashParams& p, int bid, int hd, int rbk, int li) {
+  const int lanes_total = p.n_kvbh * p.head_splits;
+  const int per_lane = p.row_tiles * p.n_chunks;  // split mode: (row tile, key chunk) pairs
+  int lane_id, within;
+  if (p.remap) {
+    const int x = bid & 7, sidx = bid >> 3;
+    lane_id = x + 8 * (sidx / per_lane);
+    within = sidx % per_lane;
+  } else {
+    lane_id = bid % lanes_total;
+    within = bid / lanes_total;
+  }
+  PipeItem it;
+  const int rt = p.row_tiles - 1 - within / p.n_chunks;
+  it.chunk = within % p.n_chunks;
+  it.kvbh = lane_id / p.head_splits;
+  const int hsplit = lane_id % p.head_splits;
+  const int batch = it.kvbh / p.Hkv_pb;
+  it.bh = batch * p.H + (it.kvbh % p.Hkv_pb) * p.G + hsplit * PHEADS + hd;
+  it.T_eff = p.row_end < p.T ? p.row_end : p.T;
+  const int64_t r0 = (int64_t)rt * PROWS;
+  it.r1 = (r0 + PROWS < it.T_eff ? r0 + PROWS : it.T_eff) - 1;
+  it.qlo = p.offset + r0 * p.pos_step;
+  it.qhi = p.offset + it.r1 * p.pos_step;
+  it.rw = r0 + 32 * rbk;  // first row of this wave
+  it.wave_live = it.rw <= it.r1;
+  it.qw0 = p.offset + it.rw * p.pos_step;
+  it.qw1 = p.offset + (it.rw + 31 < it.r1 ? it.rw + 31 : it.r1) * p.pos_step;
+  it.qme = it.qw0 + li * p.pos_step;  // this lane's query position
+  return it;
+}
+
 template <bool F16>
 __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) {
   __shared__ __attribute__((aligned(1024))) uint16_t smem[PLDS];
@@ -305,32 +344,11 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
   const int hd = wave & 3, rbk = wave >> 2;  // head slot, row block (= ping-pong group)
 
   // ---- work item: (KV head, 64-row tile), XCD-aware as in flash_kernel ----
-  const int lanes_total = p.n_kvbh * p.head_splits;
-  const int per_lane = p.row_tiles * p.n_chunks;  // split mode: (row tile, key chunk) pairs
-  int lane_id, within;
-  const int bid = blockIdx.x;
-  if (p.remap) {
-    const int x = bid & 7, sidx = bid >> 3;
-    lane_id = x + 8 * (sidx / per_lane);
-    within = sidx % per_lane;
-  } else {
-    lane_id = bid % lanes_total;
-    within = bid / lanes_total;
-  }
-  const int rt = p.row_tiles - 1 - within / p.n_chunks;
-  const int chunk = within % p.n_chunks;
-  const int kvbh = lane_id / p.head_splits, hsplit = lane_id % p.head_splits;
-  const int batch = kvbh / p.Hkv_pb;
-  const int bh = batch * p.H + (kvbh % p.Hkv_pb) * p.G + hsplit * PHEADS + hd;
-
-  const int64_t T_eff = p.row_end < p.T ? p.row_end : p.T;
-  const int64_t r0 = (int64_t)rt * PROWS;
-  const int64_t r1 = (r0 + PROWS < T_eff ? r0 + PROWS : T_eff) - 1;
-  const int64_t qlo = p.offset + r0 * p.pos_step, qhi = p.offset + r1 * p.pos_step;
-  const int64_t rw = r0 + 32 * rbk;            // first row of this wave
-  const bool wave_live = rw <= r1;
-  const int64_t qw0 = p.offset + rw * p.pos_step, qw1 = p.offset + (rw + 31 < r1 ? rw + 31 : r1) * p.pos_step;
-  const int64_t qme = qw0 + li * p.pos_step;   // this lane's query position
+  PipeItem it = pipe_item(p, blockIdx.x, hd, rbk, li);
+  const int bh = it.bh, kvbh = it.kvbh, chunk = it.chunk;
+  const int64_t T_eff = it.T_eff, r1 = it.r1, qlo = it.qlo, qhi = it.qhi, rw = it.rw;
+  const bool wave_live = it.wave_live;
+  const int64_t qw0 = it.qw0, qw1 = it.qw1, qme = it.qme;
 
   PingState st;
   {
@@ -410,14 +428,14 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
     return (int64_t)__builtin_amdgcn_readfirstlane(t + d) * kTileKeys;
   };
   // VALU phase of tile t: the lazy softmax for unmasked tiles, the masked one (front | causal window) otherwise
+  auto softmax_masked = [&](int t) {
+    const int64_t k0 = upos(t), k1 = k0 + kTileKeys - 1;
+    const bool live = wave_live && k0 <= qw1 && !(k0 >= p.front && k1 <= qw0 - p.window);
+    ping_softmax_masked<F16>(st, p.c, qme, PipeWindowMask{k0, p.front, p.window, live}, h);
+  };
   auto softmax = [&](int t) {
-    if (t < nu) {
-      ping_softmax_open<F16>(st, p.c);
-    } else {
-      const int64_t k0 = upos(t), k1 = k0 + kTileKeys - 1;
-      const bool live = wave_live && k0 <= qw1 && !(k0 >= p.front && k1 <= qw0 - p.window);
-      ping_softmax_masked<F16>(st, p.c, qme, PipeWindowMask{k0, p.front, p.window, live}, h);
-    }
+    if (t < nu) ping_softmax_open<F16>(st, p.c);
+    else softmax_masked(t);
   };
 
   uint16_t* ring = smem;
@@ -455,6 +473,7 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
       if (t + 2 < ntot) ld.tile(kst(t + 2), vst(t + 2), upos(t + 2));
       ring_barrier();
     }
+    // every tile of this loop is masked: t >= max(nu, 1) >= nu
 #pragma unroll 1
     for (int t = nu > 1 ? nu : 1; t < ntot; ++t) {
       __builtin_amdgcn_s_setprio(1);
@@ -462,7 +481,7 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
       __builtin_amdgcn_s_setprio(0);
       vm_wait_tile(false);
       ring_barrier();
-      softmax(t);
+      softmax_masked(t);
       if (t + 2 < ntot) ld.tile(kst(t + 2), vst(t + 2), upos(t + 2));
       ring_barrier();
     }
@@ -470,20 +489,28 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
     if (rbk == 0) ring_barrier();  // realign the two groups
   }
 
+  // The work item again, from copies of the block and lane indices that the compiler cannot see through: the values
+  // the routed phase and the epilogue need are recomputed here instead of being held (and spilled) across the loop.
+  {
+    int bid2 = blockIdx.x, li2 = li;
+    asm volatile("" : "+s"(bid2));
+    asm volatile("" : "+v"(li2));
+    it = pipe_item(p, bid2, hd, rbk, li2);
+  }
   // ---- routed keys: per-head tiles pre-gathered by route_tiles_kernel; the two waves of a head share the loads ----
   if (p.route_k > 0) {
     __syncthreads();  // every wave is done with the ring
     uint16_t* kl = smem + hd * 2 * PTE;
     uint16_t* vt = kl + PTE;
-    int64_t g_first = qlo / p.route_chunk, g_last = qhi / p.route_chunk;
+    int64_t g_first = it.qlo / p.route_chunk, g_last = it.qhi / p.route_chunk;
     if (g_last >= p.n_groups) g_last = p.n_groups - 1;
     const uint32_t loff = 16u * (uint32_t)lane;
     for (int64_t g = g_first; g <= g_last; ++g) {
-      const int32_t* irow = p.idx + (int64_t)bh * p.si0 + g * p.si1;
+      const int32_t* irow = p.idx + (int64_t)it.bh * p.si0 + g * p.si1;
       // This head's pre-gathered batches of group g: batch b is a K tile at b * 2 PTE and its V^T tile after it.
       // Each of the head's two waves loads blocks rbk + 2 i (i < 8) of a tile straight into LDS.
       const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<uint16_t*>(p.rtiles + ((int64_t)bh * p.n_groups + g) * p.rt_batches * 2 * PTE), 0,
+          const_cast<uint16_t*>(p.rtiles + ((int64_t)it.bh * p.n_groups + g) * p.rt_batches * 2 * PTE), 0,
           p.rt_batches * 2 * PTE * 2, 0x00020000);
       auto load_tile = [&](int b, uint16_t* dst, int part) {
 #pragma unroll
@@ -496,7 +523,7 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
         }
       };
       // The head's route slots, kRouteCache at a time, go to LDS in one pass (usable keys, -1 elsewhere: a key some
-      // row of the workgroup attends is >= front, < N and <= qhi - window). Batches of 64 slots run up to the last
+      // row of the workgroup attends is >= front, < N and <= it.qhi - window). Batches of 64 slots run up to the last
       // one holding a usable key.
       for (int sb = 0; sb < p.route_k; sb += kRouteCache) {
         const int nslots = p.route_k - sb < kRouteCache ? p.route_k - sb : kRouteCache;
@@ -504,7 +531,7 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
         for (int s0 = 64 * rbk; s0 < kRouteCache; s0 += 128) {
           const int sl = s0 + lane;
           const int64_t key = sl < nslots ? irow[(int64_t)(sb + sl) * p.si2] : -1;
-          const bool ok = key >= p.front && key < p.N && key <= qhi - p.window;
+          const bool ok = key >= p.front && key < p.N && key <= it.qhi - p.window;
           route_keys[hd][sl] = ok ? (int32_t)key : -1;
           if (__builtin_amdgcn_ballot_w64(ok)) nbh = s0 / kTileKeys + 1;
         }
@@ -530,10 +557,10 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
           }
           vm_wait_tile(false);
           __syncthreads();
-          if (work && wave_live) {
+          if (work && it.wave_live) {
             const PipeRoutedMask rm{keys, p.window, p.route_chunk, g};
             ping_qk<F16>(st, kl, li, h);
-            ping_softmax_masked<F16>(st, p.c, qme, rm, h);
+            ping_softmax_masked<F16>(st, p.c, it.qme, rm, h);
             ping_pv<F16>(st, vt, li, h);
           }
           __syncthreads();
@@ -543,12 +570,12 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
   }
 
   // ---- epilogue ----
-  if (!wave_live) return;
-  const int64_t row = rw + li;
+  if (!it.wave_live) return;
+  const int64_t row = it.rw + li;
   const float lt = xhalf_sum(st.l);
-  if (row >= T_eff) return;
+  if (row >= it.T_eff) return;
   if (p.n_chunks > 1) {  // partial (O, m, l) of this key chunk for flash_merge_kernel
-    const int64_t base = ((int64_t)chunk * p.BH + bh) * p.T + row;
+    const int64_t base = ((int64_t)it.chunk * p.BH + it.bh) * p.T + row;
     float* po = p.part_o + base * PD;
 #pragma unroll
     for (int dv = 0; dv < PD / 32; ++dv)
@@ -563,7 +590,7 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
     return;
   }
   const float inv = 1.0f / fmaxf(lt, 1.0e-20f);
-  uint16_t* orow = p.out + (int64_t)bh * p.so0 + row * p.so1;
+  uint16_t* orow = p.out + (int64_t)it.bh * p.so0 + row * p.so1;
 #pragma unroll
   for (int dv = 0; dv < PD / 32; ++dv)
 #pragma unroll
