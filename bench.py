@@ -212,8 +212,7 @@ def decode_leg(dev, seed):
     per-head fp32 scales = absmax/127), 256 steps; each step quantises one new token into the cache and attends to
     all n + 1 rows with a fresh bf16 query. Reported per step with the cache bytes a step must read."""
     import torch
-    from bigger_bird_amd import decode_int8, quantize
-    from bigger_bird_amd.kv_int8 import quantize_pair
+    from bigger_bird_amd import decode_int8_append, quantize
 
     n0, steps, H, Hkv, d = 131072, 256, 32, 8, 128
     g = torch.Generator(device=dev).manual_seed(seed + 5)
@@ -229,9 +228,8 @@ def decode_leg(dev, seed):
     scale = d ** -0.5
 
     def step(i):
-        rows = slice(n0 + i, n0 + i + 1)
-        quantize_pair(k[rows], v[rows], (k8[rows], ks[rows]), (v8[rows], vs[rows]), scale_dtype=torch.float32)
-        return decode_int8(qs[i], k8, ks, v8, vs, n0 + i + 1, scale)
+        # the new token's K / V rows are quantised into row n0 + i by the decode kernel itself (bb_decode_append)
+        return decode_int8_append(qs[i], k8, ks, v8, vs, k[n0 + i], v[n0 + i], n0 + i + 1, scale)
 
     with torch.inference_mode():
         for i in range(8):  # warm-up (rewrites the same rows)
@@ -251,7 +249,7 @@ def decode_leg(dev, seed):
                         "d=128, fp32 per-token per-head scales, 256 steps",
             "us_per_step": round(us, 2), "bytes_per_step": int(bytes_step), "achieved_gbps": round(gbps, 1),
             "peak_gbps": PEAK_HBM_GBPS, "frac": round(gbps / PEAK_HBM_GBPS, 4),
-            "kernels": "quantize (K and V row in one launch) + decode_mfma_kernel + decode_merge_kernel per step"}
+            "kernels": "per step decode_mfma_kernel (new-row quantisation + split-K decode) + decode_merge_kernel"}
 
 
 def sparse_decode_leg(dev, seed):

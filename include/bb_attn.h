@@ -128,6 +128,20 @@ int bb_decode(const void* q, int64_t sq, const int8_t* k8, const void* ks, const
 size_t bb_decode_workspace(int64_t n, int H, int Hkv, int D);
 
 /*
+ * One INT8 decode step: quantises the new token's K and V rows (bf16 [Hkv, D], head strides sknew / svnew) into row
+ * n - 1 of the int8 cache (k8 / v8 with scales ks / vs, as bb_int8_quantize with min_scale), then attends the query
+ * to all n rows, as bb_decode. Replaces the pair Int8KVLayer.update of a one-token step (modal_rd/kv_int8.py:104-112,
+ * the new rows quantised into spare capacity) and RDAttention.exact_attention over the cache
+ * (modal_rd/attention.py:137-141). For D = 128 with 4 query heads per KV head the decode kernel quantises the rows
+ * itself (the workgroup that reads row n - 1 writes it first); other shapes take a quantise launch first. Workspace:
+ * bb_decode_workspace(n, ...).
+ */
+int bb_decode_append(const void* q, int64_t sq, int8_t* k8, void* ks, int8_t* v8, void* vs, int scale_is_f16,
+                     const void* knew, int64_t sknew, const void* vnew, int64_t svnew, float min_scale, int64_t n,
+                     int H, int Hkv, int D, float scale, void* out, int64_t so, void* ws, size_t ws_bytes,
+                     void* stream);
+
+/*
  * bb_decode without a workspace argument and without any allocation: the split partials go to a static device array
  * of bb_decode_noalloc_max_bytes() bytes (4 MiB) inside the library, one per GPU, held until the process ends. No
  * counterpart in the reference: this is for callers that cannot allocate (code under HIP graph capture, serving

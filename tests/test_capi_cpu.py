@@ -118,3 +118,24 @@ def test_argmax_argument_checks():
     assert L.bb_argmax(ctypes.c_void_p(16), 10, 3, out, None) != 0
     assert "dtype must be" in L.bb_last_error().decode()
     assert L.bb_argmax(None, 10, 1, out, None) != 0
+
+
+def test_int8_layer_host_state_without_gpu():
+    """Int8KVLayer's host-side state: construction (HF's DynamicLayer assigns keys / values in its constructor),
+    the empty-cache queries, crop on an empty layer and make_int8_cache's per-layer settings need no GPU."""
+    from bigger_bird_amd.kv_int8 import Int8KVLayer, make_int8_cache
+
+    layer = Int8KVLayer()
+    assert layer._pending is None and layer.keys is None and layer.values is None
+    assert layer.get_seq_length() == 0 and layer.nbytes() == 0
+    layer.crop(-3)
+    assert layer.get_seq_length() == 0
+    with pytest.raises(NotImplementedError):
+        layer.batch_repeat_interleave(2)
+    from transformers import LlamaConfig
+
+    cfg = LlamaConfig(num_hidden_layers=3, hidden_size=64, num_attention_heads=4, num_key_value_heads=2,
+                      intermediate_size=128, vocab_size=32)
+    cache = make_int8_cache(cfg, fused=False, scale_dtype=torch.float32)
+    assert len(cache.layers) == 3
+    assert all(isinstance(x, Int8KVLayer) and not x.fused and x.scale_dtype == torch.float32 for x in cache.layers)

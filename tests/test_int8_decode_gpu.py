@@ -67,6 +67,48 @@ def test_decode_int8_matches_oracle(n, H, Hkv, d, f16, dev):
     _check(out, ref, f"decode_int8 n={n}")
 
 
+@pytest.mark.parametrize("n,H,Hkv,d,f16", [(1, 32, 8, 128, True), (2049, 32, 8, 128, False),
+                                           (131073, 32, 8, 128, True), (5000, 16, 2, 64, False),
+                                           (700, 16, 8, 128, True)])
+def test_decode_int8_append_matches_separate_steps(n, H, Hkv, d, f16, dev):
+    """decode_int8_append (the new token's K / V rows quantised into row n - 1 by the decode kernel at d = 128 with 4
+    query heads per KV head, and the whole cache attended) equals quantize_pair into that row followed by decode_int8: the
+    cache rows and scales bitwise against the oracle's quantisation, the output bitwise against the separate
+    steps and within tolerance of the float64 oracle. The new rows are strided [Hkv, d] views as a model's k_proj
+    output gives them; shapes other than d = 128 / 4 groups take the quantise-then-decode path."""
+    print(f"case decode_append n={n} H={H}/{Hkv} d={d} f16={f16}", flush=True)
+    from bigger_bird_amd import decode_int8_append
+    from bigger_bird_amd.kv_int8 import quantize_pair
+
+    cap = n + 3
+    g = torch.Generator(device=dev).manual_seed(n + 17)
+    k = torch.randn(cap, Hkv, d, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(cap, Hkv, d, device=dev, generator=g).to(torch.bfloat16)
+    q = torch.randn(H, d, device=dev, generator=g).to(torch.bfloat16)
+    new = torch.randn(2, 1, Hkv, 1, 3 * d, device=dev, generator=g).to(torch.bfloat16)
+    knew, vnew = new[0, 0, :, 0, d:2 * d], new[1, 0, :, 0, d:2 * d]  # [Hkv, d], head stride 3 d
+    assert knew.stride() == (3 * d, 1)
+    sd = torch.float16 if f16 else torch.float32
+    k8, ks = quantize(k, scale_dtype=sd)
+    v8, vs = quantize(v, scale_dtype=sd)
+    k8[n - 1:] = 77  # stale bytes where the new row goes and past it
+    a8, as_, b8, bs = k8.clone(), ks.clone(), v8.clone(), vs.clone()
+    out = decode_int8_append(q, k8, ks, v8, vs, knew, vnew, n, d ** -0.5)
+    quantize_pair(knew[None], vnew[None], (a8[n - 1:n], as_[n - 1:n]), (b8[n - 1:n], bs[n - 1:n]), scale_dtype=sd)
+    want = decode_int8(q, a8, as_, b8, bs, n, d ** -0.5)
+    torch.cuda.synchronize()
+    qk, sk16, sk32 = oracle.quantize(knew[None].cpu())
+    qv, sv16, sv32 = oracle.quantize(vnew[None].cpu())
+    assert torch.equal(k8[n - 1:n].cpu(), qk) and torch.equal(v8[n - 1:n].cpu(), qv)
+    sk, sv = (sk16, sv16) if f16 else (sk32, sv32)
+    bits = torch.int16 if f16 else torch.int32
+    assert torch.equal(ks[n - 1:n].cpu().view(bits), sk.view(bits))
+    assert torch.equal(vs[n - 1:n].cpu().view(bits), sv.view(bits))
+    assert torch.equal(k8[:n - 1], a8[:n - 1]) and torch.equal(k8[n:], a8[n:])  # nothing else written
+    assert torch.equal(out, want)
+    _check(out, oracle.decode(q, k8, ks, v8, vs, n, d ** -0.5), f"decode_append n={n}")
+
+
 def test_decode_bf16_matches_sdpa(dev):
     print("case decode_bf16", flush=True)
     n, H, Hkv, d = 5000, 32, 8, 128

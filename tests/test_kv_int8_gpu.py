@@ -154,6 +154,33 @@ def test_appends_across_growth_and_crop(dev):
         layer.crop(3)
 
 
+def test_deferred_row_is_quantised_on_every_path(dev):
+    """A one-token bf16 step handed out as Int8Handle keeps its row unquantised until the handle is attended (the
+    decode kernel quantises it, bb_decode_append). Reading the cache, a further update, crop or nbytes before that
+    quantises it first, so every path sees the same int8 rows as a one-shot quantisation."""
+    print("case int8_layer_deferred_rows", flush=True)
+    g = torch.Generator().manual_seed(8)
+    H, Hkv, d = 32, 8, 128
+    k = torch.randn(1, Hkv, 303, d, generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn(1, Hkv, 303, d, generator=g).to(torch.bfloat16).to(dev)
+    q = torch.randn(1, H, 1, d, generator=g).to(torch.bfloat16).to(dev)
+    want_k, want_v = (dequantize(*quantize(x[0].transpose(0, 1)), torch.bfloat16).transpose(0, 1)[None]
+                      for x in (k, v))
+    layer = Int8KVLayer()
+    layer.update(k[..., :300, :], v[..., :300, :])
+    hk, _ = layer.update(k[..., 300:301, :], v[..., 300:301, :], {"bb_attend": True})
+    assert isinstance(hk, kv_int8.Int8Handle) and layer._pending is not None
+    assert torch.equal(layer.keys, want_k[..., :301, :]) and layer._pending is None  # read -> quantised first
+    layer.update(k[..., 301:302, :], v[..., 301:302, :], {"bb_attend": True})
+    layer.update(k[..., 302:303, :], v[..., 302:303, :], {"bb_attend": True})  # update -> previous row first
+    out = hk.attend(q, d ** -0.5)  # a stale handle attends the whole current cache
+    assert layer._pending is None
+    assert torch.equal(layer.values, want_v) and torch.equal(layer.keys, want_k)
+    st_k, st_v = layer.store_k, layer.store_v
+    ref = oracle.decode(q[0, :, 0], st_k.q, st_k.s, st_v.q, st_v.s, 303, d ** -0.5)
+    assert (out[0, :, 0].double().cpu() - ref).abs().max().item() < 2e-2
+
+
 def test_config5_decode_through_the_layer(dev):
     """131072 cached tokens, 32 q / 8 KV heads, d 128, fp32 per-token scales, 256 decode steps:
     each step's K/V row goes in through Int8KVLayer.update and attention runs through RDAttention.exact_attention ->

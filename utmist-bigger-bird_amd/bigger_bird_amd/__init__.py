@@ -11,9 +11,10 @@ from .attention import RDAttention, install, rope_inplace, routes, vertical_budg
 from .decode import bigger_bird_decode, bigger_bird_route, pooled_probs
 from .flash import bigger_bird_flash, exact_attention, transpose_v
 from .graph_decode import StaticDecoder, graph_generate, graph_prefill
-from .kv_int8 import Int8KVLayer, decode_bf16, decode_int8, dequantize, make_int8_cache, quantize
+from .kv_int8 import (Int8KVLayer, decode_bf16, decode_int8, decode_int8_append, dequantize, make_int8_cache,
+                      quantize)
 
 __all__ = ["RDAttention", "install", "rope_inplace", "routes", "vertical_budget", "bigger_bird_flash", "exact_attention", "transpose_v",
-           "Int8KVLayer", "decode_bf16", "decode_int8", "dequantize", "make_int8_cache", "quantize",
+           "Int8KVLayer", "decode_bf16", "decode_int8", "decode_int8_append", "dequantize", "make_int8_cache", "quantize",
            "bigger_bird_decode", "bigger_bird_route", "pooled_probs", "StaticDecoder", "graph_prefill",
            "graph_generate"]

@@ -35,6 +35,8 @@ SIGNATURES = {
     "bb_decode": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp, _i32, _vp, c_i64p, _vp, c_i64p, _i64, _i32, _i32, _i32, _f32,
                          _vp, _i64, _vp, _sz, _vp]),
     "bb_decode_workspace": (_sz, [_i64, _i32, _i32, _i32]),
+    "bb_decode_append": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp, _i32, _vp, _i64, _vp, _i64, _f32, _i64, _i32, _i32, _i32,
+                                _f32, _vp, _i64, _vp, _sz, _vp]),
     "bb_decode_noalloc": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp, _i32, _vp, c_i64p, _vp, c_i64p, _i64, _i32, _i32, _i32,
                                  _f32, _vp, _i64, _vp]),
     "bb_decode_noalloc_max_bytes": (_sz, []),

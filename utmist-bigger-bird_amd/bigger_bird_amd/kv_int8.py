@@ -132,6 +132,34 @@ def decode_int8(q, k8, ks, v8, vs, n, scale):
     return _decode(q, n, scale, k8=k8, ks=ks, v8=v8, vs=vs)
 
 
+def decode_int8_append(q, k8, ks, v8, vs, knew, vnew, n, scale, min_scale=MIN_SCALE):
+    """One decode step over an int8 cache: the new token's K / V rows knew / vnew (bf16 [Hkv, d], any head stride)
+    are quantised into cache row n - 1 (as quantize_pair would) and q [H, d] attends all n rows (as decode_int8).
+    One kernel at d = 128 with 4 query heads per KV head (bb_decode_append)."""
+    _lib.require_gpu(q, k8, ks, v8, vs, knew, vnew, what="decode_int8_append")
+    if q.dtype != torch.bfloat16 or knew.dtype != torch.bfloat16 or vnew.dtype != torch.bfloat16:
+        raise ValueError("decode_int8_append: bf16 query and new rows")
+    if ks.dtype != vs.dtype or not (k8.is_contiguous() and v8.is_contiguous() and ks.is_contiguous()
+                                    and vs.is_contiguous()):
+        raise ValueError("decode_int8_append: contiguous int8 rows and scales of one dtype")
+    if n > k8.shape[0]:
+        raise ValueError("decode_int8_append: row n - 1 is past the cache capacity")
+    hk, d = k8.shape[1], k8.shape[2]
+    if tuple(knew.shape) != (hk, d) or tuple(vnew.shape) != (hk, d) or knew.stride(-1) != 1 or vnew.stride(-1) != 1:
+        raise ValueError("decode_int8_append: new rows must be [Hkv, d] with a contiguous head_dim")
+    q = q.contiguous()
+    h = q.shape[0]
+    out = torch.empty(h, d, dtype=torch.bfloat16, device=q.device)
+    L = _lib.lib()
+    ws_bytes = L.bb_decode_workspace(n, h, hk, d)
+    ws = _lib.workspace(ws_bytes, q.device)
+    _lib.check(L.bb_decode_append(_lib.ptr(q), q.stride(0), _lib.ptr(k8), _lib.ptr(ks), _lib.ptr(v8), _lib.ptr(vs),
+                                  _scale_flag(ks.dtype), _lib.ptr(knew), knew.stride(0), _lib.ptr(vnew), vnew.stride(0),
+                                  float(min_scale), n, h, hk, d, float(scale), _lib.ptr(out), out.stride(0),
+                                  _lib.ptr(ws), ws_bytes, _lib.stream_of(q)))
+    return out
+
+
 def decode_bf16(q, k, v, scale):
     """q [H, d] bf16 over k/v [Hkv, n, d] (strided views of a bf16 cache)."""
     _lib.require_gpu(k, v, what="decode_bf16")
@@ -151,10 +179,17 @@ class Int8Handle:
         self.turbo, self.shape = layer, shape
 
     def attend(self, q, scale):
-        """q [1, H, 1, d] -> [1, H, 1, d] exact attention over the layer's whole int8 cache."""
+        """q [1, H, 1, d] -> [1, H, 1, d] exact attention over the layer's whole int8 cache. The step's new row, when
+        the layer still holds it unquantised, is quantised by the same kernel (decode_int8_append)."""
         layer = self.turbo
         k, v = layer.store_k, layer.store_v
-        out = decode_int8(q[0, :, 0], k.q, k.s, v.q, v.s, layer.n, scale)
+        pending = layer._pending
+        if pending is not None and pending[2] == layer.n - 1:
+            layer._pending = None
+            out = decode_int8_append(q[0, :, 0], k.q, k.s, v.q, v.s, pending[0], pending[1], layer.n, scale)
+        else:
+            layer._flush()
+            out = decode_int8(q[0, :, 0], k.q, k.s, v.q, v.s, layer.n, scale)
         return out[None, :, None]
 
 
@@ -208,6 +243,8 @@ class Int8KVLayer(DynamicLayer):
     fused = True  # hand handles to consumers that ask for them (cache kwargs {"bb_attend": True})
 
     def __init__(self):
+        self._pending = None  # first: DynamicLayer.__init__ assigns keys / values, whose setters flush
+        self.store_k = self.store_v = None
         super().__init__()
         self.store_k = self.store_v = None
         self.n = 0
@@ -216,7 +253,16 @@ class Int8KVLayer(DynamicLayer):
         self.dtype, self.device = key_states.dtype, key_states.device
         self.store_k = self.store_v = None
         self.n = 0
+        self._pending = None
         self.is_initialized = True
+
+    def _flush(self):
+        """Quantise a one-token step's rows still held for the fused decode (the handle was not attended)."""
+        if self._pending is not None:
+            kr, vr, row = self._pending
+            self._pending = None
+            quantize_pair(kr[None], vr[None], self.store_k.rows(row, row + 1),
+                          self.store_v.rows(row, row + 1), scale_dtype=self.scale_dtype)
 
     @staticmethod
     def _token_major(x):
@@ -236,25 +282,30 @@ class Int8KVLayer(DynamicLayer):
     # keys / values read back dequantised, as the reference's layer exposes them; assignment re-quantises
     @property
     def keys(self):
+        self._flush()
         return None if self.store_k is None else self.store_k.dequantized(self.n, self.dtype)
 
     @keys.setter
     def keys(self, x):
+        self._flush()
         if x is not None and x.numel():
             self.store_k, self.n = self._fill(x), x.shape[-2]
 
     @property
     def values(self):
+        self._flush()
         return None if self.store_v is None else self.store_v.dequantized(self.n, self.dtype)
 
     @values.setter
     def values(self, x):
+        self._flush()
         if x is not None and x.numel():
             self.store_v, self.n = self._fill(x), x.shape[-2]
 
     def update(self, key_states, value_states, cache_kwargs=None, *args, **kwargs):
         if not self.is_initialized:
             self.lazy_initialization(key_states, value_states)
+        self._flush()
         t = key_states.shape[-2]
         if self.store_k is None:
             self.store_k, self.store_v = self._fill(key_states), self._fill(value_states)
@@ -263,19 +314,25 @@ class Int8KVLayer(DynamicLayer):
         start, end = self.n, self.n + t
         self.store_k.ensure(start, end)
         self.store_v.ensure(start, end)
-        quantize_pair(self._token_major(key_states), self._token_major(value_states), self.store_k.rows(start, end),
-                      self.store_v.rows(start, end), scale_dtype=self.scale_dtype)
         self.n = end
         wants_handle = isinstance(cache_kwargs, dict) and cache_kwargs.get("bb_attend", False)
-        if self.fused and wants_handle and t == 1:
+        kr, vr = self._token_major(key_states), self._token_major(value_states)
+        if (self.fused and wants_handle and t == 1 and kr.dtype == torch.bfloat16 and vr.dtype == torch.bfloat16
+                and kr.stride(-1) == 1 and vr.stride(-1) == 1):
+            # the row is quantised by the decode kernel when the handle is attended (or by _flush before any other
+            # use of the cache)
+            self._pending = (kr[0], vr[0], start)
             handle = Int8Handle(self, (1, self.store_k.q.shape[1], end, self.store_k.q.shape[2]))
             return handle, handle
+        quantize_pair(kr, vr, self.store_k.rows(start, end), self.store_v.rows(start, end),
+                      scale_dtype=self.scale_dtype)
         return self.keys, self.values
 
     def get_seq_length(self, *args, **kwargs):
         return self.n if self.is_initialized and self.store_k is not None else 0
 
     def crop(self, tokens_to_remove):
+        self._flush()
         if tokens_to_remove > 0:
             raise NotImplementedError("Int8KVLayer.crop supports negative token counts only")
         if tokens_to_remove < 0 and self.get_seq_length():
@@ -289,6 +346,7 @@ class Int8KVLayer(DynamicLayer):
 
     def nbytes(self):
         """Bytes held by the valid rows of K and V with their scales; spare capacity is not counted."""
+        self._flush()
         if self.store_k is None:
             return 0
         return self.store_k.nbytes(self.n) + self.store_v.nbytes(self.n)

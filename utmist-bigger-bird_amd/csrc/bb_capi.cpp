@@ -445,6 +445,50 @@ int bb_decode(const void* q, int64_t sq, const int8_t* k8, const void* ks, const
   return hip_status(bb::launch_decode(p, static_cast<hipStream_t>(stream)), "bb_decode");
 }
 
+int bb_decode_append(const void* q, int64_t sq, int8_t* k8, void* ks, int8_t* v8, void* vs, int scale_is_f16,
+                     const void* knew, int64_t sknew, const void* vnew, int64_t svnew, float min_scale, int64_t n,
+                     int H, int Hkv, int D, float scale, void* out, int64_t so, void* ws, size_t ws_bytes,
+                     void* stream) {
+  g_err[0] = 0;
+  if (!knew || !vnew || !k8 || !v8 || !ks || !vs) return fail("decode_append: null argument");
+  if (!aligned(knew, 16) || !aligned(vnew, 16) || sknew % 8 || svnew % 8)
+    return fail("decode_append: new rows need a contiguous head_dim and 16-byte aligned heads");
+  if (!(min_scale > 0.0f)) return fail("decode_append: min_scale must be positive");
+  bb::DecodeParams p;
+  const int rc = decode_params(q, sq, k8, ks, v8, vs, scale_is_f16, nullptr, nullptr, nullptr, nullptr, n, H, Hkv, D,
+                               scale, out, so, p);
+  if (rc != BB_OK) return rc;
+  const size_t need = bb::decode_workspace_bytes(H, D, p.n_splits);
+  if (!ws || ws_bytes < need) return fail("workspace of %zu bytes required", need);
+  p.part = static_cast<float*>(ws);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t r0 = (n - 1) * Hkv;  // first (row, head) of the new token
+  const size_t sbytes = scale_is_f16 ? 2 : 4;
+  if (bb::decode_fuses_append(p)) {
+    p.knew = static_cast<const uint16_t*>(knew);
+    p.vnew = static_cast<const uint16_t*>(vnew);
+    p.sknew = sknew; p.svnew = svnew;
+    p.min_scale = min_scale;
+    p.wk8 = k8; p.wv8 = v8; p.wks = ks; p.wvs = vs;
+    return hip_status(bb::launch_decode(p, st), "bb_decode_append");
+  }
+  // other shapes: quantise the two rows in one launch when their strides agree, then decode
+  hipError_t e;
+  if (sknew == svnew)
+    e = bb::launch_int8_quantize(knew, 0, 1, 0, Hkv, sknew, D, min_scale, k8 + r0 * D,
+                                 static_cast<char*>(ks) + r0 * sbytes, scale_is_f16, st, vnew, v8 + r0 * D,
+                                 static_cast<char*>(vs) + r0 * sbytes);
+  else {
+    e = bb::launch_int8_quantize(knew, 0, 1, 0, Hkv, sknew, D, min_scale, k8 + r0 * D,
+                                 static_cast<char*>(ks) + r0 * sbytes, scale_is_f16, st);
+    if (e == hipSuccess)
+      e = bb::launch_int8_quantize(vnew, 0, 1, 0, Hkv, svnew, D, min_scale, v8 + r0 * D,
+                                   static_cast<char*>(vs) + r0 * sbytes, scale_is_f16, st);
+  }
+  if (e != hipSuccess) return hip_status(e, "bb_decode_append quantize");
+  return hip_status(bb::launch_decode(p, st), "bb_decode_append");
+}
+
 size_t bb_decode_noalloc_max_bytes(void) { return kDecodeScratchBytes; }
 
 int bb_decode_noalloc(const void* q, int64_t sq, const int8_t* k8, const void* ks, const int8_t* v8, const void* vs,

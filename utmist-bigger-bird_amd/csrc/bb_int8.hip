@@ -28,6 +28,33 @@ struct QuantSet {
   void* s;
 };
 
+// Quantises the 8 elements v of one row whose LPR lanes form an aligned group of the wave (each holds 8 elements of
+// the row): scale = max(absmax / 127, min_scale), q = rint(x / scale) clamped to [-127, 127], packed little-endian.
+// Every lane of the group must take part (the absmax goes through lane shuffles).
+template <int LPR>
+BB_DEV float quant8(const float (&v)[8], float min_scale, uint32_t (&packed)[2]) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+#pragma unroll
+  for (int off = LPR / 2; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+  float scale = amax / 127.0f;
+  scale = scale < min_scale ? min_scale : scale;
+  packed[0] = packed[1] = 0u;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float qv = rintf(v[i] / scale);
+    qv = fminf(fmaxf(qv, -127.0f), 127.0f);
+    packed[i >> 2] |= ((uint32_t)(uint8_t)(int8_t)qv) << (8 * (i & 3));
+  }
+  return scale;
+}
+
+BB_DEV void store_scale(void* s, int64_t i, float scale, int is_f16) {
+  if (is_f16) reinterpret_cast<__half*>(s)[i] = __float2half_rn(scale);
+  else reinterpret_cast<float*>(s)[i] = scale;
+}
+
 template <int D>
 __global__ __launch_bounds__(256) void quantize_kernel(QuantSet set0, QuantSet set1, int x_is_f32, int64_t rows,
                                                        int64_t row_stride, int inner, int64_t inner_stride,
@@ -63,26 +90,11 @@ __global__ __launch_bounds__(256) void quantize_kernel(QuantSet set0, QuantSet s
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = 0.0f;
   }
-  float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-#pragma unroll
-  for (int off = LPR / 2; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
-  float scale = amax / 127.0f;
-  scale = scale < min_scale ? min_scale : scale;
+  uint32_t packed[2];
+  const float scale = quant8<LPR>(v, min_scale, packed);
   if (!valid) return;
-  uint32_t packed[2] = {0, 0};
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float qv = rintf(v[i] / scale);
-    qv = fminf(fmaxf(qv, -127.0f), 127.0f);
-    packed[i >> 2] |= ((uint32_t)(uint8_t)(int8_t)qv) << (8 * (i & 3));
-  }
   *reinterpret_cast<u32x2_t*>(qo + r * D + 8 * lane_in_row) = u32x2_t{packed[0], packed[1]};
-  if (lane_in_row == 0) {
-    if (scale_is_f16) reinterpret_cast<__half*>(so)[r] = __float2half_rn(scale);
-    else reinterpret_cast<float*>(so)[r] = scale;
-  }
+  if (lane_in_row == 0) store_scale(so, r, scale, scale_is_f16);
 }
 
 template <int D>
@@ -288,6 +300,30 @@ __global__ __launch_bounds__(64 * kMdWaves, 2) void decode_mfma_kernel(DecodePar
   const int li = lane & 31, hh = lane >> 5;
   const int64_t j_begin = (int64_t)split * p.split_len;
   const int64_t j_end = j_begin + p.split_len < p.n ? j_begin + p.split_len : p.n;
+
+  // The step's new token sits in row n - 1, inside the last split: that split's workgroup quantises its KV head's K
+  // and V row into the cache (lanes 0..15 the K row, 16..31 the V row, 8 elements each; quantize_kernel's
+  // arithmetic) before any of its waves reads the rows. The workgroup's waves share one L1, so the barrier makes the
+  // stores visible to their loads.
+  if (p.knew != nullptr && split == p.n_splits - 1) {
+    if (wave == 0 && lane < 32) {
+      const int part = lane >> 4, lr = lane & 15;
+      const uint16_t* src = part ? p.vnew + (int64_t)g * p.svnew : p.knew + (int64_t)g * p.sknew;
+      const u32x4_t a = ld16(src + 8 * lr);
+      float v[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[2 * i] = bf16_to_f32((uint16_t)(a[i] & 0xffffu));
+        v[2 * i + 1] = bf16_to_f32((uint16_t)(a[i] >> 16));
+      }
+      uint32_t packed[2];
+      const float sc = quant8<16>(v, p.min_scale, packed);
+      const int64_t r = (p.n - 1) * p.Hkv + g;
+      *reinterpret_cast<u32x2_t*>((part ? p.wv8 : p.wk8) + r * D + 8 * lr) = u32x2_t{packed[0], packed[1]};
+      if (lr == 0) store_scale(part ? p.wvs : p.wks, r, sc, p.scale_is_f16);
+    }
+    __syncthreads();
+  }
 
   bf16x8_t qa[8];  // Q rows 0..3 = query heads 4g..4g+3; fragment dk holds d = 64 hh + 8 dk + 0..7
 #pragma unroll
@@ -612,8 +648,13 @@ hipError_t launch_int8_dequantize(const int8_t* q, const void* scale, int scale_
 
 size_t decode_workspace_bytes(int H, int D, int n_splits) { return (size_t)H * n_splits * (D + 2) * sizeof(float); }
 
+bool decode_fuses_append(const DecodeParams& p) {
+  return p.D == 128 && p.H == 4 * p.Hkv && p.k8 != nullptr && decode_mfma_fits(p);
+}
+
 hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
   if (p.n <= 0) return hipErrorInvalidValue;
+  if (p.knew != nullptr && !decode_fuses_append(p)) return hipErrorInvalidValue;
   switch (p.D) {
     case 64: return launch_decode_d<64>(p, stream);
     case 128: return launch_decode_d<128>(p, stream);

@@ -85,8 +85,21 @@ struct DecodeParams {
   uint16_t* out;       // [H, D]
   int64_t so;
   float* part;         // [H][n_splits][D + 2]
+  // Optional: the step's new token. Its K and V rows (bf16 [Hkv, D], head strides sknew / svnew) are quantised into
+  // cache row n - 1 (wk8 / wv8 with scales wks / wvs, the same buffers as k8 / v8 / ks / vs) before they are read.
+  const uint16_t* knew;
+  const uint16_t* vnew;
+  int64_t sknew, svnew;
+  float min_scale;
+  int8_t* wk8;
+  int8_t* wv8;
+  void* wks;
+  void* wvs;
 };
 size_t decode_workspace_bytes(int H, int D, int n_splits);
+// Whether launch_decode quantises the new rows (knew / vnew) inside the decode kernel; otherwise the caller quantises
+// them first and passes knew = nullptr.
+bool decode_fuses_append(const DecodeParams& p);
 hipError_t launch_decode(const DecodeParams& p, hipStream_t stream);
 
 // Split-K sparse decode over a bf16 / fp16 KV cache (front | window | routed keys per route row).
