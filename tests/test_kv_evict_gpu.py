@@ -90,10 +90,12 @@ def _topk_ref(vals, budget, front, tail):
     return torch.stack(out).to(torch.int32)
 
 
-@pytest.mark.parametrize("case", ["wide_range", "ties", "above_clamp", "below_clamp", "mixed_signs"])
+@pytest.mark.parametrize("case", ["wide_range", "ties", "above_clamp", "below_clamp", "mixed_signs", "one_bin"])
 def test_topk_columns_float_bins(case, dev):
     """The float-key histogram bins 32 per octave over [2^-40, 2^25) and clamps outside; clamped bins, heavy ties
-    (candidate overflow -> radix select) and non-positive values must still give the exact top-k."""
+    (candidate overflow -> radix select) and non-positive values must still give the exact top-k. `one_bin` puts
+    every key in one bin with distinct values inside sub-bins and exact duplicates (the final kernel's sub-bin
+    refinement and its pairwise ranking of the threshold sub-bin)."""
     print(f"case topk_float_bins {case}", flush=True)
     g = torch.Generator().manual_seed(11)
     rows, n, front, tail, budget = 4, 20000, 5, 300, 700
@@ -105,6 +107,8 @@ def test_topk_columns_float_bins(case, dev):
         vals = 2.0 ** 30 * (1 + torch.rand(rows, n, generator=g))             # one clamped bin, distinct values
     elif case == "below_clamp":
         vals = 2.0 ** -50 * (1 + torch.rand(rows, n, generator=g))
+    elif case == "one_bin":
+        vals = 1.0 + torch.randint(0, 4096, (rows, n), generator=g).float() * 2.0 ** -19
     else:
         vals = torch.randn(rows, n, generator=g)                                # half non-positive
         vals[:, ::7] = float("nan")

@@ -516,11 +516,35 @@ BB_DEV void top_range(const RoutesParams& p, int64_t& lo, int64_t& cnt) {
 // eligible range, then ordered compaction. The general path (any ties, any budget); topk_final_kernel uses it when
 // the candidate set of the fast path overflows.
 constexpr int kTopThreads = 1024;
-__device__ __noinline__ void topk_radix_head(const RoutesParams& p, int head) {
+
+// Inclusive sum over the NT threads of a workgroup in thread order: a shuffle scan per wave, then the wave totals
+// through LDS (ws: NT / 64 words). Every thread must call it; `total` receives the workgroup's sum.
+template <int NT>
+BB_DEV uint32_t block_incl_scan(uint32_t v, uint32_t* ws, uint32_t& total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t t = __shfl_up(v, off);
+    if (lane >= off) v += t;
+  }
+  if (lane == 63) ws[wave] = v;
+  __syncthreads();
+  uint32_t before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < NT / 64; ++w) {
+    const uint32_t x = ws[w];
+    before += w < wave ? x : 0u;
+    all += x;
+  }
+  __syncthreads();  // ws is free again
+  total = all;
+  return v + before;
+}
+
+__device__ __forceinline__ void topk_radix_head(const RoutesParams& p, int head) {
   __shared__ uint32_t hist[256];
   __shared__ uint64_t red[kTopThreads / 64];
-  __shared__ uint32_t scan_sel[kTopThreads];
-  __shared__ uint32_t scan_tie[kTopThreads];
+  __shared__ uint32_t scan_sel[kTopThreads / 64];
   __shared__ uint64_t s_prefix, s_mask;
   __shared__ int64_t s_need;
   __shared__ int s_exact;
@@ -602,20 +626,9 @@ __device__ __noinline__ void topk_radix_head(const RoutesParams& p, int head) {
     if (vm > prefix) ++nsel;
     else if (vm == prefix) ++ntie;
   }
-  scan_sel[tid] = nsel;
-  scan_tie[tid] = ntie;
-  __syncthreads();
-  // exclusive scans (Hillis-Steele in place, 1024 entries)
-  for (int off = 1; off < kTopThreads; off <<= 1) {
-    uint32_t a = tid >= off ? scan_sel[tid - off] : 0u;
-    uint32_t b = tid >= off ? scan_tie[tid - off] : 0u;
-    __syncthreads();
-    scan_sel[tid] += a;
-    scan_tie[tid] += b;
-    __syncthreads();
-  }
-  const int64_t sel_before = (int64_t)scan_sel[tid] - nsel;
-  const int64_t tie_before = (int64_t)scan_tie[tid] - ntie;
+  uint32_t tot;
+  const int64_t sel_before = (int64_t)block_incl_scan<kTopThreads>(nsel, scan_sel, tot) - nsel;
+  const int64_t tie_before = (int64_t)block_incl_scan<kTopThreads>(ntie, scan_sel, tot) - ntie;
   // position of an element = selected-above before it + ties taken before it
   int64_t taken_ties = tie_before < need ? tie_before : need;
   int64_t pos = sel_before + taken_ties;
@@ -643,12 +656,25 @@ __device__ __noinline__ void topk_radix_head(const RoutesParams& p, int head) {
 //                        histogram (workgroup 0 records it), then writes indices of keys above b* to `sel` and
 //                        (key, index) of keys in b* to the candidate list (at most kTopCand kept; the count goes on),
 //                        one atomic per wave and list
-//   topk_final_kernel    per head: the need = budget - above best candidates by (key desc, index asc), then all
-//                        chosen keys through an LDS bitmap of the eligible range, emitted ascending; when the
-//                        candidates overflowed or the range is too long for the bitmap, topk_radix_head instead
+//   topk_final_kernel    per head: the need = budget - above best candidates by (key desc, index asc) -- a
+//                        histogram of the next 10 key bits narrows them to one sub-bin, whose candidates are ranked
+//                        pairwise -- then all chosen keys through an LDS bitmap of the eligible range, emitted
+//                        ascending; when the candidates overflowed or the range is too long for the bitmap,
+//                        topk_radix_head instead
 constexpr int kTopChunk = 4096;       // keys per histogram / compaction workgroup (256 threads x 16)
 constexpr int kTopCand = 2048;        // candidates kept per head
 constexpr int kTopBitmapBits = 262144;
+constexpr int kTopSub = kTopThreads;  // sub-bins of the threshold bin in topk_final_kernel (one per thread)
+static_assert(kTopCand <= 32767, "candidate indices fit int16");
+
+// The 10 key bits below the ones top_bin looks at: monotone within one bin (every bin but the two clamped float bins
+// holds keys that agree on those higher bits).
+BB_DEV int top_sub_key(uint64_t v, bool float_keys) {
+  if (!v) return 0;
+  if (float_keys) return (int)(((uint32_t)v >> 8) & 1023u);
+  const int lz = __clzll((long long)v);
+  return (int)(((v << lz) >> 48) & 1023u);
+}
 
 struct TopWs {
   uint32_t* hist;     // [heads][kTopBins]
@@ -691,17 +717,11 @@ BB_DEV TopPick top_pick(const uint32_t* __restrict__ hist, uint32_t budget, uint
     c[k] = b >= 0 ? hist[b] : 0u;
     sum += c[k];
   }
-  part[tid] = sum;
   if (tid == 0) *s_pick = TopPick{-1, 0, 0};
-  __syncthreads();
-  for (int off = 1; off < 256; off <<= 1) {  // inclusive scan over threads (top bins first)
-    const uint32_t a = tid >= off ? part[tid - off] : 0u;
-    __syncthreads();
-    part[tid] += a;
-    __syncthreads();
-  }
-  const uint32_t before = part[tid] - sum;
-  if (before < budget && part[tid] >= budget) {  // the budget-th largest key lies in this thread's bins
+  uint32_t total;
+  const uint32_t incl = block_incl_scan<256>(sum, part, total);  // over threads, top bins first
+  const uint32_t before = incl - sum;
+  if (before < budget && incl >= budget) {  // the budget-th largest key lies in this thread's bins
     uint32_t cum = before;
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
@@ -715,7 +735,7 @@ BB_DEV TopPick top_pick(const uint32_t* __restrict__ hist, uint32_t budget, uint
   __syncthreads();
   TopPick r = *s_pick;
   if (r.bstar < 0) {  // fewer keys than the budget: all of them
-    const uint32_t total = part[255], zeros = hist[0];
+    const uint32_t zeros = hist[0];
     r = TopPick{0, (int)(total - zeros), (int)zeros};
   }
   return r;
@@ -724,12 +744,22 @@ BB_DEV TopPick top_pick(const uint32_t* __restrict__ hist, uint32_t budget, uint
 __global__ __launch_bounds__(256) void topk_compact_kernel(RoutesParams p, TopWs w) {
   constexpr int PER = kTopChunk / 256;
   __shared__ uint32_t part[256];
+  __shared__ uint32_t wcnt[2][4], wbase[2];
   __shared__ TopPick s_pick;
   const int head = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
   int64_t lo, cnt;
   top_range(p, lo, cnt);
   const int64_t t0 = (int64_t)blockIdx.x * kTopChunk;
   if (t0 >= cnt) return;  // uniform per workgroup; workgroup 0 always stays when there is any key
+  // the chunk's keys are loaded first, so that their latency overlaps the threshold search over the histogram
+  const bool fk = p.float_keys != 0;
+  const uint64_t* P = p.pooled + (int64_t)head * p.pstride + lo;
+  uint64_t v[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int64_t t = t0 + 256 * k + tid;
+    v[k] = t < cnt ? P[t] : 0;
+  }
   const TopPick pk = top_pick(w.hist + (int64_t)head * kTopBins, (uint32_t)p.budget, part, &s_pick);
   TopMeta* m = w.meta + head;
   if (blockIdx.x == 0 && tid == 0) {
@@ -737,15 +767,11 @@ __global__ __launch_bounds__(256) void topk_compact_kernel(RoutesParams p, TopWs
     m->above = pk.above;
     m->need = pk.need;
   }
-  const bool fk = p.float_keys != 0;
-  const uint64_t* P = p.pooled + (int64_t)head * p.pstride + lo;
-  uint64_t v[PER];
   int bin[PER];
   uint32_t ns = 0, nc = 0;
 #pragma unroll
   for (int k = 0; k < PER; ++k) {
     const int64_t t = t0 + 256 * k + tid;
-    v[k] = t < cnt ? P[t] : 0;
     bin[k] = t < cnt ? top_bin(v[k], fk) : -1;
   }
 #pragma unroll
@@ -753,14 +779,25 @@ __global__ __launch_bounds__(256) void topk_compact_kernel(RoutesParams p, TopWs
     ns += (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(bin[k] > pk.bstar));
     nc += (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(bin[k] == pk.bstar));
   }
-  // one atomic per wave and list for the whole chunk
-  uint32_t base_s = 0, base_c = 0;
+  // one atomic per workgroup and list for the whole chunk (the per-head counters are shared by every chunk)
+  const int wave = tid >> 6;
   if (lane == 0) {
-    if (ns) base_s = atomicAdd(&m->nsel, ns);
-    if (nc) base_c = atomicAdd(&m->ncand, nc);
+    wcnt[0][wave] = ns;
+    wcnt[1][wave] = nc;
   }
-  base_s = __shfl(base_s, 0);
-  base_c = __shfl(base_c, 0);
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t ts = wcnt[0][0] + wcnt[0][1] + wcnt[0][2] + wcnt[0][3];
+    const uint32_t tc = wcnt[1][0] + wcnt[1][1] + wcnt[1][2] + wcnt[1][3];
+    wbase[0] = ts ? atomicAdd(&m->nsel, ts) : 0u;
+    wbase[1] = tc ? atomicAdd(&m->ncand, tc) : 0u;
+  }
+  __syncthreads();
+  uint32_t base_s = wbase[0], base_c = wbase[1];
+  for (int w = 0; w < wave; ++w) {
+    base_s += wcnt[0][w];
+    base_c += wcnt[1][w];
+  }
   int32_t* sel = w.sel + (int64_t)head * p.pstride;
   uint64_t* candv = w.candv + (int64_t)head * kTopCand;
   int32_t* candi = w.candi + (int64_t)head * kTopCand;
@@ -784,7 +821,10 @@ __global__ __launch_bounds__(kTopThreads) void topk_final_kernel(RoutesParams p,
   __shared__ uint64_t cv[kTopCand];
   __shared__ int32_t ci[kTopCand];
   __shared__ uint32_t bits[kTopBitmapBits / 32];
-  __shared__ uint32_t scan[kTopThreads];
+  __shared__ uint32_t scan[kTopThreads / 64];
+  __shared__ uint32_t sub[kTopSub];
+  __shared__ int16_t tie_list[kTopCand];
+  __shared__ int s_sub[3];  // s*, candidates still needed from s*, length of the s* list
   const int head = blockIdx.x, tid = threadIdx.x;
   int64_t lo, cnt;
   top_range(p, lo, cnt);
@@ -801,13 +841,53 @@ __global__ __launch_bounds__(kTopThreads) void topk_final_kernel(RoutesParams p,
   }
   for (int i = tid; i < words; i += kTopThreads) bits[i] = 0u;
   __syncthreads();
-  // chosen candidates: fewer than `need` others beat them (larger value, or equal value and lower index)
-  for (int i = tid; i < nc; i += kTopThreads) {
+  // Chosen candidates: fewer than `need` others beat them (larger value, or equal value and lower index). Inside
+  // bin b* the next 10 bits of the key order the candidates further (top_sub_key): a histogram of those finds the
+  // sub-bin s* of the need-th largest candidate; candidates above s* are chosen, and only the ones in s* are ranked
+  // against each other. The clamped float bins (their keys span several octaves) rank every candidate instead.
+  const bool fk = p.float_keys != 0;
+  const bool refine = !(fk && (m.bstar == 1 || m.bstar == kTopBins - 1));
+  int need2 = m.need, sstar = -1;
+  if (refine) {
+    for (int i = tid; i < kTopSub; i += kTopThreads) sub[i] = 0u;
+    if (tid == 0) {  // need = 0 (every key above b*): no sub-bin, nothing more to choose
+      s_sub[0] = kTopSub;
+      s_sub[1] = 0;
+      s_sub[2] = 0;
+    }
+    __syncthreads();
+    for (int i = tid; i < nc; i += kTopThreads) atomicAdd(&sub[top_sub_key(cv[i], fk)], 1u);
+    __syncthreads();
+    // thread t owns sub-bin kTopSub - 1 - t (top first): inclusive scan of the counts
+    const uint32_t c = sub[kTopSub - 1 - tid];
+    uint32_t tot;
+    const uint32_t incl = block_incl_scan<kTopThreads>(c, scan, tot);
+    if (incl - c < (uint32_t)m.need && incl >= (uint32_t)m.need) {
+      s_sub[0] = kTopSub - 1 - tid;
+      s_sub[1] = m.need - (int)(incl - c);
+    }
+    __syncthreads();
+    sstar = s_sub[0];
+    need2 = s_sub[1];
+    // candidates above s* are chosen; the ones in s* go to a short list
+    for (int i = tid; i < nc; i += kTopThreads) {
+      const int sk = top_sub_key(cv[i], fk);
+      if (sk > sstar) atomicOr(&bits[(ci[i] - lo) >> 5], 1u << ((ci[i] - lo) & 31));
+      else if (sk == sstar) tie_list[atomicAdd(&s_sub[2], 1)] = i;
+    }
+    __syncthreads();
+  }
+  const int nr = refine ? s_sub[2] : nc;
+  for (int r = tid; r < nr; r += kTopThreads) {
+    const int i = refine ? tie_list[r] : r;
     const uint64_t v = cv[i];
     const int32_t ix = ci[i];
     int rank = 0;
-    for (int j = 0; j < nc; ++j) rank += (cv[j] > v) || (cv[j] == v && ci[j] < ix);
-    if (rank < m.need) atomicOr(&bits[(ix - lo) >> 5], 1u << ((ix - lo) & 31));
+    for (int q = 0; q < nr; ++q) {
+      const int j = refine ? tie_list[q] : q;
+      rank += (cv[j] > v) || (cv[j] == v && ci[j] < ix);
+    }
+    if (rank < need2) atomicOr(&bits[(ix - lo) >> 5], 1u << ((ix - lo) & 31));
   }
   for (uint32_t i = tid; i < m.nsel; i += kTopThreads) {
     const int32_t ix = w.sel[(int64_t)head * p.pstride + i];
@@ -819,15 +899,8 @@ __global__ __launch_bounds__(kTopThreads) void topk_final_kernel(RoutesParams p,
   const int w0 = tid * per, w1 = w0 + per < words ? w0 + per : words;
   uint32_t mine = 0;
   for (int x = w0; x < w1; ++x) mine += __builtin_popcount(bits[x]);
-  scan[tid] = mine;
-  __syncthreads();
-  for (int off = 1; off < kTopThreads; off <<= 1) {
-    const uint32_t a = tid >= off ? scan[tid - off] : 0u;
-    __syncthreads();
-    scan[tid] += a;
-    __syncthreads();
-  }
-  uint32_t pos = scan[tid] - mine;
+  uint32_t chosen;
+  uint32_t pos = block_incl_scan<kTopThreads>(mine, scan, chosen) - mine;
   int32_t* out = p.out_idx + (int64_t)head * p.budget;
   for (int x = w0; x < w1; ++x) {
     uint32_t b = bits[x];
@@ -839,7 +912,7 @@ __global__ __launch_bounds__(kTopThreads) void topk_final_kernel(RoutesParams p,
     }
   }
   // fewer chosen keys than the budget (a short eligible range): the remaining slots read -1
-  for (uint32_t i = scan[kTopThreads - 1] + tid; i < (uint32_t)p.budget; i += kTopThreads) out[i] = -1;
+  for (uint32_t i = chosen + tid; i < (uint32_t)p.budget; i += kTopThreads) out[i] = -1;
 }
 
 template <int D>
