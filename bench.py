@@ -54,7 +54,8 @@ def parse_args():
     ap.add_argument("--no-short-arm", action="store_true",
                     help="skip the B=4, T=32768 sparse-vs-dense leg (BASELINE configs[3])")
     ap.add_argument("--copy-probe", action="store_true",
-                    help="only run a plain 1 GiB device copy 5 times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+                    help="only run kernels of known traffic, 5 launches each: a 1 GiB device copy, a 1 GiB read "
+                         "(sum) and a 1 GiB write (fill); calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--cpu-sample-blocks", type=int, default=96,
                     help="64-row blocks (of 4 heads each) timed for the CPU baseline")
     return ap.parse_args()
@@ -553,12 +554,17 @@ def main():
         print(json.dumps({"full_model": full_model_leg(torch.device("cuda:0"), args.seed, args.T)}), flush=True)
         return
     if args.copy_probe:
-        src = torch.ones(1 << 29, dtype=torch.int16, device="cuda")  # 1 GiB
+        src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")  # 1 GiB
         dst = torch.empty_like(src)
         for _ in range(5):
-            dst.copy_(src)
+            dst.copy_(src)  # reads and writes 1 GiB
+        for _ in range(5):
+            src.sum()  # reads 1 GiB
+        for _ in range(5):
+            dst.fill_(2.0)  # writes 1 GiB
         torch.cuda.synchronize()
-        print(json.dumps({"copy_probe_bytes": src.numel() * 2, "launches": 5}), flush=True)
+        print(json.dumps({"probe_bytes": src.numel() * 4, "launches_each": 5, "kernels": ["copy", "sum", "fill"]}),
+              flush=True)
         return
     from bigger_bird_amd import RDAttention, _lib
     from bigger_bird_amd.synth import attended_pairs, make_inputs

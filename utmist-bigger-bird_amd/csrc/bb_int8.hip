@@ -574,11 +574,13 @@ __global__ __launch_bounds__(256) void rope_kernel(uint16_t* __restrict__ x, int
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t total = (int64_t)B * Hh * T * cpr;
   if (t >= total) return;
+  // head fastest: the Hh rows of one position share their cos / sin row, which then stays in cache (with the
+  // position fastest every head would stream the whole cos / sin table again)
   const int c = (int)(t % cpr);
   const int64_t row = t / cpr;
-  const int64_t pos = row % T;
-  const int64_t bh = row / T;
-  const int64_t b = bh / Hh, hh = bh % Hh;
+  const int64_t hh = row % Hh;
+  const int64_t bp = row / Hh;
+  const int64_t pos = bp % T, b = bp / T;
   uint16_t* xr = x + b * sx0 + hh * sx1 + pos * sx2;
   const uint16_t* cr = cs + b * sc0 + pos * sc1;
   const uint16_t* sr = sn + b * sc0 + pos * sc1;
