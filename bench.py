@@ -263,6 +263,7 @@ def sparse_decode_leg(dev, seed):
     sparse decode reads."""
     import torch
     from bigger_bird_amd import bigger_bird_decode, bigger_bird_route
+    from bigger_bird_amd.decode import kv_append
 
     n0, steps, H, Hkv, d = 131072, 64, 32, 8, 128
     front, window, routed = 64, 16384, 512
@@ -276,9 +277,7 @@ def sparse_decode_leg(dev, seed):
     scale = d ** -0.5
 
     def step(length):
-        k.index_copy_(1, length, kb[:, None])
-        v.index_copy_(1, length, vb[:, None])
-        length.add_(1)
+        kv_append(k, v, kb, vb, length)  # the new row at the device-side length, then length += 1, one launch
         idx = bigger_bird_route(qb, k, routed, front=front, window=window, scale=scale, n=length)
         return bigger_bird_decode(qb, k, v, idx, front=front, window=window, scale=scale, n=length)
 

@@ -187,6 +187,17 @@ int bb_decode_route(const void* q, int64_t sq, const void* k, const int64_t* sk,
 size_t bb_decode_route_workspace(int64_t cap, int H, int Hkv, int splits, int k_route);
 
 /*
+ * One decode step's cache append at a length held in device memory (so a captured graph stays valid as the cache
+ * grows): with n = *n_dev, k[h, n, :] = knew[h, :] and v[h, n, :] = vnew[h, :] for the Hkv heads (16-bit elements,
+ * D % 8 == 0; k / v strides sk[2] / sv[2]: head, token; knew / vnew head strides), then *n_dev += n_inc. A length
+ * outside [0, cap) writes nothing and leaves *n_dev unchanged. One launch in place of the two index_copy_ calls and
+ * the length add of a decode step (modal_rd/graph_decode.py's cache append, kernels/bigger_bird_decode.py's callers).
+ */
+int bb_kv_append(void* k, const int64_t* sk, void* v, const int64_t* sv, const void* knew, int64_t sknew,
+                 const void* vnew, int64_t svnew, int Hkv, int D, int64_t cap, int64_t* n_dev, int64_t n_inc,
+                 void* stream);
+
+/*
  * Cache compaction for kv_evict: dst[h, i, :] = src[h, idx[h, i], :] for heads x m rows of D 16-bit elements
  * (D % 8 == 0); src [heads, n_src, D] strides ss[2], dst strides sd[2] (head, row), idx int64 [heads, m] with row
  * stride si0; an index outside [0, n_src) gives a zero row. Replaces the K/V gather of RDAttention.evict

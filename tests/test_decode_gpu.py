@@ -13,6 +13,7 @@ import torch
 
 import oracle
 from bigger_bird_amd import bigger_bird_decode, bigger_bird_route, pooled_probs
+from bigger_bird_amd.decode import kv_append
 
 pytestmark = pytest.mark.gpu
 
@@ -159,9 +160,7 @@ def test_graph_captured_decode_step(dev):
     scale = d ** -0.5
 
     def step(k, v, length, q, kn, vn):
-        k.index_copy_(1, length, kn[:, None])
-        v.index_copy_(1, length, vn[:, None])
-        length.add_(1)
+        kv_append(k, v, kn, vn, length)
         idx = bigger_bird_route(q, k, routed, front=front, window=window, scale=scale, n=length)
         return bigger_bird_decode(q, k, v, idx, front=front, window=window, scale=scale, n=length), idx
 
@@ -190,3 +189,31 @@ def test_graph_captured_decode_step(dev):
         assert torch.equal(idx_g, eager[i][1]), i
         assert torch.equal(out_g, eager[i][0]), i
         _ = torch.zeros(1, device=dev).sum().item()  # unrelated eager work between replays
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_kv_append_matches_index_copy(dtype, dev):
+    """bb_kv_append writes the new rows at the device-side length and advances it: bitwise what two index_copy_ calls
+    and the add do, on strided cache views and strided new rows; a length at the capacity writes nothing."""
+    print(f"case kv_append {dtype}", flush=True)
+    hk, cap, d = 8, 300, 128
+    g = torch.Generator().manual_seed(3)
+    arena = torch.randn(2, hk, cap, 2 * d, generator=g).to(dtype).to(dev)
+    k, v = arena[0, :, :, :d], arena[1, :, :, d:]  # [hk, cap, d] views with row stride 2 d
+    ref = arena.clone()
+    kr, vr = ref[0, :, :, :d], ref[1, :, :, d:]
+    length, lref = torch.tensor([123], device=dev), torch.tensor([123], device=dev)
+    for step in range(3):
+        rows = torch.randn(hk, 3 * d, generator=g).to(dtype).to(dev)
+        kn, vn = rows[:, :d], rows[:, 2 * d:]
+        kv_append(k, v, kn, vn, length)
+        kr.index_copy_(1, lref, kn[:, None])
+        vr.index_copy_(1, lref, vn[:, None])
+        lref.add_(1)
+        torch.cuda.synchronize()
+        assert torch.equal(arena, ref) and int(length.item()) == 124 + step
+    full = torch.tensor([cap], device=dev)
+    before = arena.clone()
+    kv_append(k, v, kn, vn, full)
+    torch.cuda.synchronize()
+    assert torch.equal(arena, before) and int(full.item()) == cap

@@ -128,6 +128,27 @@ def gather_rows(x, idx):
     return out
 
 
+def kv_append(k, v, knew, vnew, length, advance=1):
+    """One decode step's append: k[:, n] = knew and v[:, n] = vnew at n = length (an int64 GPU tensor of one element),
+    then length += advance, in one launch (the two index_copy_ calls and the add of a decode step). k / v [Hkv, cap, D]
+    (any cache view with 16-byte aligned rows), knew / vnew [Hkv, D]. A length outside [0, cap) writes nothing."""
+    if not (k.is_cuda and v.is_cuda and knew.is_cuda and vnew.is_cuda and length.is_cuda):
+        raise ValueError("kv_append needs GPU tensors")
+    if k.element_size() != 2 or v.dtype != k.dtype or knew.dtype != k.dtype or vnew.dtype != k.dtype:
+        raise ValueError("kv_append: one 16-bit dtype")
+    hk, cap, d = k.shape
+    if v.shape != k.shape or tuple(knew.shape) != (hk, d) or tuple(vnew.shape) != (hk, d):
+        raise ValueError("kv_append: k / v [Hkv, cap, D] and new rows [Hkv, D]")
+    if length.dtype != torch.int64 or length.numel() != 1:
+        raise ValueError("kv_append: length must be one int64")
+    if knew.stride(-1) != 1 or vnew.stride(-1) != 1 or k.stride(-1) != 1 or v.stride(-1) != 1:
+        raise ValueError("kv_append: rows need a contiguous head_dim")
+    _lib.check(_lib.lib().bb_kv_append(_lib.ptr(k), _lib.i64s(k.stride(0), k.stride(1)), _lib.ptr(v),
+                                       _lib.i64s(v.stride(0), v.stride(1)), _lib.ptr(knew), knew.stride(0),
+                                       _lib.ptr(vnew), vnew.stride(0), hk, d, cap, _lib.ptr(length), int(advance),
+                                       _lib.stream_of(k)))
+
+
 def topk_columns(vals, budget, *, front=0, tail=0):
     """Per row of vals [rows, n] (fp32): the `budget` columns of [front, n - tail) with the largest values (values
     <= 0 and NaN last, ties to the lower index), ascending int32 [rows, budget], -1 past the eligible count: the

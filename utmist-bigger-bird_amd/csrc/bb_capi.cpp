@@ -628,6 +628,23 @@ int bb_decode_route(const void* q, int64_t sq, const void* k, const int64_t* sk,
                     "bb_decode_route top-k");
 }
 
+int bb_kv_append(void* k, const int64_t* sk, void* v, const int64_t* sv, const void* knew, int64_t sknew,
+                 const void* vnew, int64_t svnew, int Hkv, int D, int64_t cap, int64_t* n_dev, int64_t n_inc,
+                 void* stream) {
+  g_err[0] = 0;
+  if (!k || !v || !sk || !sv || !knew || !vnew || !n_dev) return fail("kv_append: null argument");
+  if (Hkv <= 0 || D <= 0 || D % 8 || cap <= 0) return fail("kv_append: rows must be whole 16-byte units");
+  if (!aligned(k, 16) || !aligned(v, 16) || !aligned(knew, 16) || !aligned(vnew, 16) || sk[0] % 8 || sk[1] % 8 ||
+      sv[0] % 8 || sv[1] % 8 || sknew % 8 || svnew % 8)
+    return fail("kv_append: rows must be 16-byte aligned");
+  if (!aligned(n_dev, 8)) return fail("kv_append: misaligned length");
+  return hip_status(bb::launch_kv_append(static_cast<uint16_t*>(k), sk[0], sk[1], static_cast<uint16_t*>(v), sv[0],
+                                         sv[1], static_cast<const uint16_t*>(knew), sknew,
+                                         static_cast<const uint16_t*>(vnew), svnew, Hkv, D, cap, n_dev, n_inc,
+                                         static_cast<hipStream_t>(stream)),
+                    "bb_kv_append");
+}
+
 int bb_gather_rows(const void* src, const int64_t* ss, int64_t n_src, int heads, const int64_t* idx, int64_t si0, int m,
                    int D, void* dst, const int64_t* sd, void* stream) {
   g_err[0] = 0;

@@ -417,6 +417,28 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const uint16_t* __rest
        ok ? ld16(src + (int64_t)h * ss0 + row * ss1 + 8 * c) : u32x4_t{0, 0, 0, 0});
 }
 
+// One decode step's cache append: row n = *n_dev of every KV head of k and of v (strides head, token) takes the new
+// rows knew / vnew [heads, D] (head strides), then *n_dev advances by n_inc. One workgroup, so every thread reads the
+// length before thread 0 moves it. A length at or past the capacity writes nothing and leaves the length as it is.
+__global__ __launch_bounds__(256) void kv_append_kernel(uint16_t* __restrict__ k, int64_t sk0, int64_t sk1,
+                                                        uint16_t* __restrict__ v, int64_t sv0, int64_t sv1,
+                                                        const uint16_t* __restrict__ knew, int64_t skn,
+                                                        const uint16_t* __restrict__ vnew, int64_t svn, int heads, int D,
+                                                        int64_t cap, int64_t* __restrict__ n_dev, int64_t n_inc) {
+  const int64_t n = *n_dev;
+  const int cpr = D / 8;
+  if (n >= 0 && n < cap) {
+    for (int e = threadIdx.x; e < 2 * heads * cpr; e += 256) {
+      const int which = e / (heads * cpr), r = e % (heads * cpr), h = r / cpr, c = r % cpr;
+      const uint16_t* src = which ? vnew + (int64_t)h * svn : knew + (int64_t)h * skn;
+      uint16_t* dst = which ? v + (int64_t)h * sv0 + n * sv1 : k + (int64_t)h * sk0 + n * sk1;
+      st16(dst + 8 * c, ld16(src + 8 * c));
+    }
+  }
+  __syncthreads();  // every thread has read n
+  if (threadIdx.x == 0 && n >= 0 && n < cap) *n_dev = n + n_inc;
+}
+
 __global__ __launch_bounds__(256) void f32_keys_kernel(const float* __restrict__ vals, int64_t sv0, int64_t n,
                                                        uint64_t* __restrict__ keys) {
   const int r = blockIdx.y;
@@ -608,6 +630,14 @@ hipError_t launch_gather_rows(const uint16_t* src, int64_t ss0, int64_t ss1, int
   if (work <= 0 || heads <= 0) return hipSuccess;
   hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)((work + 255) / 256), heads), dim3(256), 0, stream, src, ss0,
                      ss1, n_src, idx, si0, m, D, dst, sd0, sd1);
+  return hipGetLastError();
+}
+
+hipError_t launch_kv_append(uint16_t* k, int64_t sk0, int64_t sk1, uint16_t* v, int64_t sv0, int64_t sv1,
+                            const uint16_t* knew, int64_t skn, const uint16_t* vnew, int64_t svn, int heads, int D,
+                            int64_t cap, int64_t* n_dev, int64_t n_inc, hipStream_t stream) {
+  hipLaunchKernelGGL(kv_append_kernel, dim3(1), dim3(256), 0, stream, k, sk0, sk1, v, sv0, sv1, knew, skn, vnew, svn,
+                     heads, D, cap, n_dev, n_inc);
   return hipGetLastError();
 }
 

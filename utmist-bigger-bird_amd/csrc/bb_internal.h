@@ -155,6 +155,10 @@ hipError_t launch_gather_rows(const uint16_t* src, int64_t ss0, int64_t ss1, int
 hipError_t launch_rms_norm(const uint16_t* x, int64_t sx, int rows, int D, const uint16_t* w, float eps, int f16,
                            uint16_t* out, int64_t so, hipStream_t stream);
 // Index of the largest element of x [n] (kind 0 fp32, 1 bf16, 2 fp16; vec16: 16-byte aligned), to out[0].
+// Decode-step cache append at a device-side length (advanced by n_inc afterwards).
+hipError_t launch_kv_append(uint16_t* k, int64_t sk0, int64_t sk1, uint16_t* v, int64_t sv0, int64_t sv1,
+                            const uint16_t* knew, int64_t skn, const uint16_t* vnew, int64_t svn, int heads, int D,
+                            int64_t cap, int64_t* n_dev, int64_t n_inc, hipStream_t stream);
 hipError_t launch_argmax(const void* x, int64_t n, int kind, bool vec16, int64_t* out, hipStream_t stream);
 hipError_t launch_f32_keys(const float* vals, int64_t sv0, int rows, int64_t n, uint64_t* keys, hipStream_t stream);
 
