@@ -14,7 +14,7 @@ generate / EOS / rewind / feed protocol. The design is this package's own:
   shape and reads its varying values from device memory: the step is captured once and replayed per token.
 * Step (one token through the model): embedding; per layer RMSNorm -> one fused QKV projection (the q, k and v
   weights concatenated once at construction when they are plain bias-free Linear layers of one dtype) -> RoPE on q and
-  k in place -> the new K and V row into the arena at `slot` (one index_copy_) -> attention -> o_proj, residual ->
+  k in place -> the new K and V row into the arena at `slot` (one bb_kv_append) -> attention -> o_proj, residual ->
   RMSNorm -> MLP, residual; final norm, lm_head, greedy token by a one-workgroup HIP argmax written straight into
   the control block.
 * Attention per layer: split-K flash decoding over the filled rows (bigger_bird_decode with front 0, window =
@@ -34,7 +34,7 @@ from transformers.cache_utils import DynamicLayer
 from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
 
 from .attention import rope_inplace
-from .decode import argmax_index, bigger_bird_decode, bigger_bird_route, rms_norm
+from .decode import argmax_index, bigger_bird_decode, bigger_bird_route, kv_append, rms_norm
 
 # Control block: slot indices and the per-step / per-token increments.
 N, POS, TOK, MADE, SLOT = range(5)
@@ -216,7 +216,7 @@ class StaticDecoder:
                 kv = None
             if kv is None:
                 kv = torch.stack((k[0], v[0]))
-            self.arena[i].index_copy_(2, self._slot, kv)
+            kv_append(self.arena[i][0], self.arena[i][1], kv[0, :, 0], kv[1, :, 0], self._slot, advance=0)
             o = self._attend(i, plan, q[0, :, 0])
             hid = hid + plan.base.o_proj(o.reshape(1, 1, -1))
             hid = hid + layer.mlp(self._norm(layer.post_attention_layernorm, hid))
