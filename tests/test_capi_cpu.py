@@ -139,3 +139,28 @@ def test_int8_layer_host_state_without_gpu():
     cache = make_int8_cache(cfg, fused=False, scale_dtype=torch.float32)
     assert len(cache.layers) == 3
     assert all(isinstance(x, Int8KVLayer) and not x.fused and x.scale_dtype == torch.float32 for x in cache.layers)
+
+
+def test_decode_append_and_kv_append_argument_errors():
+    """Argument checks of the decode-step entry points run before any launch (no GPU needed)."""
+    L = _lib.lib()
+    p = ctypes.c_void_p(256)
+    # bb_decode_append: a missing new row, then a misaligned one, then a non-positive min_scale
+    rc = L.bb_decode_append(p, 128, p, p, p, p, 0, None, 128, p, 128, 1e-4, 100, 32, 8, 128, 0.1, p, 128, p, 1 << 30,
+                            None)
+    assert rc == -1 and "null argument" in L.bb_last_error().decode()
+    rc = L.bb_decode_append(p, 128, p, p, p, p, 0, ctypes.c_void_p(258), 128, p, 128, 1e-4, 100, 32, 8, 128, 0.1, p,
+                            128, p, 1 << 30, None)
+    assert rc == -1 and "16-byte aligned" in L.bb_last_error().decode()
+    rc = L.bb_decode_append(p, 128, p, p, p, p, 0, p, 128, p, 128, 0.0, 100, 32, 8, 128, 0.1, p, 128, p, 1 << 30, None)
+    assert rc == -1 and "min_scale" in L.bb_last_error().decode()
+    rc = L.bb_decode_append(p, 128, p, p, p, p, 0, p, 128, p, 128, 1e-4, 100, 32, 8, 128, 0.1, p, 128, p, 16, None)
+    assert rc == -1 and "workspace" in L.bb_last_error().decode()
+    # bb_kv_append
+    s2 = _lib.i64s(128 * 64, 128)
+    rc = L.bb_kv_append(p, s2, p, s2, p, 128, p, 128, 8, 128, 64, None, 1, None)
+    assert rc == -1 and "null argument" in L.bb_last_error().decode()
+    rc = L.bb_kv_append(p, s2, p, s2, p, 128, p, 128, 8, 100, 64, p, 1, None)
+    assert rc == -1 and "16-byte units" in L.bb_last_error().decode()
+    rc = L.bb_kv_append(p, _lib.i64s(128 * 64, 129), p, s2, p, 128, p, 128, 8, 128, 64, p, 1, None)
+    assert rc == -1 and "16-byte aligned" in L.bb_last_error().decode()
