@@ -98,11 +98,12 @@ def staged_prefill(attn, q, k, v, ev):
 
 def main_traffic():
     """HBM bytes per launch of the main kernel from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
-    (profiles/prefill_128k_hbm_traffic.json, scaled by a calibrating 1 GiB copy); None when absent."""
+    (profiles/prefill_128k_hbm_traffic.json, scaled by calibrating kernels of known traffic); None when absent."""
     path = ROOT / "profiles" / "prefill_128k_hbm_traffic.json"
     try:
         data = json.loads(path.read_text())
-        return int(data["kernels"]["flash_ping_kernel [main]"]["bytes"])
+        keys = [k for k in data["kernels"] if k.startswith("flash_ping_kernel") and k.endswith("[main]")]
+        return int(data["kernels"][keys[0]]["bytes"])
     except (OSError, KeyError, ValueError):
         return None
 
