@@ -42,17 +42,6 @@ struct FlashSchedule {
 
 constexpr int kCUs = 256;
 
-// Waves per flash workgroup: 8 (32 query rows per wave, two waves per SIMD) or 4 (64 rows, one per SIMD).
-// BB_FLASH_WAVES=4 selects the latter for measurement.
-int flash_waves() {
-  static int w = [] {
-    const char* e = getenv("BB_FLASH_WAVES");
-    int v = e ? atoi(e) : 8;
-    return v == 4 ? 4 : 8;
-  }();
-  return w;
-}
-
 // The software-pipelined main-pass kernel is used wherever it applies; BB_FLASH_PIPE=0 selects the generic kernel
 // (for measurement).
 bool flash_pipe_enabled() {
@@ -229,7 +218,6 @@ static int sparse_flash_impl(const void* q, const int64_t* sq, const void* k, co
   p.head_splits = s.head_splits;
   p.n_chunks = s.n_chunks;
   p.remap = ((int64_t)p.n_kvbh * s.head_splits) % 8 == 0;
-  p.waves = flash_waves();
   p.np = bb_transpose_v_cols(N);
   p.c = (float)((double)scale * 1.4426950408889634);
   hipStream_t st = static_cast<hipStream_t>(stream);

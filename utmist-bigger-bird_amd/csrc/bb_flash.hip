@@ -460,7 +460,7 @@ hipError_t launch_dw(const FlashParams& p, int hpw, bool split, hipStream_t stre
 
 template <int D>
 hipError_t launch_d(const FlashParams& p, int hpw, bool split, hipStream_t stream) {
-  return p.waves == 8 ? launch_dw<D, 8>(p, hpw, split, stream) : launch_dw<D, 4>(p, hpw, split, stream);
+  return launch_dw<D, 8>(p, hpw, split, stream);
 }
 
 }  // namespace

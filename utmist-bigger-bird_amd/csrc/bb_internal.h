@@ -23,7 +23,7 @@ struct FlashParams {
   int rt_batches;           // 64-slot batches of one route list (route_k rounded up to 64)
   int f16;                  // 16-bit element type: 0 bf16, 1 fp16
   int BH, H, G, Hkv_pb, n_kvbh, front, window, route_k, n_groups;
-  int row_tiles, head_splits, n_chunks, remap, waves;
+  int row_tiles, head_splits, n_chunks, remap;
   float c;  // scale * log2(e)
 };
 
