@@ -228,7 +228,7 @@ BB_DEV float ping_exp(PingState& st, float c) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         pe[e] = fast_exp2(fmaf(st.s[kb][8 * u + e], c, nm));
-        sum += pe[e];
+        sum = kb == 0 && u == 0 && e == 0 ? pe[e] : sum + pe[e];  // no 0 + p[0] add
       }
       st.pk[kb][u] = as_bf16x8(u32x4_t{pack2<F16>(pe[0], pe[1]), pack2<F16>(pe[2], pe[3]),
                                        pack2<F16>(pe[4], pe[5]), pack2<F16>(pe[6], pe[7])});
@@ -282,9 +282,9 @@ BB_DEV void ping_softmax_open(PingState& st, float c) {
   float sum = ping_exp<F16>(st, c);
   const float lim = __builtin_amdgcn_exp2f(kRescaleThreshold);
   const bool over = !(sum <= lim);
-  const auto sw = __builtin_amdgcn_permlane32_swap((uint32_t)over, (uint32_t)over, false, false);
-  const bool need = (sw[0] | sw[1]) != 0u;
-  if (__builtin_amdgcn_ballot_w64(need)) {
+  if (__builtin_amdgcn_ballot_w64(over)) {  // some lane needs it, so some row does: only then pair up the lanes
+    const auto sw = __builtin_amdgcn_permlane32_swap((uint32_t)over, (uint32_t)over, false, false);
+    const bool need = (sw[0] | sw[1]) != 0u;
     const float mt = ping_tile_max(st, c);
     // the new offset never goes below the old one, so rows that do not need it keep theirs
     ping_rescale(st, need, __builtin_elementwise_maximum(mt, st.m));
