@@ -184,20 +184,67 @@ BB_DEV void ping_pv(PingState& st, const uint16_t* vt, int li, int h) {
 // matrix core between each read and the MFMA that consumes it). Fragment i < 16 is the V^T fragment of PV step
 // (kb, u, dv) = (i / 8, i / 4 % 2, i % 4); fragment 16 + j the K fragment of QK step (kb, dk) = (j / 8, j % 8).
 constexpr int kRing = 4;
-BB_DEV const u32x4_t* ping_frag(const uint16_t* kl, const uint16_t* vt, int i, int li, int h) {
+
+// Per-lane byte offsets of the fragments inside a K tile (k[dk], key half 0; half 1 is 8192 bytes on) and a V^T tile
+// (v[2 a + u] for d block 0; d block dv is 4096 dv bytes on, with a = kb ^ (dv & 1), since vt_swz(32 dv + li) =
+// vt_swz(li) ^ 4 (dv & 1)). With them a fragment address is one add of the tile's wave-uniform LDS address plus an
+// immediate.
+struct FragOfs {
+  uint32_t k[PD / 16];
+  uint32_t v[4];
+};
+BB_DEV FragOfs frag_ofs(int li, int h) {
+  FragOfs f;
+#pragma unroll
+  for (int dk = 0; dk < PD / 16; ++dk) f.k[dk] = 2u * (uint32_t)k_off<PD>(li, 2 * dk + h);
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) f.v[2 * a + u] = 2u * (uint32_t)vt_off(li, 4 * a + 2 * u + h);
+  return f;
+}
+BB_DEV uint32_t lds_addr(const void* p) {
+  return (uint32_t)reinterpret_cast<uintptr_t>(
+      reinterpret_cast<__attribute__((address_space(3))) const void*>(reinterpret_cast<uintptr_t>(p)));
+}
+BB_DEV u32x4_t lds16(uint32_t addr) {
+  return *(const __attribute__((address_space(3))) u32x4_t*)(uintptr_t)addr;
+}
+// The tile's fragment base addresses, one add each, kept opaque so that the per-fragment constants go into the
+// ds_read offset field instead of being folded into the scalar and added per read.
+struct FragBase {
+  uint32_t k[PD / 16];
+  uint32_t v[4];
+};
+BB_DEV FragBase frag_base(uint32_t kl, uint32_t vt, const FragOfs& f) {
+  FragBase b;
+#pragma unroll
+  for (int j = 0; j < PD / 16; ++j) {
+    b.k[j] = kl + f.k[j];
+    asm volatile("" : "+v"(b.k[j]));
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    b.v[j] = vt + f.v[j];
+    asm volatile("" : "+v"(b.v[j]));
+  }
+  return b;
+}
+BB_DEV u32x4_t ping_frag_at(const FragBase& b, int i) {
   if (i < 16) {
     const int kb = i / 8, u = (i / 4) % 2, dv = i % 4;
-    return reinterpret_cast<const u32x4_t*>(vt + vt_off(32 * dv + li, 2 * (2 * kb + u) + h));
+    return lds16(b.v[2 * (kb ^ (dv & 1)) + u] + 4096u * dv);
   }
   const int j = i - 16, kb = j / 8, dk = j % 8;
-  return reinterpret_cast<const u32x4_t*>(kl + k_off<PD>(32 * kb + li, 2 * dk + h));
+  return lds16(b.k[dk] + 8192u * kb);
 }
 
 template <bool F16>
-BB_DEV void ping_mfma_phase(PingState& st, const uint16_t* kl, const uint16_t* vt, int li, int h) {
+BB_DEV void ping_mfma_phase(PingState& st, uint32_t kl, uint32_t vt, const FragOfs& fo) {
+  const FragBase fb = frag_base(kl, vt, fo);
   u32x4_t ring[kRing];
 #pragma unroll
-  for (int i = 0; i < kRing; ++i) ring[i] = *ping_frag(kl, vt, i, li, h);
+  for (int i = 0; i < kRing; ++i) ring[i] = ping_frag_at(fb, i);
   st.s[0] = f32x16_t{};
   st.s[1] = f32x16_t{};
 #pragma unroll
@@ -210,7 +257,7 @@ BB_DEV void ping_mfma_phase(PingState& st, const uint16_t* kl, const uint16_t* v
       const int j = i - 16, kb = j / 8, dk = j % 8;
       st.s[kb] = mma32<F16>(a, st.qf[dk], st.s[kb]);
     }
-    if (i + kRing < 32) ring[i % kRing] = *ping_frag(kl, vt, i + kRing, li, h);
+    if (i + kRing < 32) ring[i % kRing] = ping_frag_at(fb, i + kRing);
     __builtin_amdgcn_sched_barrier(0);
   }
 }
@@ -441,6 +488,7 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
   uint16_t* ring = smem;
   auto kst = [&](int t) { return ring + (t & (PST - 1)) * 2 * PTE; };
   auto vst = [&](int t) { return ring + (t & (PST - 1)) * 2 * PTE + PTE; };
+  const FragOfs fo = frag_ofs(li, h);
   TileLoader ld;
   ld.init(kbase, p.sk1, p.N, vtbase, p.np, wave, lane);
 
@@ -462,7 +510,7 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
     for (int t = 1; t < nu; ++t) {
       // MFMA phase: PV of tile t-1, QK of tile t
       __builtin_amdgcn_s_setprio(1);
-      ping_mfma_phase<F16>(st, kst(t), vst(t - 1), li, h);
+      ping_mfma_phase<F16>(st, lds_addr(kst(t)), lds_addr(vst(t - 1)), fo);
       __builtin_amdgcn_s_setprio(0);
       vm_wait_tile(false);  // tile t+1 has landed
       ring_barrier();
@@ -477,7 +525,7 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
 #pragma unroll 1
     for (int t = nu > 1 ? nu : 1; t < ntot; ++t) {
       __builtin_amdgcn_s_setprio(1);
-      ping_mfma_phase<F16>(st, kst(t), vst(t - 1), li, h);
+      ping_mfma_phase<F16>(st, lds_addr(kst(t)), lds_addr(vst(t - 1)), fo);
       __builtin_amdgcn_s_setprio(0);
       vm_wait_tile(false);
       ring_barrier();
