@@ -108,6 +108,18 @@ def main_traffic():
         return None
 
 
+def main_activity():
+    """Clock and matrix-core busy fraction of the main kernel from the committed rocprofv3 counter summary
+    (profiles/prefill_128k_mfma_busy.json: GRBM_GUI_ACTIVE, SQ_VALU_MFMA_BUSY_CYCLES); empty when absent."""
+    path = ROOT / "profiles" / "prefill_128k_mfma_busy.json"
+    try:
+        m = json.loads(path.read_text())["flash_ping_kernel [main]"]
+        return {"mfma_busy": m["mfma_busy"], "clock_ghz": m["clock_ghz"],
+                "activity_source": "profiles/prefill_128k_mfma_busy.md"}
+    except (OSError, KeyError, ValueError):
+        return {}
+
+
 def cpu_model():
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -651,7 +663,8 @@ def main():
                      "achieved": round(main_tflops, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(main_tflops / PEAK_BF16_TFLOPS, 4), "traffic": main_traffic(),
                      "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE/WRITE_SIZE, copy-calibrated)",
-                     "flop_per_launch": flops_main, "avg_launch_ms": round(stage_avg["main"], 4)},
+                     "flop_per_launch": flops_main, "avg_launch_ms": round(stage_avg["main"], 4),
+                     **main_activity()},
         "tail_roofline": {"bound": "mfma", "achieved": round(tail_tflops, 1), "peak": PEAK_BF16_TFLOPS,
                           "unit": "TFLOP/s", "frac": round(tail_tflops / PEAK_BF16_TFLOPS, 4),
                           "hbm_gbps": round(tail_bytes / (stage_avg["tail"] * 1e-3) / 1e9, 1),
