@@ -182,7 +182,8 @@ BB_DEV void ping_pv(PingState& st, const uint16_t* vt, int li, int h) {
 // MFMA phase of the window loop: O^T += V^T(t-1) P(t-1)^T (16 MFMAs), then S(t) = K(t) Q^T (16 MFMAs), with the LDS
 // fragment reads software-pipelined four MFMAs ahead through a register ring (the LDS latency would otherwise idle the
 // matrix core between each read and the MFMA that consumes it). Fragment i < 16 is the V^T fragment of PV step
-// (kb, u, dv) = (i / 8, i / 4 % 2, i % 4); fragment 16 + j the K fragment of QK step (kb, dk) = (j / 8, j % 8).
+// (kb, u, dv) = (i / 8, i / 4 % 2, i % 4); fragment 16 + j the K fragment of QK step (kb, dk) = (j % 2, j / 2): the
+// two key halves' chains interleave, so consecutive MFMAs share their Q operand (each chain still sums dk in order).
 constexpr int kRing = 4;
 
 // Per-lane byte offsets of the fragments inside a K tile (k[dk], key half 0; half 1 is 8192 bytes on) and a V^T tile
@@ -235,7 +236,7 @@ BB_DEV u32x4_t ping_frag_at(const FragBase& b, int i) {
     const int kb = i / 8, u = (i / 4) % 2, dv = i % 4;
     return lds16(b.v[2 * (kb ^ (dv & 1)) + u] + 4096u * dv);
   }
-  const int j = i - 16, kb = j / 8, dk = j % 8;
+  const int j = i - 16, kb = j % 2, dk = j / 2;
   return lds16(b.k[dk] + 8192u * kb);
 }
 
@@ -254,7 +255,7 @@ BB_DEV void ping_mfma_phase(PingState& st, uint32_t kl, uint32_t vt, const FragO
       const int kb = i / 8, u = (i / 4) % 2, dv = i % 4;
       st.o[dv] = mma32<F16>(a, st.pk[kb][u], st.o[dv]);
     } else {
-      const int j = i - 16, kb = j / 8, dk = j % 8;
+      const int j = i - 16, kb = j % 2, dk = j / 2;
       st.s[kb] = mma32<F16>(a, st.qf[dk], st.s[kb]);
     }
     if (i + kRing < 32) ring[i % kRing] = ping_frag_at(fb, i + kRing);
