@@ -372,12 +372,12 @@ int bb_int8_dequantize(const int8_t* q, const void* scale, int scale_is_f16, int
                     "bb_int8_dequantize");
 }
 
-// Keys per decode workgroup: about four workgroups per CU, at least 256 keys, a multiple of 128 (four 32-key wave
-// chunks of the MFMA decode).
+// Keys per decode workgroup: four workgroups per CU of equal length (at least 256 keys). The length is not rounded:
+// the bytes per CU, not the 32-key chunks per wave, set the time of this HBM-bound kernel (rounding 131073 keys up
+// to 1152 per split left 912 workgroups, some CUs with a third more bytes than others).
 static int64_t decode_split_len(int64_t n, int Hkv) {
   int64_t len = cdiv(n, cdiv(4 * kCUs, Hkv));
-  if (len < 256) len = 256;
-  return cdiv(len, 128) * 128;
+  return len < 256 ? 256 : len;
 }
 static int decode_splits(int64_t n, int Hkv) { return (int)cdiv(n, decode_split_len(n, Hkv)); }
 

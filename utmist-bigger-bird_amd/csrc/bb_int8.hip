@@ -482,39 +482,60 @@ bool decode_mfma_fits(const DecodeParams& p) {
   return (p.n + kMdChunk) * (int64_t)p.Hkv * 128 < ((int64_t)1 << 31);
 }
 
-// Split merge: one workgroup per query head; thread (d, split group) folds every (1024 / D)-th split of column d
-// (all loads independent, so they overlap), then the groups combine through LDS.
-constexpr int kMergeThreads = 1024;
+// Split merge: a workgroup per (query head, 16 columns), so that the partials are read by 8x as many CUs. Thread
+// (column, group) folds every 16th split of its column with a running maximum, loading 8 splits at a time; the 16
+// groups then combine through LDS.
+constexpr int kMergeThreads = 256;
+constexpr int kMergeCols = 16;
+constexpr int kMergeGroups = kMergeThreads / kMergeCols;
+constexpr int kMergePer = 8;
 template <int D>
 __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(DecodeParams p) {
-  constexpr int NG = kMergeThreads / D;
-  __shared__ float red_m[kMergeThreads], red_l[NG], red_o[NG][D];
-  const int h = blockIdx.x, t = threadIdx.x, d = t % D, grp = t / D;
-  const float* base = p.part + (int64_t)h * p.n_splits * (D + 2);
-  float M = -1.0e30f;
-  for (int s = t; s < p.n_splits; s += kMergeThreads) M = fmaxf(M, base[(int64_t)s * (D + 2) + D]);
-  red_m[t] = M;
-  __syncthreads();
-  for (int w = kMergeThreads / 2; w > 0; w >>= 1) {
-    if (t < w) red_m[t] = fmaxf(red_m[t], red_m[t + w]);
-    __syncthreads();
+  __shared__ float sm_m[kMergeGroups], sm_l[kMergeGroups], sm_o[kMergeGroups][kMergeCols];
+  const int h = blockIdx.x, t = threadIdx.x, dl = t % kMergeCols, grp = t / kMergeCols;
+  const int d = kMergeCols * blockIdx.y + dl;
+  const int ns = p.n_splits;
+  const float* base = p.part + (int64_t)h * ns * (D + 2);
+  float M = -1.0e30f, L = 0.0f, O = 0.0f;
+  for (int i0 = 0; grp + kMergeGroups * i0 < ns; i0 += kMergePer) {
+    float mv[kMergePer], lv[kMergePer], ov[kMergePer];
+#pragma unroll
+    for (int i = 0; i < kMergePer; ++i) {
+      const int s = grp + kMergeGroups * (i0 + i);
+      const bool ok = s < ns;
+      const float* r = base + (int64_t)(ok ? s : 0) * (D + 2);
+      mv[i] = ok ? r[D] : -1.0e30f;
+      lv[i] = ok ? r[D + 1] : 0.0f;
+      ov[i] = ok ? r[d] : 0.0f;
+    }
+    float mn = M;
+#pragma unroll
+    for (int i = 0; i < kMergePer; ++i) mn = fmaxf(mn, mv[i]);
+    const float a = fast_exp2(M - mn);
+    L *= a;
+    O *= a;
+#pragma unroll
+    for (int i = 0; i < kMergePer; ++i) {
+      const float w = fast_exp2(mv[i] - mn);
+      L += w * lv[i];
+      O += w * ov[i];
+    }
+    M = mn;
   }
-  M = red_m[0];
-  float L = 0.0f, O = 0.0f;
-#pragma unroll 4
-  for (int s = grp; s < p.n_splits; s += NG) {
-    const float* r = base + (int64_t)s * (D + 2);
-    const float w = fast_exp2(r[D] - M);
-    L += w * r[D + 1];
-    O += w * r[d];
-  }
-  red_o[grp][d] = O;
-  if (d == 0) red_l[grp] = L;
+  sm_o[grp][dl] = O;
+  if (dl == 0) { sm_m[grp] = M; sm_l[grp] = L; }
   __syncthreads();
   if (grp == 0) {
+    float mx = sm_m[0];
+#pragma unroll
+    for (int g2 = 1; g2 < kMergeGroups; ++g2) mx = fmaxf(mx, sm_m[g2]);
     float lt = 0.0f, ot = 0.0f;
 #pragma unroll
-    for (int g2 = 0; g2 < NG; ++g2) { lt += red_l[g2]; ot += red_o[g2][d]; }
+    for (int g2 = 0; g2 < kMergeGroups; ++g2) {
+      const float w = fast_exp2(sm_m[g2] - mx);
+      lt += w * sm_l[g2];
+      ot += w * sm_o[g2][dl];
+    }
     p.out[(int64_t)h * p.so + d] = f32_to_bf16(ot / fmaxf(lt, 1.0e-20f));
   }
 }
@@ -530,7 +551,7 @@ hipError_t launch_decode_dg(const DecodeParams& p, hipStream_t stream) {
     hipLaunchKernelGGL((decode_kernel<D, G, true>), dim3(p.n_splits, p.Hkv), dim3(kDecThreads), 0, stream, p);
   else
     hipLaunchKernelGGL((decode_kernel<D, G, false>), dim3(p.n_splits, p.Hkv), dim3(kDecThreads), 0, stream, p);
-  hipLaunchKernelGGL(decode_merge_kernel<D>, dim3(p.H), dim3(kMergeThreads), 0, stream, p);
+  hipLaunchKernelGGL(decode_merge_kernel<D>, dim3(p.H, D / kMergeCols), dim3(kMergeThreads), 0, stream, p);
   return hipGetLastError();
 }
 
