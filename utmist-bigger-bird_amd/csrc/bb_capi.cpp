@@ -500,15 +500,15 @@ int bb_decode_noalloc(const void* q, int64_t sq, const int8_t* k8, const void* k
 // Key chunks of the split-K decode kernels, as kernels/bigger_bird_decode.py:84-88 and bigger_bird_route.py:91-94
 // choose them (64-key blocks, about four workgroups per CU; `splits` > 0 requests a count).
 // Keys per split of a decode-time key range: `splits` when given, else about `per_cu` workgroups per CU over all
-// `programs` rows (at least 256 keys each), in whole 64-key blocks. The split-K decode runs best at 2 per CU (fewer,
-// longer splits: less per-workgroup set-up and a cheaper merge; 5.3 TB/s over a 128K-token bf16 cache), the routing
-// scores pass at 4.
+// `programs` rows (at least 256 keys each), not rounded, so that every workgroup reads the same number of keys. The
+// split-K decode runs best at 2 per CU (fewer, longer splits: less per-workgroup set-up and a cheaper merge; 5.3 TB/s
+// over a 128K-token bf16 cache), the routing scores pass at 4.
 static int64_t decode_chunk_len(int64_t total, int programs, int splits, int64_t cap_splits, int per_cu = 2) {
   if (total <= 0) return 64;
   int64_t s = splits > 0 ? splits
                          : std::max<int64_t>(1, std::min<int64_t>(cdiv(total, 4 * 64), cdiv(per_cu * kCUs, programs)));
   if (cap_splits > 0 && s > cap_splits) s = cap_splits;
-  return cdiv(cdiv(total, s), 64) * 64;
+  return cdiv(total, s);
 }
 
 size_t bb_sparse_decode_workspace(int H, int Hkv, int D, int rows, int front, int window, int route_k, int splits) {
