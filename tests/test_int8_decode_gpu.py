@@ -48,8 +48,10 @@ def _check(got, ref, what):
     assert err.max().item() < 2e-2 and err.mean().item() < 2e-3, what
 
 
+# 32769 and 131329 keys: 128 splits of 257 / 1027 keys (not a multiple of the 32-key chunk), the last one short
 @pytest.mark.parametrize("n,H,Hkv,d,f16", [(1, 32, 8, 128, True), (300, 32, 8, 128, True), (4099, 32, 8, 128, False),
-                                           (20000, 16, 2, 64, True), (131072, 32, 8, 128, False)])
+                                           (20000, 16, 2, 64, True), (32769, 32, 8, 128, True),
+                                           (131072, 32, 8, 128, False), (131329, 32, 8, 128, False)])
 def test_decode_int8_matches_oracle(n, H, Hkv, d, f16, dev):
     print(f"case decode_int8 n={n} H={H}/{Hkv} d={d} f16={f16}", flush=True)
     cap = n + 5  # spare capacity past n must be ignored
