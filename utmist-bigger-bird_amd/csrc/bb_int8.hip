@@ -330,9 +330,10 @@ __global__ __launch_bounds__(64 * kMdWaves, 2) void decode_mfma_kernel(DecodePar
   for (int dk = 0; dk < 8; ++dk)
     qa[dk] = as_bf16x8(li < 4 ? ld16(p.q + (int64_t)(4 * g + li) * p.sq + 64 * hh + 8 * dk) : u32x4_t{0, 0, 0, 0});
 
-  // one buffer resource per cache over KV head g's rows 0..n-1 (row j at byte j * row_bytes): rows >= n read as 0
+  // one buffer resource per cache over KV head g's rows up to this split's end (row j at byte j * row_bytes): the
+  // rows a split's last, partial 32-key chunk reaches past it read as 0 instead of being fetched
   const int64_t row_bytes = (int64_t)p.Hkv * D;
-  const int range = (int)((p.n - 1) * row_bytes + D);
+  const int range = (int)((j_end - 1) * row_bytes + D);
   const __amdgpu_buffer_rsrc_t krs =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(p.k8 + (int64_t)g * D), 0, range, 0x00020000);
   const __amdgpu_buffer_rsrc_t vrs =
@@ -361,7 +362,7 @@ __global__ __launch_bounds__(64 * kMdWaves, 2) void decode_mfma_kernel(DecodePar
       r.k[c4] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(krs, off + 16u * c4, 0, 0));
       r.v[c4] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(vrs, off + 16u * c4, 0, 0));
     }
-    const int64_t si = (key < p.n ? key : p.n - 1) * p.Hkv + g;
+    const int64_t si = (key < j_end ? key : j_end - 1) * p.Hkv + g;
     if constexpr (F16S) {
       r.ks = __half2float(reinterpret_cast<const __half*>(p.ks)[si]);
       r.vs = __half2float(reinterpret_cast<const __half*>(p.vs)[si]);
