@@ -267,7 +267,7 @@ def decode_leg(dev, seed):
 
 
 def sparse_decode_leg(dev, seed):
-    """Sparse decode after a 128K prefill (SURVEY next step: kernels/bigger_bird_decode.py + bigger_bird_route.py):
+    """Sparse decode after a 128K prefill (the reference's kernels/bigger_bird_decode.py + bigger_bird_route.py):
     bf16 cache of 131072 tokens (+1 per step), 32 q / 8 KV heads, d=128; a step appends the new K/V row at the
     device-side length, routes (pooled decode routing over every cached key, top 512 per KV head outside the sink
     and the 16384-key window) and attends sink 64 + window 16384 + the 512 routed keys. The step's inputs are fixed
@@ -481,7 +481,7 @@ def graph_decode_leg(model, ids, steps=32):
 
 
 def full_model_leg(dev, seed, T=131072):
-    """BASELINE configs[2] (SURVEY next step): prefill of a random-init Llama-3-8B-architecture model in bf16 (32 layers,
+    """prefill of a random-init Llama-3-8B-architecture model in bf16 (32 layers,
     hidden 4096, 32 q / 8 KV heads, FFN 14336, vocab 128256, RoPE theta 500000) at T uniform-random token ids, with
     RDAttention on every layer: the sparse arm (final cfg {64, 16384, 512, 256}) and the exact arm (`dense_rd`: the
     same module with exact causal attention on the HIP kernel). KV cache on, last-token logits only, as the
