@@ -619,11 +619,12 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
   }
 
   // ---- epilogue ----
+  if (p.route_k <= 0) __syncthreads();  // the ring is free for the output staging (the routed phase ends on one)
   if (!it.wave_live) return;
-  const int64_t row = it.rw + li;
   const float lt = xhalf_sum(st.l);
-  if (row >= it.T_eff) return;
   if (p.n_chunks > 1) {  // partial (O, m, l) of this key chunk for flash_merge_kernel
+    const int64_t row = it.rw + li;
+    if (row >= it.T_eff) return;
     const int64_t base = ((int64_t)it.chunk * p.BH + it.bh) * p.T + row;
     float* po = p.part_o + base * PD;
 #pragma unroll
@@ -638,17 +639,31 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
     }
     return;
   }
+  // The normalised rows pass through this wave's 8 KB of LDS (row r at r * 256 bytes, its 16-byte chunk k in slot
+  // k ^ (r % 16)), so that every global store writes two whole rows: lane l of store i takes bytes 8 (l % 32) .. of
+  // row 2 i + l / 32. Stored from the fragment layout, each store would touch 32 rows.
   const float inv = 1.0f / fmaxf(lt, 1.0e-20f);
-  uint16_t* orow = p.out + (int64_t)it.bh * p.so0 + row * p.so1;
+  uint16_t* stage = smem + wave * (32 * PD);
 #pragma unroll
   for (int dv = 0; dv < PD / 32; ++dv)
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
-      const int d0 = 32 * dv + 8 * g4 + 4 * h;
+      const int k = 4 * dv + g4;
       const u32x2_t w = {pack2<F16>(st.o[dv][4 * g4] * inv, st.o[dv][4 * g4 + 1] * inv),
                          pack2<F16>(st.o[dv][4 * g4 + 2] * inv, st.o[dv][4 * g4 + 3] * inv)};
-      *reinterpret_cast<u32x2_t*>(orow + d0) = w;
+      *reinterpret_cast<u32x2_t*>(stage + li * PD + 8 * (k ^ (li & 15)) + 4 * h) = w;
     }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  uint16_t* obase = p.out + (int64_t)it.bh * p.so0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int r = 2 * i + (lane >> 5), q = lane & 31, k = q >> 1;
+    const u32x2_t w = *reinterpret_cast<const u32x2_t*>(stage + r * PD + 8 * (k ^ (r & 15)) + 4 * (q & 1));
+    const int64_t row = it.rw + r;
+    if (row < it.T_eff) *reinterpret_cast<u32x2_t*>(obase + row * p.so1 + 4 * q) = w;
+  }
 }
 
 // Pre-gathers, per query head and route group, the routed K rows and V^T columns of every 64-slot batch into the
