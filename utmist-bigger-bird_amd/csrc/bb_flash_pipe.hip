@@ -623,19 +623,31 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
   if (!it.wave_live) return;
   const float lt = xhalf_sum(st.l);
   if (p.n_chunks > 1) {  // partial (O, m, l) of this key chunk for flash_merge_kernel
-    const int64_t row = it.rw + li;
-    if (row >= it.T_eff) return;
-    const int64_t base = ((int64_t)it.chunk * p.BH + it.bh) * p.T + row;
-    float* po = p.part_o + base * PD;
+    // The fp32 rows pass through this wave's 16 KB of LDS (row r at r * 512 bytes, its 16-byte chunk k in slot
+    // k ^ (r % 16)) so that every global store writes two whole rows, as for the output below.
+    float* fstage = reinterpret_cast<float*>(smem) + wave * (32 * PD);
 #pragma unroll
     for (int dv = 0; dv < PD / 32; ++dv)
 #pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4)
-        *reinterpret_cast<f32x4_t*>(po + 32 * dv + 8 * g4 + 4 * h) =
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int k = 8 * dv + 2 * g4 + h;
+        *reinterpret_cast<f32x4_t*>(fstage + li * PD + 4 * (k ^ (li & 15))) =
             f32x4_t{st.o[dv][4 * g4], st.o[dv][4 * g4 + 1], st.o[dv][4 * g4 + 2], st.o[dv][4 * g4 + 3]};
-    if (h == 0) {
-      p.part_ml[2 * base] = st.m;
-      p.part_ml[2 * base + 1] = lt;
+      }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int64_t base0 = ((int64_t)it.chunk * p.BH + it.bh) * p.T + it.rw;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = 2 * i + (lane >> 5), k = lane & 31;
+      const f32x4_t v = *reinterpret_cast<const f32x4_t*>(fstage + r * PD + 4 * (k ^ (r & 15)));
+      if (it.rw + r < it.T_eff) *reinterpret_cast<f32x4_t*>(p.part_o + (base0 + r) * PD + 4 * k) = v;
+    }
+    const int64_t row = it.rw + li;
+    if (h == 0 && row < it.T_eff) {
+      p.part_ml[2 * (base0 + li)] = st.m;
+      p.part_ml[2 * (base0 + li) + 1] = lt;
     }
     return;
   }
