@@ -24,11 +24,21 @@ extern "C" {
 #define BB_EINVAL (-1)
 #define BB_EHIP (-2)
 
-/* Library version (major * 10000 + minor * 100 + patch). */
+/* Library version (major * 10000 + minor * 100 + patch). The minor number changes with every change of an entry
+ * point's parameter list, so a caller built against another header can refuse the library:
+ *   100  first release
+ *   200  bb_sparse_flash takes is_f16 (after D); bb_sparse_flash_workspace takes n_groups (after route_k) and
+ *        has_key_mask (last); bb_rope_inplace takes is_f16 (before stream) */
+#define BB_ABI_VERSION 200
 int bb_version(void);
 
 /* Message of the last failed call on this host thread ("" if none). */
 const char* bb_last_error(void);
+
+/* Optional set-up for the current device (no reference counterpart): resolves the device address of
+ * bb_decode_noalloc's static scratch, which that entry point otherwise looks up on its first call on a device. Call
+ * it once per device before capturing bb_decode_noalloc into a HIP graph. Allocates nothing. */
+int bb_init(void);
 
 /*
  * Sparse flash attention: one joint softmax over front anchors | causal local window | routed keys.
@@ -52,10 +62,13 @@ int bb_sparse_flash(const void* q, const int64_t* sq, const void* k, const int64
                     int64_t route_chunk, float scale, int64_t row_end, void* ws, size_t ws_bytes, void* stream);
 
 /* Workspace bytes for bb_sparse_flash (n_groups and route_k as passed to it); have_vt != 0 when the caller passes a
- * precomputed V^T. Besides V^T and the split partials it holds the routed K/V^T tiles pre-gathered per query head
- * (32 KB per 64 route slots per head and group) for head_dim 128 with a multiple of 4 query heads per KV head. */
+ * precomputed V^T, has_key_mask != 0 when it passes a key_mask. Besides V^T and the split partials it holds the
+ * routed K/V^T tiles pre-gathered per query head (32 KB per 64 route slots per head) for head_dim 128 with a
+ * multiple of 4 query heads per KV head, a single route group and no key mask; with several route groups the kernel
+ * gathers the routed rows itself and no tiles are reserved. */
 size_t bb_sparse_flash_workspace(int BH, int64_t T, int64_t N, int D, int num_heads, int kv_groups, int64_t front,
-                                 int64_t window, int route_k, int n_groups, int64_t row_end, int have_vt);
+                                 int64_t window, int route_k, int n_groups, int64_t row_end, int have_vt,
+                                 int has_key_mask);
 
 /*
  * Non-causal exact attention: every one of the T query rows attends all N keys (T <= N), in one launch (plus a merge

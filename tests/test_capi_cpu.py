@@ -30,15 +30,23 @@ def test_library_exports_every_declared_function():
 
 def test_version_and_sizes():
     L = _lib.lib()
-    assert L.bb_version() >= 100
+    assert L.bb_version() == 200  # the parameter lists of include/bb_attn.h (BB_ABI_VERSION)
     assert L.bb_transpose_v_cols(1) == 64 and L.bb_transpose_v_cols(64) == 64 and L.bb_transpose_v_cols(65) == 128
     assert L.bb_routes_workspace(131072, 32, 8, 1, 64) > 32 * 131072 * 8
     assert L.bb_decode_workspace(131072, 32, 8, 128) > 0
     # tail shape: few row tiles, no routes -> the split-key schedule asks for partials
-    tail = L.bb_sparse_flash_workspace(32, 256, 131072, 128, 32, 4, 0, 131072, 0, 1, 256, 1)
-    main = L.bb_sparse_flash_workspace(32, 131072, 131072, 128, 32, 4, 64, 16384, 512, 1, 131072 - 256, 1)
+    tail = L.bb_sparse_flash_workspace(32, 256, 131072, 128, 32, 4, 0, 131072, 0, 1, 256, 1, 0)
+    main = L.bb_sparse_flash_workspace(32, 131072, 131072, 128, 32, 4, 64, 16384, 512, 1, 131072 - 256, 1, 0)
     # main pass: only the routed tiles pre-gathered per head (512 slots = 8 batches of a 16 KB K and V^T tile each)
     assert tail > 0 and main == 32 * 8 * 2 * 64 * 128 * 2
+    # the module's default budget (2048 slots) pre-gathers 32 batches per head
+    assert L.bb_sparse_flash_workspace(32, 131072, 131072, 128, 32, 4, 64, 4096, 2048, 1, 131072, 1, 0) == \
+        32 * 32 * 2 * 64 * 128 * 2
+    # vertical_scope (modal_rd/results/b7_v2k_scope8k.json: vertical 2048, scope_chunk 4096 -> 32 route groups at
+    # 128K): the kernel gathers the used batches itself, so nothing is reserved for routed tiles (1 GiB otherwise)
+    assert L.bb_sparse_flash_workspace(32, 131072, 131072, 128, 32, 4, 64, 4096, 2048, 32, 131072, 1, 0) == 0
+    # a key mask leaves the pipelined kernel: no routed tiles either
+    assert L.bb_sparse_flash_workspace(32, 131072, 131072, 128, 32, 4, 64, 16384, 512, 1, 131072, 1, 1) == 0
 
 
 def _flash_call(**over):

@@ -1,4 +1,4 @@
-"""kv_evict on the GPU (mirrors the reference's tests/test_kv_evict.py:26-64 with a tiny random-init Llama):
+"""kv_evict on the GPU (mirrors the reference's tests/test_kv_evict.py:26-100 with a tiny random-init Llama):
 prefill logits are unchanged by eviction, every layer's cache shrinks to sink + window + groups * vertical rows, the
 kept positions are sorted and unique with the sink, the window and every routed column of the layer's query heads,
 and the compacted cache equals the full cache gathered at the kept positions (torch's own gather). The two HIP
@@ -150,3 +150,53 @@ def test_evict_options_match_torch_topk(dev, monkeypatch):
             assert torch.equal(got.layers[i].values, want.layers[i].values), (opts, i)
         if opts.get("evict_full_layers"):
             assert kept[0].shape[-1] == N and got.layers[0].keys.shape[-2] == N
+
+
+def test_decode_matches_masked_full_cache(dev):
+    """tests/test_kv_evict.py:67-100 of the reference: 6 greedy tokens through HF generate on the evicted cache (the
+    HIP decode over the compacted rows; this also checks that RoPE positions continue from the prompt length) equal
+    those of a full-cache model whose decode attention is masked to the same kept positions plus every generated
+    token. The masked reference runs float32 SDPA; scores within 2e-2 (bf16), sequences equal."""
+    import types
+
+    import torch.nn.functional as F
+
+    print("case kv_evict_decode", flush=True)
+    torch.manual_seed(4)
+    ids = torch.randint(0, 512, (1, N), device=dev)
+    gen = dict(max_new_tokens=6, min_new_tokens=6, do_sample=False, use_cache=True, pad_token_id=0,
+               output_scores=True, return_dict_in_generate=True)
+    ev = _tiny(dev)
+    install(ev, "rd", kv_evict=True, **KW)
+    with torch.inference_mode():
+        out = ev.generate(ids, **gen)
+    kept = [layer.self_attn.kept for layer in ev.model.layers]
+    g = ev.config.num_attention_heads // ev.config.num_key_value_heads
+    m = KW["sink"] + KW["window"] + g * KW["vertical"]
+    assert all(kp.shape[-1] == m for kp in kept)
+
+    ref = _tiny(dev)
+    install(ref, "rd", **KW)
+    for layer, kp in zip(ref.model.layers, kept):
+        attn = layer.self_attn
+        orig = attn.exact_attention
+
+        def masked(self, q, k, v, t, n, _orig=orig, _kp=kp):
+            if t == n:
+                return _orig(q, k, v, t, n)
+            keep = torch.zeros(self.num_kv_heads, n, dtype=torch.bool, device=q.device)
+            keep.scatter_(1, _kp, True)
+            keep[:, N:] = True  # every generated token
+            mask = keep.repeat_interleave(self.groups, 0)[None, :, None, :]
+            kf = k.float().repeat_interleave(self.groups, 1)
+            vf = v.float().repeat_interleave(self.groups, 1)
+            o = F.scaled_dot_product_attention(q.float(), kf, vf, attn_mask=mask, scale=self.scaling)
+            return o.to(q.dtype)
+
+        attn.exact_attention = types.MethodType(masked, attn)
+    with torch.inference_mode():
+        want = ref.generate(ids, **gen)
+    assert len(out.scores) == 6, "all decode steps must run"
+    assert torch.equal(out.sequences, want.sequences)
+    for a, b in zip(out.scores, want.scores):
+        torch.testing.assert_close(a.float(), b.float(), atol=2e-2, rtol=2e-2)

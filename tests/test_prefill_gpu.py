@@ -3,7 +3,8 @@ at BASELINE config 1 (T=8192, {64, 2048, 128, 256}) and config 2 (T=131072, {64,
 per KV head) on the inputs the reference's routes() saw (tests/golden): routes set-exact against the reference, and
 output rows within max-abs 2e-2 / mean-abs 2e-3 of the float64 oracle over the union mask -- every (head, row) at
 config 1; at config 2, 8 heads (one per KV group) at every 64-row tile boundary, the window edges, routed keys' first
-rows, 4096 random rows and every exact-tail row. Config 4 (B=4) checks sampled rows of all 32 heads.
+rows, 4096 random rows and every exact-tail row. Config 4 (B=4) checks sampled rows of all 32 heads, and each
+element's routes set-exact (pooled values bit-equal) against the oracle on that element's inputs.
 """
 from types import SimpleNamespace
 
@@ -108,6 +109,20 @@ def test_config4_batch_sampled_rows(dev):
             assert torch.equal(one[0, :, :T - r], out[b, :, :T - r]), b
             assert (one[0, :, T - r:].float() - out[b, :, T - r:].float()).abs().max().item() < 4e-3, b
     attn.last_routes = routes_all
+    # every element's routes at this shape against the oracle on that element's own inputs: set-exact, and the
+    # pooled values of the batched launch bit-equal to the oracle's (eligible columns [sink, T - window))
+    from bigger_bird_amd.attention import routes as hip_routes
+    with torch.inference_mode():
+        idx_b, pooled_b = hip_routes(inp["q"], inp["k"], num_heads=H, num_kv_heads=Hkv, sink=cfg["sink"], window=W,
+                                     budget=512, scaling=d ** -0.5, return_pooled=True)
+    assert torch.equal(idx_b.view(B, H, -1), routes_all)
+    for b in range(B):
+        want, want_pooled = oracle.routes(inp["q"][b], inp["k"][b], sink=cfg["sink"], window=W, budget=512,
+                                          scaling=d ** -0.5, return_pooled=True)
+        assert torch.equal(routes_all[b].cpu(), want), f"config4 b={b}: routes differ from the oracle"
+        prob = (want_pooled.double() * 2.0 ** -40 / 64).float()
+        got = pooled_b.view(B, H, -1)[b].cpu()
+        assert torch.equal(got[:, cfg["sink"]:T - W], prob[:, cfg["sink"]:T - W]), f"config4 b={b}: pooled differ"
     gen = torch.Generator().manual_seed(9)
     rows = torch.tensor([0, 63, 64, W - 1, W, W + 64, T // 2, T - r - 1, T - r, T - 1])
     rows = torch.cat([rows, torch.randint(0, T, (4,), generator=gen)])

@@ -63,3 +63,33 @@ def test_noalloc_rejects_partials_beyond_the_scratch(dev):
     assert rc == -1 and "exceed the static scratch" in L.bb_last_error().decode()
     with pytest.raises(ValueError, match="static scratch"):
         _lib.check(rc)
+
+
+def test_noalloc_in_captured_graph(dev):
+    """bb_decode_noalloc captured into a HIP graph (its scratch address is resolved when the library is loaded, before
+    any capture): every replay, with eager work between replays, equals bb_decode bitwise."""
+    print("case decode_noalloc graph capture", flush=True)
+    L = _lib.lib()
+    H, Hkv, d, n = 32, 8, 128, 40000
+    k8, ks, v8, vs = _cache(n, Hkv, d, 21, dev, True)
+    g = torch.Generator(device=dev).manual_seed(22)
+    q = torch.randn(H, d, device=dev, generator=g).to(torch.bfloat16)
+    ws = torch.empty(L.bb_decode_workspace(n, H, Hkv, d), dtype=torch.uint8, device=dev)
+    want = torch.empty(H, d, dtype=torch.bfloat16, device=dev)
+    _lib.check(_call(L, False, q, k8, ks, v8, vs, n, H, Hkv, d, want, ws))
+    out = torch.empty(H, d, dtype=torch.bfloat16, device=dev)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up outside the capture
+        _lib.check(_call(L, True, q, k8, ks, v8, vs, n, H, Hkv, d, out))
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _lib.check(_call(L, True, q, k8, ks, v8, vs, n, H, Hkv, d, out))
+    for i in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16)), f"replay {i} differs"

@@ -18,10 +18,12 @@ _vp, _i32, _i64, _f32, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctyp
 SIGNATURES = {
     "bb_version": (_i32, []),
     "bb_last_error": (ctypes.c_char_p, []),
+    "bb_init": (_i32, []),
     "bb_sparse_flash": (_i32, [_vp, c_i64p, _vp, c_i64p, _vp, c_i64p, _vp, _vp, c_i64p, _i32, _i32, _vp, _i64,
                                _vp, c_i64p, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _i64, _i64, _i64, _f32, _i64,
                                _vp, _sz, _vp]),
-    "bb_sparse_flash_workspace": (_sz, [_i32, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _i32, _i32, _i64, _i32]),
+    "bb_sparse_flash_workspace": (_sz, [_i32, _i64, _i64, _i32, _i32, _i32, _i64, _i64, _i32, _i32, _i64, _i32,
+                                        _i32]),
     "bb_exact_attention": (_i32, [_vp, c_i64p, _vp, c_i64p, _vp, c_i64p, _vp, _vp, c_i64p, _i32, _i64, _i64, _i32, _i32,
                                   _i32, _i32, _f32, _vp, _sz, _vp]),
     "bb_exact_attention_workspace": (_sz, [_i32, _i64, _i64, _i32, _i32, _i32, _i32]),
@@ -67,6 +69,11 @@ def lib():
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(handle, name)
             fn.restype, fn.argtypes = res, args
+        if torch.cuda.is_available():
+            # per-device set-up of the current device ahead of any graph capture (bb_decode_noalloc's scratch)
+            rc = handle.bb_init()
+            if rc != 0:
+                raise RuntimeError(handle.bb_last_error().decode(errors="replace"))
         _LIB = handle
     return _LIB
 

@@ -50,6 +50,15 @@ def vertical_budget(n, vertical, vertical_sqrt):
     return vertical
 
 
+def forward_pool(score, p, back=0):
+    """[H, n] -> [H, n] span pooling of key scores (modal_rd/attention.py:70-75): key j takes the largest score among
+    keys j - (p - 1) .. j + back (the row's ends clipped), so the p - 1 keys that continue a high-scoring key (the rest
+    of a copied number or span) and the `back` keys leading up to it rank with it. p < 1 counts as 1."""
+    before = max(p, 1) - 1
+    padded = torch.nn.functional.pad(score[:, None], (before, back), value=-float("inf"))
+    return torch.nn.functional.max_pool1d(padded, before + back + 1, stride=1)[:, 0]
+
+
 def route_positions(n, r, mode, sink, window, device):
     """Absolute positions of the route queries (modal_rd/attention.py:150-155)."""
     if mode == "spread":
@@ -172,10 +181,11 @@ class RDAttention(nn.Module):
             none = torch.full((self.num_heads, 1, 1), -1, dtype=torch.int32, device=q.device)
             return bigger_bird_flash(q[0], k[0], v[0], none, front=0, window=n, num_heads=self.num_heads,
                                      kv_groups=self.groups, scale=self.scaling)[None]
-        if t == 1 and q.dtype == torch.bfloat16:
+        if t == 1 and q.dtype == torch.bfloat16 and self.head_dim in (64, 128) and self.groups in (1, 2, 4, 8):
             from .kv_int8 import decode_bf16
             return decode_bf16(q[0, :, 0], k[0], v[0], self.scaling)[None, :, None]
-        # 1 < t < n: every query attends every cached key (the reference's non-causal SDPA), one launch
+        # 1 < t < n, or a decode step the decode kernel does not take (head_dim 32, fp16, other group counts): every
+        # query attends every cached key (the reference's non-causal SDPA), one launch
         return exact_attention(q[0], k[0], v[0], num_heads=self.num_heads, kv_groups=self.groups,
                                scale=self.scaling)[None]
 
@@ -266,10 +276,7 @@ class RDAttention(nn.Module):
         routed = routed.view(hk, g, n).any(1)
         score = self.evict_scores(q, k) if self.evict_obs else pooled.view(hk, g, n).amax(1)
         if self.evict_pool > 1 or self.evict_pool_back:
-            # each key takes the best score among the `pool - 1` keys before it and the `pool_back` keys after it
-            before, after = max(self.evict_pool, 1) - 1, self.evict_pool_back
-            padded = torch.nn.functional.pad(score[:, None], (before, after), value=-float("inf"))
-            score = torch.nn.functional.max_pool1d(padded, before + after + 1, stride=1)[:, 0]
+            score = forward_pool(score, self.evict_pool, self.evict_pool_back)
         recent = min(max(self.window, self.evict_window), n - self.sink)
         priority = routed.float() * 2 + score  # routed columns first, then by score (>= 0 on [sink, n - recent))
         slots = g * routes.shape[-1]

@@ -83,7 +83,7 @@ def bigger_bird_flash(q, k, v, indices, *, front=64, window=256, token_mask=None
     re = t if row_end is None else int(row_end)
     L = _lib.lib()
     ws_bytes = L.bb_sparse_flash_workspace(bh, t, n, d, num_heads, kv_groups, min(front, n), window, route_k,
-                                           indices.shape[1], re, int(vt is not None))
+                                           indices.shape[1], re, int(vt is not None), int(mask is not None))
     ws = _lib.workspace(ws_bytes, q.device) if ws_bytes else None
     _lib.check(L.bb_sparse_flash(
         _lib.ptr(q), _lib.i64s(*q.stride()), _lib.ptr(k), _lib.i64s(*k.stride()), _lib.ptr(v), _lib.i64s(*v.stride()),

@@ -87,7 +87,29 @@ class _LayerPlan:
         self.qkv_w = None
         if all(_plain_linear(p) for p in projs) and len({p.weight.dtype for p in projs}) == 1:
             with torch.inference_mode(False), torch.no_grad():
-                self.qkv_w = torch.cat([p.weight for p in projs], 0)
+                self.qkv_w = _fuse_rows([p.weight for p in projs])
+
+
+def _fuse_rows(weights):
+    """One [sum of rows, cols] matrix whose row blocks are the given weights, without a second copy of them: the
+    weights are moved into the fused buffer once (each parameter then holds a view of its block, same values), and
+    weights that already are adjacent blocks of one buffer are viewed as it directly."""
+    first = weights[0]
+    rows, cols = sum(w.shape[0] for w in weights), first.shape[1]
+    adjacent = all(w.is_contiguous() and w.shape[1] == cols for w in weights)
+    offset = first.storage_offset()
+    for w in weights:
+        adjacent = adjacent and w.untyped_storage().data_ptr() == first.untyped_storage().data_ptr()
+        adjacent = adjacent and w.storage_offset() == offset
+        offset += w.numel()
+    if adjacent:
+        return first.new_empty(0).set_(first.untyped_storage(), first.storage_offset(), (rows, cols), (cols, 1))
+    fused = torch.cat([w.detach() for w in weights], 0)
+    start = 0
+    for w in weights:
+        w.data = fused[start:start + w.shape[0]]
+        start += w.shape[0]
+    return fused
 
 
 class StaticDecoder:

@@ -317,8 +317,11 @@ class Int8KVLayer(DynamicLayer):
         self.n = end
         wants_handle = isinstance(cache_kwargs, dict) and cache_kwargs.get("bb_attend", False)
         kr, vr = self._token_major(key_states), self._token_major(value_states)
+        # the fused decode reads the new rows as 16-byte units: contiguous head_dim, 16-byte aligned rows and a head
+        # stride of whole units (bb_decode_append's checks); anything else is quantised here
         if (self.fused and wants_handle and t == 1 and kr.dtype == torch.bfloat16 and vr.dtype == torch.bfloat16
-                and kr.stride(-1) == 1 and vr.stride(-1) == 1):
+                and all(x[0].stride(-1) == 1 and x[0].stride(0) % 8 == 0 and x[0].data_ptr() % 16 == 0
+                        for x in (kr, vr))):
             # the row is quantised by the decode kernel when the handle is attended (or by _flush before any other
             # use of the cache)
             self._pending = (kr[0], vr[0], start)

@@ -118,7 +118,15 @@ int decode_scratch(void** out) {
 
 extern "C" {
 
-int bb_version(void) { return 100; }
+int bb_version(void) { return BB_ABI_VERSION; }
+
+// Per-device set-up done ahead of time: the device address of bb_decode_noalloc's static scratch, so that the entry
+// point's first call on this device (which may sit inside a HIP graph capture) does no symbol lookup.
+int bb_init(void) {
+  g_err[0] = 0;
+  void* addr = nullptr;
+  return decode_scratch(&addr);
+}
 
 const char* bb_last_error(void) { return g_err; }
 
@@ -126,18 +134,26 @@ int64_t bb_transpose_v_cols(int64_t N) { return cdiv(N > 0 ? N : 1, 64) * 64; }
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Routed tiles are pre-gathered for the pipelined kernel (head_dim 128, query heads per KV head a multiple of 4).
-static bool routed_tiles_wanted(int D, int kv_groups, int route_k) { return route_k > 0 && D == 128 && kv_groups % 4 == 0; }
+// Routed tiles are pre-gathered for the pipelined kernel (head_dim 128, query heads per KV head a multiple of 4, no
+// token mask) when the route list has a single group. With several groups (vertical_scope) most groups are empty and
+// the tiles of every group would cost BH x groups x 32 KB per 64 slots, so the kernel gathers the batches it uses
+// itself. K rows of 4 GiB or more per KV head also leave the pipelined kernel; the reservation does not see the row
+// stride and is made anyway (it is small next to such K).
+static bool routed_tiles_wanted(int D, int kv_groups, int route_k, int n_groups, bool key_mask) {
+  return route_k > 0 && n_groups == 1 && !key_mask && D == 128 && kv_groups % 4 == 0 && flash_pipe_enabled();
+}
 
 size_t bb_sparse_flash_workspace(int BH, int64_t T, int64_t N, int D, int num_heads, int kv_groups, int64_t front,
-                                 int64_t window, int route_k, int n_groups, int64_t row_end, int have_vt) {
+                                 int64_t window, int route_k, int n_groups, int64_t row_end, int have_vt,
+                                 int has_key_mask) {
   if (BH <= 0 || T <= 0 || N <= 0 || kv_groups <= 0 || BH % kv_groups) return 0;
   if (window >= N) route_k = 0;
   if (row_end <= 0 || row_end > T) row_end = T;
   FlashSchedule s = flash_schedule(BH, T, N, num_heads, kv_groups, front, window, route_k, row_end);
   size_t bytes = 0;
   if (!have_vt) bytes += align256((size_t)(BH / kv_groups) * D * bb_transpose_v_cols(N) * 2);
-  if (routed_tiles_wanted(D, kv_groups, route_k)) bytes += align256(bb::route_tiles_bytes(BH, n_groups, route_k));
+  if (routed_tiles_wanted(D, kv_groups, route_k, n_groups, has_key_mask != 0))
+    bytes += align256(bb::route_tiles_bytes(BH, n_groups, route_k));
   if (s.split) bytes += (size_t)s.n_chunks * BH * T * (size_t)(D + 2) * sizeof(float);
   return bytes;
 }
@@ -222,7 +238,7 @@ static int sparse_flash_impl(const void* q, const int64_t* sq, const void* k, co
   p.c = (float)((double)scale * 1.4426950408889634);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const size_t need = bb_sparse_flash_workspace(BH, T, N, D, num_heads, kv_groups, front, window, route_k, p.n_groups,
-                                                row_end, vt != nullptr);
+                                                row_end, vt != nullptr, key_mask != nullptr);
   if (need && (!ws || ws_bytes < need)) return fail("workspace of %zu bytes required", need);
   char* wsp = static_cast<char*>(ws);
   if (vt) {
@@ -236,7 +252,7 @@ static int sparse_flash_impl(const void* q, const int64_t* sq, const void* k, co
     p.vt = vt_ws;
   }
   const bool pipe = flash_pipe_enabled() && s.hpw == 4 && bb::flash_pipe_supported(p, D);
-  if (routed_tiles_wanted(D, kv_groups, route_k)) {
+  if (routed_tiles_wanted(D, kv_groups, route_k, p.n_groups, key_mask != nullptr)) {
     uint16_t* rt = reinterpret_cast<uint16_t*>(wsp);
     wsp += align256(bb::route_tiles_bytes(BH, p.n_groups, route_k));
     if (pipe) {
@@ -268,7 +284,7 @@ int bb_sparse_flash(const void* q, const int64_t* sq, const void* k, const int64
 }
 
 size_t bb_exact_attention_workspace(int BH, int64_t T, int64_t N, int D, int num_heads, int kv_groups, int have_vt) {
-  return bb_sparse_flash_workspace(BH, T, N, D, num_heads, kv_groups, 0, N, 0, 1, T, have_vt);
+  return bb_sparse_flash_workspace(BH, T, N, D, num_heads, kv_groups, 0, N, 0, 1, T, have_vt, 0);
 }
 
 int bb_exact_attention(const void* q, const int64_t* sq, const void* k, const int64_t* sk, const void* v,

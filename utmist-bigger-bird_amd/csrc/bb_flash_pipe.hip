@@ -13,8 +13,9 @@
 //     resource bounds;
 //   * the exponent offset moves only when a probability would exceed 2^8 (O rescales stay rare); tiles without masked
 //     elements skip the per-tile maximum unless the row sum says the offset must move;
-//   * routed keys differ per head: after the window loop the two waves of a head gather its routed K rows and V rows
-//     into that head's LDS tile.
+//   * routed keys differ per head: after the window loop the two waves of a head stream its routed K / V^T tiles into
+//     that head's LDS tile, pre-gathered per 64-slot batch by route_tiles_kernel (one route group), or gather the
+//     batch's K rows and V rows themselves (several route groups: the GATHER instantiation).
 #include "bb_common.h"
 #include "bb_flash_tiles.h"
 #include "bb_internal.h"
@@ -380,7 +381,9 @@ BB_DEV PipeItem pipe_item(const FlashParams& p, int bid, int hd, int rbk, int li
   return it;
 }
 
-template <bool F16>
+// GATHER: the routed phase gathers the rows of its batches itself (route lists with several groups, where no tiles
+// are pre-gathered); a separate instantiation, so that the common kernel's register allocation is not affected.
+template <bool F16, bool GATHER>
 __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) {
   __shared__ __attribute__((aligned(1024))) uint16_t smem[PLDS];
   __shared__ __attribute__((aligned(16))) int32_t route_keys[PHEADS][kRouteCache];
@@ -600,9 +603,40 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
         for (int bi = 0; bi < nb; ++bi) {
           const bool work = bi < my_nb;
           const int32_t* keys = route_keys[hd] + kTileKeys * bi;
-          if (work) {
-            load_tile(b0 + bi, kl, 0);
-            load_tile(b0 + bi, vt, 1);
+          if constexpr (!GATHER) {
+            if (work) {
+              load_tile(b0 + bi, kl, 0);
+              load_tile(b0 + bi, vt, 1);
+            }
+          } else if (work) {
+            // No pre-gathered tiles (several route groups): the head's two waves gather the batch's rows here. K rows
+            // go straight to LDS (empty slots read row 0, masked out); V rows are transposed through registers in
+            // units of 4 keys x 8 d into the permuted V^T layout. Only batches holding a usable key are gathered.
+            const uint16_t* kb = p.k + (int64_t)it.kvbh * p.sk0;
+            const uint16_t* vb = p.v + (int64_t)it.kvbh * p.sv0;
+            for (int b = rbk; b < PBLK; b += 2) {
+              const int e = b * 512 + 8 * lane;
+              const int row = e / PD, chk = ((e % PD) / 8) ^ (row & (PD / 8 - 1));
+              const int32_t kr = keys[row];
+              lds_dma16(kb + (int64_t)(kr >= 0 ? kr : 0) * p.sk1 + 8 * chk, kl + b * 512);
+            }
+            for (int u = lane + 64 * rbk; u < (kTileKeys / 4) * (PD / 8); u += 128) {
+              const int bq = u % (PD / 8), a4 = u / (PD / 8);
+              u32x4_t vr[4];
+#pragma unroll
+              for (int s2 = 0; s2 < 4; ++s2) {
+                const int32_t kr = keys[4 * a4 + s2];
+                vr[s2] = kr >= 0 ? ld16(vb + (int64_t)kr * p.sv1 + 8 * bq) : u32x4_t{0, 0, 0, 0};
+              }
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+                const uint32_t lo = __builtin_amdgcn_perm(vr[1][e >> 1], vr[0][e >> 1], sel);
+                const uint32_t hi = __builtin_amdgcn_perm(vr[3][e >> 1], vr[2][e >> 1], sel);
+                *reinterpret_cast<u32x2_t*>(vt + vt_off(8 * bq + e, 2 * (a4 >> 2) + (a4 & 1)) + 4 * ((a4 >> 1) & 1)) =
+                    u32x2_t{lo, hi};
+              }
+            }
           }
           vm_wait_tile(false);
           __syncthreads();
@@ -751,8 +785,14 @@ hipError_t launch_flash_pipe(const FlashParams& p, hipStream_t stream) {
   const int64_t items = (int64_t)p.n_kvbh * p.head_splits * p.row_tiles * p.n_chunks;
   if (items <= 0) return hipSuccess;
   if (items > 0x7fffffff) return hipErrorInvalidValue;
-  if (p.f16) hipLaunchKernelGGL(flash_ping_kernel<true>, dim3((unsigned)items), dim3(64 * PNW), 0, stream, p);
-  else hipLaunchKernelGGL(flash_ping_kernel<false>, dim3((unsigned)items), dim3(64 * PNW), 0, stream, p);
+  const dim3 grid((unsigned)items), block(64 * PNW);
+  if (p.route_k > 0 && !p.rtiles) {
+    if (p.f16) hipLaunchKernelGGL((flash_ping_kernel<true, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((flash_ping_kernel<false, true>), grid, block, 0, stream, p);
+  } else {
+    if (p.f16) hipLaunchKernelGGL((flash_ping_kernel<true, false>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((flash_ping_kernel<false, false>), grid, block, 0, stream, p);
+  }
   return hipGetLastError();
 }
 
