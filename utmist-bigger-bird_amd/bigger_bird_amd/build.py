@@ -26,7 +26,8 @@ FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{INCLUDE}",
 ]
-SOURCES = ["bb_flash.hip", "bb_flash_pipe.hip", "bb_routes.hip", "bb_int8.hip", "bb_decode.hip", "bb_capi.cpp"]
+SOURCES = ["bb_flash.hip", "bb_flash_pipe.hip", "bb_routes.hip", "bb_int8.hip", "bb_decode.hip", "bb_probe.hip",
+           "bb_capi.cpp"]
 
 
 def _compile(src: Path, obj: Path) -> None:

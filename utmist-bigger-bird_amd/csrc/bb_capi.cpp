@@ -704,6 +704,14 @@ int bb_argmax(const void* x, int64_t n, int dtype, int64_t* out, void* stream) {
   return hip_status(bb::launch_argmax(x, n, dtype, aligned(x, 16), out, static_cast<hipStream_t>(stream)), "bb_argmax");
 }
 
+int bb_stream_read(const void* buf, size_t bytes, uint32_t* sink, int workgroups, void* stream) {
+  g_err[0] = 0;
+  if (!buf || !sink) return fail("stream_read: null argument");
+  if (bytes % 16 || !aligned(buf, 16) || workgroups <= 0) return fail("stream_read: 16-byte aligned whole units");
+  return hip_status(bb::launch_stream_read(buf, (int64_t)bytes, sink, workgroups, static_cast<hipStream_t>(stream)),
+                    "bb_stream_read");
+}
+
 int bb_rope_inplace(void* x, const int64_t* sx, int B, int Hh, int64_t T, int D, const void* cos, const void* sin,
                     const int64_t* sc, int is_f16, void* stream) {
   g_err[0] = 0;

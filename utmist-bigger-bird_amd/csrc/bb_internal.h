@@ -49,7 +49,7 @@ struct RoutesParams {
   int scores_reference_order;  // 1: every score by the reference-order chain (no MFMA), for cross-checks
   float scaling;
   uint16_t* scores;     // [B*Hkv][G*r][n] bf16 workspace
-  uint32_t* rowmax;     // [B*H*r] ordered-float keys
+  uint32_t* rowmax;     // [B*H*r] row maxima (fp32 bits)
   uint64_t* rowsum;     // [B*H*r] fixed point 2^40
   uint64_t* pooled;     // [B*H][pstride] fixed point 2^40
   int32_t* out_idx;     // [B*H][budget]
@@ -165,5 +165,8 @@ hipError_t launch_f32_keys(const float* vals, int64_t sv0, int rows, int64_t n, 
 // RoPE in place (HF apply_rotary_pos_emb arithmetic in bf16, or fp16 when f16).
 hipError_t launch_rope(uint16_t* x, int64_t sx0, int64_t sx1, int64_t sx2, int B, int Hh, int64_t T, int D,
                        const uint16_t* cos, const uint16_t* sin, int64_t sc0, int64_t sc1, int f16, hipStream_t stream);
+
+// HBM read ceiling probe (bb_probe.hip): XOR of `bytes` (a multiple of 16) of buf, one word per workgroup to sink.
+hipError_t launch_stream_read(const void* buf, int64_t bytes, uint32_t* sink, int workgroups, hipStream_t stream);
 
 }  // namespace bb

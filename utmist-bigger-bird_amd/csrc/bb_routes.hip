@@ -37,7 +37,7 @@ namespace {
 constexpr int kScoreKeys = 32;    // keys per scores_kernel block (8 key groups of 4)
 constexpr int kScoreIters = 16;   // key blocks per scores_kernel workgroup
 constexpr int kSumKeys = 1024;    // keys per rowsum_kernel workgroup
-constexpr int kPoolKeys = 256;    // keys per pooled_kernel workgroup
+constexpr int kPoolKeys = 512;    // keys per pooled_kernel workgroup (2 per thread)
 constexpr int kMaxRows = 256;     // G * r handled by one scores workgroup (rows beyond this use more row blocks)
 constexpr float kFixOne = 1099511627776.0f;  // 2^40
 
@@ -184,24 +184,50 @@ __global__ __launch_bounds__(256) void scores_kernel(RoutesParams p, RouteGeom g
 }
 
 // MFMA scores with exact fix-up (head_dim 128). The bf16 score of every (route row, key) must be the one the
-// reference order above produces. Both that order and the MFMA path sum the same 128 exact bf16 products in fp32:
-//   * reference order: at most 21 roundings on any path (16 in an even or odd chain, one for even + odd, four for the
-//     block sum), so its error is at most 21 u sum|q_d k_d| (u = 2^-24);
-//   * MFMA path: each of the eight 16-element slices of d is its own MFMA with a zero accumulator, so a slice's
-//     error is at most 16 x 2^-23 x max|p| <= 32 u sum_slice|p| (16 products aligned to the largest and truncated,
-//     then one rounding), and the eight partials are added in fp32 (7 u): at most 39 u sum|q_d k_d| in all.
-// sum|q_d k_d| comes from a second, accumulating MFMA over |q| and |k| (sign bits cleared; its relative error,
-// below 2^-16, only scales the slack). With B = kScoreSlack sum|q_d k_d| + 2^-100 (kScoreSlack >= 60 u): if s - B
-// and s + B round to the same bf16 value, so does the exact reference-order score, and that value is taken;
-// otherwise (scores near a rounding boundary, or tiny) the score is recomputed in the reference order.
+// reference order above produces. Both that order and the MFMA path sum the same 128 exact bf16 products
+// p_d = q_d k_d in fp32, and each result's distance from the exact sum is bounded per product (u = 2^-24; every
+// rounding of a partial sum x errs by at most u |x|, and |x| <= the sum of |p_d| over the products in it):
+//   * reference order, d = 32 c + 2 t + parity: the even / odd chain of block c rounds at its steps t' = 1..15 (step 0
+//     adds to zero exactly), then once for even + odd, then at the block sums c' = 1..3. Product d passes through
+//     (16 - max(t, 1)) + 1 + (4 - max(c, 1)) roundings (19 at most, 11.7 on average against the 21 of a uniform
+//     bound).
+//   * MFMA path: slice s (d = 16 s .. 16 s + 15) is one MFMA with a zero accumulator, its 16 products aligned to the
+//     largest one and truncated below 2^-23 of it (the error model measured on the hardware), then rounded: at most
+//     32 u M_s + 2 u sum_s|p|, with M_s = max over the slice of |p_d| <= max|q_d| max|k_d|; the eight slice partials
+//     are then added in order, so slice s passes through 8 - max(s, 1) more roundings.
+// So |reference - MFMA| <= u (sum_d c_d |q_d| |k_d| + 32 sum_s max_s|q| max_s|k|) with
+// c_d = (16 - max(t, 1)) + 1 + (4 - max(c, 1)) + (10 - max(s, 1)). One accumulating MFMA chain computes that bound
+// per score: |K| against the weighted row c_d |q_d| (rounded up to bf16), then one more MFMA of the per-slice maxima
+// of |K| against 32 x the per-slice maxima of |Q|. The bound's own MFMA rounding (all terms are non-negative; below
+// 2^-16 relative), the fp32 evaluation of the bound and second-order terms are covered by the factor 1 + 2^-10 in
+// kScoreSlack, underflow by the absolute 2^-100. If s - B and s + B round to the same bf16 value, so does the
+// reference-order score (it is an fp32 value in [s - B, s + B]), and that value is taken; otherwise (a score near a
+// rounding boundary, or tiny) the score is recomputed in the reference order.
 //
 // Workgroup: one KV head, up to 256 route rows (G r), kScoreIters blocks of 32 keys; 8 waves, wave w owns rows
-// 32w..32w+31 (one MFMA block, Q^T operands in registers; two waves per SIMD hide each other's MFMA, LDS and
-// fix-up latencies). Per key block S^T = K Q^T (eight slice partials) and |K| |Q|^T run on 16 MFMAs with K from LDS.
-// Scores go through an LDS tile per wave so that fix-ups land before one coalesced store.
-constexpr float kScoreSlack = 4.0e-6f;  // 67 u >= (21 + 39) u (1 + 2^-16)
-constexpr int kMsRowPitch = 136;        // bf16 elements per staged Q row (272 bytes: conflict-free row reads)
-constexpr int kMsKPitch = 132;          // floats per fp32 K row (fix-up reads)
+// 32w..32w+31 (one MFMA block, Q^T operands in registers; two waves per SIMD hide each other's MFMA and LDS
+// latencies). Per key block S^T = K Q^T (eight slice partials) and the bound run on 17 MFMAs with K from LDS. The
+// flagged scores of all eight waves go to one workgroup list, which every thread then works through (about 2% of
+// the scores: a few wave-iterations per block for the whole workgroup, instead of one per wave). Scores go through an
+// LDS tile per wave so that fix-ups land before one coalesced store, made at the start of the next block.
+constexpr float kScoreSlack = 5.9662e-8f;  // u (1 + 2^-10)
+constexpr int kMsRowPitch = 136;           // bf16 elements per staged Q row (272 bytes: conflict-free row reads)
+constexpr int kMsTilePitch = 40;           // bf16 per score-tile row (80 bytes: conflict-free 8-byte row writes)
+
+// Weight c_d of the certification bound for element d of a 128-element dot product (see above).
+BB_DEV int bound_weight(int d) {
+  const int c = d >> 5, t = (d & 31) >> 1, s = d >> 4;
+  return (16 - (t > 1 ? t : 1)) + 1 + (4 - (c > 1 ? c : 1)) + (10 - (s > 1 ? s : 1));
+}
+
+// Magnitude maximum of the eight bf16 values of a fragment (abs bit patterns order as unsigned integers).
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+BB_DEV uint32_t abs_max8(u32x4_t a) {
+  const u16x2_t m = __builtin_elementwise_max(
+      __builtin_elementwise_max(__builtin_bit_cast(u16x2_t, a[0]), __builtin_bit_cast(u16x2_t, a[1])),
+      __builtin_elementwise_max(__builtin_bit_cast(u16x2_t, a[2]), __builtin_bit_cast(u16x2_t, a[3])));
+  return m[0] > m[1] ? m[0] : m[1];
+}
 
 constexpr int kMsWaves = 8;
 
@@ -211,9 +237,10 @@ __global__ __launch_bounds__(64 * kMsWaves) void scores_mfma_kernel(RoutesParams
   static_assert(D == 128, "MFMA scores are built for head_dim 128");
   __shared__ __attribute__((aligned(16))) uint16_t qs[kMaxRows][kMsRowPitch];  // Q rows (bf16)
   __shared__ __attribute__((aligned(16))) uint16_t kt[kScoreKeys][D];          // K block, chunk c of key j at c ^ (j % 16)
-  __shared__ __attribute__((aligned(16))) float kf[kScoreKeys][kMsKPitch];     // the same block in fp32
-  __shared__ __attribute__((aligned(16))) uint16_t st[kMsWaves][32][kScoreKeys];  // per-wave score tile (bf16)
-  __shared__ uint32_t flist[kMsWaves][32 * kScoreKeys];                          // per-wave fix-up list: lane << 4 | r
+  __shared__ __attribute__((aligned(16))) float kf[kScoreKeys][D];             // the same block in fp32 (same slots)
+  __shared__ __attribute__((aligned(16))) uint16_t st[kMsWaves][32][kMsTilePitch];  // per-wave score tile (bf16)
+  __shared__ uint16_t flist[kMsWaves * 32 * kScoreKeys];                       // fix-ups: wave << 10 | lane << 4 | r
+  __shared__ uint32_t fcount;                                                  // entries of flist
   __shared__ uint32_t rmax_fix[kMaxRows];                                      // ordered-float max of fixed-up x
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 31, h = lane >> 5;
@@ -234,6 +261,7 @@ __global__ __launch_bounds__(64 * kMsWaves) void scores_mfma_kernel(RoutesParams
     *reinterpret_cast<u32x4_t*>(&qs[row][8 * c8]) = v;
   }
   for (int e = tid; e < kMaxRows; e += 64 * kMsWaves) rmax_fix[e] = 0u;  // ordered key below every float
+  if (tid == 0) fcount = 0u;
   __syncthreads();
 
   // B operands (Q^T of row 32 wave + li) and the causal limit
@@ -242,12 +270,45 @@ __global__ __launch_bounds__(64 * kMsWaves) void scores_mfma_kernel(RoutesParams
   u32x4_t qf[D / 16];
 #pragma unroll
   for (int dk = 0; dk < D / 16; ++dk) qf[dk] = *reinterpret_cast<const u32x4_t*>(&qs[myrow][16 * dk + 8 * h]);
+  // bound operands: c_d |q_d| rounded up to bf16 (this lane holds d = 16 dk + 8 h + e), and 32 x the per-slice
+  // maxima of |q| (positions 0..7 of the lane with h = 0, zeros at positions 8..15)
+  u32x4_t qw[D / 16];
+  u32x4_t mq32 = {0, 0, 0, 0};
+#pragma unroll
+  for (int dk = 0; dk < D / 16; ++dk) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      uint32_t packed = 0;
+#pragma unroll
+      for (int hw = 0; hw < 2; ++hw) {
+        const float a = __uint_as_float(((qf[dk][w] >> (16 * hw)) & 0x7fffu) << 16);
+        const float v = a * (float)bound_weight(16 * dk + 8 * h + 2 * w + hw);  // exact: <= 13 significant bits
+        packed |= ((__float_as_uint(v) + 0xffffu) >> 16) << (16 * hw);          // rounded up to bf16
+      }
+      qw[dk][w] = packed;
+    }
+    const uint32_t half = abs_max8(qf[dk] & u32x4_t{0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu});
+    const auto sw = __builtin_amdgcn_permlane32_swap(half, half, false, false);
+    const uint32_t mq = sw[0] > sw[1] ? sw[0] : sw[1];                 // max |q| over slice dk of row li
+    const uint32_t m32 = __float_as_uint(__uint_as_float(mq << 16) * 32.0f) >> 16;  // exact
+    if (h == 0) mq32[dk >> 1] |= m32 << (16 * (dk & 1));
+  }
   const int64_t qlim = myrow < nrows ? p.qpos[(row0 + myrow) % p.r] : -1;
   float rmax = -__builtin_huge_valf();
   const uint16_t* kbase = p.k + (int64_t)bkv * p.sk0;
   uint16_t* srow_base = p.scores + (int64_t)bkv * g.rows * g.ns;
-  uint16_t (*tile)[kScoreKeys] = st[wave];
-  uint32_t* fl = flist[wave];
+  uint16_t (*tile)[kMsTilePitch] = st[wave];
+  // tile -> scores for the block at key jb: 32 rows x 32 keys, one 16-byte chunk (8 keys) per lane and step
+  auto store_tile = [&](int64_t jb) {
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const int e = 64 * s2 + lane, lrow = e >> 2, c = e & 3;
+      const int row = 32 * wave + lrow;
+      const int64_t j = jb + 8 * c;
+      if (row < nrows && j + 8 <= g.ns)
+        st16(srow_base + (int64_t)(row0 + row) * g.ns + j, *reinterpret_cast<const u32x4_t*>(&tile[lrow][8 * c]));
+    }
+  };
 
   // K blocks: thread (key tid / 16, chunk tid % 16) holds 16 bytes; the next block's load is in flight while the
   // current one is processed
@@ -257,49 +318,62 @@ __global__ __launch_bounds__(64 * kMsWaves) void scores_mfma_kernel(RoutesParams
     return j < p.n ? ld16(kbase + j * p.sk1 + 8 * schunk) : u32x4_t{0, 0, 0, 0};
   };
   u32x4_t knext = kload(0);
+  int64_t jlast = -1;  // key of the block whose tile is still to be stored
   for (int it = 0; it < kScoreIters; ++it) {
     const int64_t j0 = ((int64_t)kchunk * kScoreIters + it) * kScoreKeys;
     if (j0 >= p.n) break;
-    __syncthreads();  // the previous K block is no longer read
-    {  // stage the K block, bf16 for the MFMA and fp32 for the fix-ups
-      const int key = skey, c = schunk;
+    __syncthreads();  // the previous block's K and fix-up list are no longer read, and its fix-ups have landed
+    if (jlast >= 0) store_tile(jlast);
+    jlast = j0;
+    if (tid == 0) fcount = 0u;
+    {  // stage the K block: bf16 for the MFMA fragments, fp32 for the fix-ups (chunk c of key j in slot c ^ (j % 16))
+      const int slot = 8 * (schunk ^ (skey & 15));
       const u32x4_t v = knext;
-      *reinterpret_cast<u32x4_t*>(&kt[key][8 * (c ^ (key & 15))]) = v;
-      *reinterpret_cast<f32x4_t*>(&kf[key][8 * c]) = f32x4_t{
+      *reinterpret_cast<u32x4_t*>(&kt[skey][slot]) = v;
+      *reinterpret_cast<f32x4_t*>(&kf[skey][slot]) = f32x4_t{
           __uint_as_float(v[0] << 16), __uint_as_float(v[0] & 0xffff0000u), __uint_as_float(v[1] << 16),
           __uint_as_float(v[1] & 0xffff0000u)};
-      *reinterpret_cast<f32x4_t*>(&kf[key][8 * c + 4]) = f32x4_t{
+      *reinterpret_cast<f32x4_t*>(&kf[skey][slot + 4]) = f32x4_t{
           __uint_as_float(v[2] << 16), __uint_as_float(v[2] & 0xffff0000u), __uint_as_float(v[3] << 16),
           __uint_as_float(v[3] & 0xffff0000u)};
     }
     __syncthreads();
     if (it + 1 < kScoreIters) knext = kload(it + 1);
 
-    // S^T = K Q^T as eight slice partials (zero accumulators) summed in fp32, and A^T = |K| |Q|^T
+    // S^T = K Q^T as eight slice partials (zero accumulators) summed in fp32, and the bound's sum of c_d |q_d| |k_d|
     // (each partial is added one step later, while the next slice's MFMAs run: two partials live at a time)
     f32x16_t acc = f32x16_t{}, aac = f32x16_t{}, prev = f32x16_t{};
+    uint32_t mk[D / 16];  // max |k| over this lane's half of slice dk (key li)
 #pragma unroll
     for (int dk = 0; dk < D / 16; ++dk) {
       const u32x4_t kv = *reinterpret_cast<const u32x4_t*>(&kt[li][8 * ((2 * dk + h) ^ (li & 15))]);
       const f32x16_t cur = mfma32(as_bf16x8(kv), as_bf16x8(qf[dk]), f32x16_t{});
-      aac = mfma32(as_bf16x8(kv & kAbs), as_bf16x8(qf[dk] & kAbs), aac);
+      const u32x4_t ka = kv & kAbs;
+      aac = mfma32(as_bf16x8(ka), as_bf16x8(qw[dk]), aac);
+      mk[dk] = abs_max8(ka);
       if (dk == 1) acc = prev;
       else if (dk > 1) acc = acc + prev;
       prev = cur;
       __builtin_amdgcn_sched_barrier(0);
     }
     acc = acc + prev;
+    {  // + 32 sum_s max_s|k| max_s|q|: slice maxima of key li (both halves) at positions 0..7 of the h = 0 lane
+      u32x4_t mka = {0, 0, 0, 0};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t x = mk[2 * i] | (mk[2 * i + 1] << 16);
+        const auto sw = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+        const u16x2_t m = __builtin_elementwise_max(__builtin_bit_cast(u16x2_t, sw[0]), __builtin_bit_cast(u16x2_t, sw[1]));
+        mka[i] = h == 0 ? __builtin_bit_cast(uint32_t, m) : 0u;
+      }
+      aac = mfma32(as_bf16x8(mka), as_bf16x8(mq32), aac);
+    }
 
     // certify or flag every score; lane (li, h) holds row li's keys 8 (r / 4) + 4 h + r % 4 of the block
     int64_t lim64 = (qlim < p.n - 1 ? qlim : p.n - 1) - j0;  // live keys: kk <= lim
     const int lim = lim64 < -1 ? -1 : (lim64 > kScoreKeys ? kScoreKeys : (int)lim64);
     const int limh = lim - 4 * h;  // compared with the lane-independent part of kk
-    // fix-up entries are (lane << 4) | r; the zero comes from an instruction the compiler cannot look through, so
-    // the 16 entry values are formed in the loop rather than hoisted out of it (and spilled)
-    uint32_t opaque_zero;
-    asm volatile("s_mov_b32 %0, 0" : "=s"(opaque_zero));
-    const uint32_t ebase = ((uint32_t)lane << 4) + opaque_zero;
-    uint32_t nfix = 0;
+    uint32_t fixbits = 0;  // bit r: score r of this lane needs the fix-up
     uint32_t outw[8];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -318,25 +392,35 @@ __global__ __launch_bounds__(64 * kMsWaves) void scores_mfma_kernel(RoutesParams
       else outw[r >> 1] = out;
       if ((r & 3) == 3)  // keys 8 (r / 4) + 4 h + 0..3 are consecutive: one 8-byte store
         *reinterpret_cast<u32x2_t*>(&tile[li][kk - 3]) = u32x2_t{outw[(r >> 1) - 1], outw[r >> 1]};
-      const bool fix = live && !sure;
-      const uint64_t bal = __builtin_amdgcn_ballot_w64(fix);
-      if (fix) {
-        const uint32_t before = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-        fl[nfix + before] = ebase + (uint32_t)r;
-      }
-      nfix += (uint32_t)__builtin_popcountll(bal);
+      fixbits |= (uint32_t)(live && !sure) << r;
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // this wave's flagged scores go to the workgroup list: one atomic per wave reserves their slots
+    {
+      const uint32_t cnt = __builtin_popcount(fixbits);
+      uint32_t incl = cnt;  // inclusive prefix sum over the wave's lanes
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t t = __shfl_up(incl, off);
+        if (lane >= off) incl += t;
+      }
+      const uint32_t total = __shfl(incl, 63);
+      uint32_t base = 0;
+      if (lane == 0 && total) base = atomicAdd(&fcount, total);
+      base = __shfl(base, 0) + incl - cnt;
+      const uint32_t ebase = ((uint32_t)wave << 10) | ((uint32_t)lane << 4);
+      for (uint32_t b = fixbits; b; b &= b - 1) flist[base++] = (uint16_t)(ebase | (uint32_t)__builtin_ctz(b));
+    }
+    __syncthreads();  // the list is complete
 
-    // exact recomputation of the flagged scores in the reference order
-    for (uint32_t e = lane; e < nfix; e += 64) {
-      const uint32_t ent = fl[e];
-      const int el = (int)(ent >> 4), er = (int)(ent & 15u);
+    // exact recomputation of the flagged scores in the reference order, by every thread of the workgroup
+    const uint32_t nfix = fcount;
+    for (uint32_t e = tid; e < nfix; e += 64 * kMsWaves) {
+      const uint32_t ent = flist[e];
+      const int ew = (int)(ent >> 10), el = (int)((ent >> 4) & 63u), er = (int)(ent & 15u);
       const int lrow = el & 31, kk = 8 * (er >> 2) + 4 * (el >> 5) + (er & 3);
-      const uint16_t* qr = qs[32 * wave + lrow];
+      const uint16_t* qr = qs[32 * ew + lrow];
       const float* kr = kf[kk];
+      const int ksw = kk & 15;  // chunk c of key kk sits at slot c ^ (kk % 16)
       float accx = 0.0f;
 #pragma unroll
       for (int blk = 0; blk < D / 32; ++blk) {
@@ -345,8 +429,8 @@ __global__ __launch_bounds__(64 * kMsWaves) void scores_mfma_kernel(RoutesParams
         for (int c2 = 0; c2 < 4; ++c2) {
           const int c = 4 * blk + c2;  // 8-element chunk of d
           const u32x4_t qv = *reinterpret_cast<const u32x4_t*>(qr + 8 * c);
-          const f32x4_t k0 = *reinterpret_cast<const f32x4_t*>(kr + 8 * c);
-          const f32x4_t k1 = *reinterpret_cast<const f32x4_t*>(kr + 8 * c + 4);
+          const f32x4_t k0 = *reinterpret_cast<const f32x4_t*>(kr + 8 * (c ^ ksw));
+          const f32x4_t k1 = *reinterpret_cast<const f32x4_t*>(kr + 8 * (c ^ ksw) + 4);
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
             const float ke = w < 2 ? k0[2 * w] : k1[2 * w - 4], ko = w < 2 ? k0[2 * w + 1] : k1[2 * w - 3];
@@ -357,25 +441,13 @@ __global__ __launch_bounds__(64 * kMsWaves) void scores_mfma_kernel(RoutesParams
         accx = accx + (ev + od);
       }
       const uint16_t out = f32_to_bf16(accx);
-      tile[lrow][kk] = out;
-      atomicMax(&rmax_fix[32 * wave + lrow], float_to_ordered(bf16_to_f32(out) * p.scaling));
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-    // tile -> scores: 32 rows x 32 keys, one 16-byte chunk (8 keys) per lane and step
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) {
-      const int e = 64 * s2 + lane, lrow = e >> 2, c = e & 3;
-      const int row = 32 * wave + lrow;
-      const int64_t j = j0 + 8 * c;
-      if (row < nrows && j + 8 <= g.ns)
-        st16(srow_base + (int64_t)(row0 + row) * g.ns + j, *reinterpret_cast<const u32x4_t*>(&tile[lrow][8 * c]));
+      st[ew][lrow][kk] = out;
+      atomicMax(&rmax_fix[32 * ew + lrow], float_to_ordered(bf16_to_f32(out) * p.scaling));
     }
   }
-  // row maxima: the two halves of a row's lanes, then the fixed-up scores
+  // the last block's fix-ups, then its tile; row maxima: the two halves of a row's lanes, then the fixed-up scores
   __syncthreads();
+  if (jlast >= 0) store_tile(jlast);
   {
     const float mx = xhalf_max(rmax);
     if (h == 0 && myrow < nrows) {
@@ -396,8 +468,28 @@ __global__ __launch_bounds__(64) void rowmax_kernel(RoutesParams p, RouteGeom g,
   if (lane == 0) p.rowmax[(int64_t)bkv * g.rows + row] = __float_as_uint(mx);
 }
 
+// fix40(det_exp2(y) * scale) as an integer-valued float below 2^41, for y <= 0 (or -inf / NaN) and 0 < scale <= 1,
+// bit for bit: det_exp2's ldexp and fix40's scale by 2^40 fold into one exact ldexp of fl(p scale) (det_exp2(y) scale
+// rounds to fl(p scale) 2^n whenever that is a normal float; otherwise both results truncate to 0), and fix40's
+// floor is one truncation. y <= -100 and NaN give 0 as in det_exp2: clamped to -101, the value stays below 2^-59.
+BB_DEV float fix40_exp2(float y, float scale) {
+  y = fmaxf(y, -101.0f);
+  const float n = rintf(y);
+  const float f = y - n;
+  float q = 1.5252733804059840e-05f;
+  q = fmaf(q, f, 1.5403530393381610e-04f);
+  q = fmaf(q, f, 1.3333558146428443e-03f);
+  q = fmaf(q, f, 9.6181291076284772e-03f);
+  q = fmaf(q, f, 5.5504108664821580e-02f);
+  q = fmaf(q, f, 2.4022650695910071e-01f);
+  q = fmaf(q, f, 6.9314718055994531e-01f);
+  q = fmaf(q, f, 1.0f);
+  return truncf(ldexpf(q * scale, (int)(n + 40.0f)));
+}
+
 // Fixed-point partial row sums: one wave per row (4 rows in flight per workgroup), 16 keys per lane. The rows of a
-// key block may be cut into blockIdx.z slices of g.sum_rows rows, so short sequences still fill the chip.
+// key block may be cut into blockIdx.z slices of g.sum_rows rows, so short sequences still fill the chip. The terms
+// are integers below 2^41, so their sums stay exact in double precision (1024 terms per workgroup row < 2^51).
 __global__ __launch_bounds__(256) void rowsum_kernel(RoutesParams p, RouteGeom g, uint64_t* __restrict__ psum) {
   const int kb = blockIdx.x, bkv = blockIdx.y;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -414,7 +506,7 @@ __global__ __launch_bounds__(256) void rowsum_kernel(RoutesParams p, RouteGeom g
   for (int row = r_begin + wave; row < r_end; row += 4) {
     const float M = __uint_as_float(p.rowmax[(int64_t)bkv * g.rows + row]);
     const uint16_t* src = p.scores + ((int64_t)bkv * g.rows + row) * g.ns + j0;
-    uint64_t acc = 0;
+    double acc = 0.0;
     if (j0 + 16 <= p.n) {
       const u32x4_t a = na, b = nb;
       if (row + 4 < r_end) {
@@ -426,24 +518,32 @@ __global__ __launch_bounds__(256) void rowsum_kernel(RoutesParams p, RouteGeom g
       for (int e = 0; e < 16; ++e) {
         const uint16_t sb = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
         const float x = bf16_to_f32(sb) * p.scaling;
-        acc += fix40(det_exp2((x - M) * kLog2e));
+        acc += (double)fix40_exp2((x - M) * kLog2e, 1.0f);
       }
     } else {
       for (int e = 0; e < 16 && j0 + e < p.n; ++e) {
         const float x = bf16_to_f32(src[e]) * p.scaling;
-        acc += fix40(det_exp2((x - M) * kLog2e));
+        acc += (double)fix40_exp2((x - M) * kLog2e, 1.0f);
       }
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
-    if (lane == 0) psum[((int64_t)bkv * g.n_kb2 + kb) * g.rows + row] = acc;
+    if (lane == 0) psum[((int64_t)bkv * g.n_kb2 + kb) * g.rows + row] = (uint64_t)acc;
   }
 }
 
-// One wave per (KV head, route row): integer partial sums (order-free), then 2^40 / Z.
+// One wave per (KV head, route row): integer partial sums (order-free), then 2^40 / Z. The workgroups of the first G
+// rows of each KV head also clear that query head's top-k histogram and list counters, which the top-k kernels
+// accumulate into.
 __global__ __launch_bounds__(64) void invz_kernel(RoutesParams p, RouteGeom g, const uint64_t* __restrict__ psum,
-                                                 float* __restrict__ invz) {
+                                                 float* __restrict__ invz, uint32_t* __restrict__ top_hist,
+                                                 uint32_t* __restrict__ top_meta) {
   const int row = blockIdx.x, bkv = blockIdx.y, lane = threadIdx.x;
+  if (row < g.G) {
+    const int head = (bkv / p.Hkv) * p.H + (bkv % p.Hkv) * g.G + row;
+    for (int b = lane; b < kTopBins; b += 64) top_hist[(int64_t)head * kTopBins + b] = 0u;
+    if (lane < kTopMetaWords) top_meta[kTopMetaWords * head + lane] = 0u;
+  }
   uint64_t z = 0;
   for (int kb = lane; kb < g.n_kb2; kb += 64) z += psum[((int64_t)bkv * g.n_kb2 + kb) * g.rows + row];
 #pragma unroll
@@ -455,49 +555,50 @@ __global__ __launch_bounds__(64) void invz_kernel(RoutesParams p, RouteGeom g, c
   }
 }
 
-// Pooled fixed-point probability per (query head, key): thread per key, loop over the head's r rows.
-__global__ __launch_bounds__(256) void pooled_kernel(RoutesParams p, RouteGeom g, const float* __restrict__ invz,
-                                                    uint32_t* __restrict__ top_hist, uint32_t* __restrict__ top_meta) {
-  const int64_t j = (int64_t)blockIdx.x * kPoolKeys + threadIdx.x;
+// Pooled fixed-point probability per (query head, key): two consecutive keys per thread (one 4-byte score load per
+// route row, eight rows' loads in flight), the head's r rows in a loop, sums exact in double precision (64 rows x
+// 2^41 < 2^53).
+__global__ __launch_bounds__(256) void pooled_kernel(RoutesParams p, RouteGeom g, const float* __restrict__ invz) {
+  const int64_t j0 = 2 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
   const int head = blockIdx.y;  // over B * H
-  if (blockIdx.x == 0) {  // clear this head's top-k histogram and list counters (the next kernels accumulate)
-    for (int b = threadIdx.x; b < kTopBins; b += kPoolKeys) top_hist[(int64_t)head * kTopBins + b] = 0u;
-    if (threadIdx.x < kTopMetaWords) top_meta[kTopMetaWords * head + threadIdx.x] = 0u;
-  }
-  if (j >= p.n) return;
+  if (j0 >= p.n) return;
   const int batch = head / p.H, hh = head % p.H;
   const int kvh = hh / g.G, hs = hh % g.G;
   const int64_t bkv = (int64_t)batch * p.Hkv + kvh;
-  uint64_t P = 0;
-  const bool eligible = j >= p.sink && j < p.n - p.window;
-  if (eligible) {
-    // eight rows per step: their score loads are in flight together (one row at a time waits on every load)
-    const int64_t ridx0 = bkv * g.rows + (int64_t)hs * p.r;
+  const int64_t lo = p.sink, hi = p.n - p.window;  // eligible keys [lo, hi)
+  double P0 = 0.0, P1 = 0.0;
+  if (j0 + 2 > lo && j0 < hi) {
+    // keys past n read as -inf: score rows end at g.ns, a multiple of 8, and the scorer stores -inf there
+    const uint16_t* src = p.scores + (bkv * g.rows + (int64_t)hs * p.r) * g.ns + j0;
+    const float* mrow = reinterpret_cast<const float*>(p.rowmax) + bkv * g.rows + (int64_t)hs * p.r;
+    const float* zrow = invz + bkv * g.rows + (int64_t)hs * p.r;
     int i = 0;
-    for (; i + 8 <= p.r; i += 8) {
-      uint16_t sb[8];
+    for (; i < p.r; i += 8) {
+      const int nb = p.r - i < 8 ? p.r - i : 8;
+      uint32_t w[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) sb[u] = p.scores[(ridx0 + i + u) * g.ns + j];
+      for (int u = 0; u < 8; ++u) w[u] = u < nb ? *reinterpret_cast<const uint32_t*>(src + (int64_t)(i + u) * g.ns) : 0u;
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const int64_t ridx = ridx0 + i + u;
-        const float x = bf16_to_f32(sb[u]) * p.scaling;
-        const float e = det_exp2((x - __uint_as_float(p.rowmax[ridx])) * kLog2e);
-        const uint64_t pf = fix40(e * invz[ridx]);
-        if (p.pool_max) P = pf > P ? pf : P;
-        else P += pf;
+        if (u >= nb) break;
+        const float M = mrow[i + u], iz = zrow[i + u];
+        const float x0 = bf16_to_f32((uint16_t)(w[u] & 0xffffu)) * p.scaling;
+        const float x1 = bf16_to_f32((uint16_t)(w[u] >> 16)) * p.scaling;
+        const double f0 = (double)fix40_exp2((x0 - M) * kLog2e, iz);
+        const double f1 = (double)fix40_exp2((x1 - M) * kLog2e, iz);
+        if (p.pool_max) {
+          P0 = f0 > P0 ? f0 : P0;
+          P1 = f1 > P1 ? f1 : P1;
+        } else {
+          P0 += f0;
+          P1 += f1;
+        }
       }
     }
-    for (; i < p.r; ++i) {
-      const int64_t ridx = ridx0 + i;
-      const float x = bf16_to_f32(p.scores[ridx * g.ns + j]) * p.scaling;
-      const float e = det_exp2((x - __uint_as_float(p.rowmax[ridx])) * kLog2e);
-      const uint64_t pf = fix40(e * invz[ridx]);
-      if (p.pool_max) P = pf > P ? pf : P;
-      else P += pf;
-    }
   }
-  p.pooled[(int64_t)head * p.n + j] = P;
+  uint64_t* dst = p.pooled + (int64_t)head * p.n + j0;
+  dst[0] = j0 >= lo && j0 < hi ? (uint64_t)P0 : 0ull;
+  if (j0 + 1 < p.n) dst[1] = j0 + 1 >= lo && j0 + 1 < hi ? (uint64_t)P1 : 0ull;
 }
 
 // Eligible range [sink, n - window) of the top-k kernels; n comes from device memory when n_dev is set (decode
@@ -926,9 +1027,10 @@ hipError_t launch_routes_d(RoutesParams& p, const RouteGeom& g, float* pmax, uin
     hipLaunchKernelGGL(scores_kernel<D>, dim3(g.n_kb1, g.row_blocks, nbkv), dim3(256), 0, stream, p, g, pmax);
   hipLaunchKernelGGL(rowmax_kernel, dim3(g.rows, nbkv), dim3(64), 0, stream, p, g, pmax);
   hipLaunchKernelGGL(rowsum_kernel, dim3(g.n_kb2, nbkv, g.sum_splits), dim3(256), 0, stream, p, g, psum);
-  hipLaunchKernelGGL(invz_kernel, dim3(g.rows, nbkv), dim3(64), 0, stream, p, g, psum, invz);
-  hipLaunchKernelGGL(pooled_kernel, dim3((unsigned)((p.n + kPoolKeys - 1) / kPoolKeys), p.B * p.H), dim3(kPoolKeys), 0,
-                     stream, p, g, invz, tw.hist, reinterpret_cast<uint32_t*>(tw.meta));
+  hipLaunchKernelGGL(invz_kernel, dim3(g.rows, nbkv), dim3(64), 0, stream, p, g, psum, invz, tw.hist,
+                     reinterpret_cast<uint32_t*>(tw.meta));
+  hipLaunchKernelGGL(pooled_kernel, dim3((unsigned)((p.n + kPoolKeys - 1) / kPoolKeys), p.B * p.H), dim3(256), 0,
+                     stream, p, g, invz);
   if (p.budget > 0) {
     int64_t lo = p.sink < p.n ? (p.sink > 0 ? p.sink : 0) : p.n, hi = p.n - p.window < p.n ? p.n - p.window : p.n;
     const int64_t cnt = hi > lo ? hi - lo : 0;
