@@ -15,8 +15,10 @@ Printed JSON (one line): value = ms per layer (lower is better); effective TFLOP
 HIP events around its launches on the stream it runs on; `cpu_baseline` = the CPU restatement of the reference's
 PyTorch path (oracle.routes_reference_order + oracle.flash_ref) timed on a bounded sample and scaled to a layer.
 Also reported, next to the headline: `tail_roofline` (the exact 256-row tail, TFLOP/s and HBM GB/s), `decode`
-(INT8-KV decode: microseconds per step and HBM GB/s against 8 TB/s) and `short_arm`
-(B=4 at T=32768: sparse prefill against dense causal SDPA on the same inputs).
+(INT8-KV decode: microseconds per step and HBM GB/s against 8 TB/s and against
+`hbm_read_ceiling`, the rate of a plain 16-byte streaming read over 4 GiB measured in the same run) and `short_arm`
+(B=4 at T=32768: sparse prefill, with its stage split, against dense causal SDPA on the same
+inputs).
 """
 import argparse
 import json
@@ -72,14 +74,16 @@ def staged_prefill(attn, q, k, v, ev):
     order; the output is checked bit-identical to sparse_prefill once before timing)."""
     import torch
     from bigger_bird_amd import bigger_bird_flash, transpose_v
+    from bigger_bird_amd.attention import _flat_heads
 
     n = k.shape[-2]
-    bh = attn.num_heads
+    bsz = q.shape[0]
+    bh = bsz * attn.num_heads
     kw = dict(num_heads=attn.num_heads, kv_groups=attn.groups, scale=attn.scaling)
     ev["routes"][0].record()
     idx = attn.routes(q, k)
     ev["routes"][1].record()
-    Q, K, V = q[0], k[0], v[0]
+    Q, K, V = _flat_heads(q), _flat_heads(k), _flat_heads(v)  # B > 1: one batch of B * H heads, as sparse_prefill
     ev["transpose_v"][0].record()
     vt = transpose_v(V)
     ev["transpose_v"][1].record()
@@ -93,7 +97,34 @@ def staged_prefill(attn, q, k, v, ev):
         ev["tail"][0].record()
         bigger_bird_flash(Q[:, n - r:], K, V, none, front=0, window=n, vt=vt, out=out[:, n - r:], **kw)
         ev["tail"][1].record()
-    return out[None], idx
+    return out.unflatten(0, (bsz, attn.num_heads)), idx if bsz == 1 else idx.view(bsz, attn.num_heads, -1)
+
+
+def hbm_read_ceiling(dev, gib=4, workgroups=16384, reps=10):
+    """HBM read rate of a plain 16-byte streaming read (bb_stream_read) over `gib` GiB, far past the 256 MB Infinity
+    Cache: the ceiling the decode kernels are reported against next to the published 8 TB/s. Best of `reps`."""
+    import torch
+    from bigger_bird_amd import _lib
+
+    nbytes = gib << 30
+    buf = torch.ones(nbytes // 4, dtype=torch.float32, device=dev)
+    sink = torch.empty(workgroups, dtype=torch.int32, device=dev)
+    L = _lib.lib()
+    run = lambda: _lib.check(L.bb_stream_read(_lib.ptr(buf), nbytes, _lib.ptr(sink), workgroups,  # noqa: E731
+                                              _lib.stream_of(buf)))
+    run()
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        run()
+        b.record()
+        torch.cuda.synchronize()
+        best = min(best, a.elapsed_time(b))
+    del buf
+    return {"gbps": round(nbytes / (best * 1e-3) / 1e9, 1), "bytes": nbytes, "workgroups": workgroups,
+            "kernel": "stream_read_kernel (bb_stream_read): 16-byte loads, 4 in flight per thread"}
 
 
 def main_traffic():
@@ -221,7 +252,7 @@ def config1_side_by_side(dev, seed):
             "max_abs_gpu_vs_cpu": round(err.max().item(), 5), "mean_abs_gpu_vs_cpu": round(err.mean().item(), 6)}
 
 
-def decode_leg(dev, seed):
+def decode_leg(dev, seed, ceiling):
     """exact decode over an INT8 cache of 131072 tokens (32 q / 8 KV heads, d=128, per-token
     per-head fp32 scales = absmax/127), 256 steps; each step quantises one new token into the cache and attends to
     all n + 1 rows with a fresh bf16 query. Reported per step with the cache bytes a step must read."""
@@ -263,10 +294,11 @@ def decode_leg(dev, seed):
                         "d=128, fp32 per-token per-head scales, 256 steps",
             "us_per_step": round(us, 2), "bytes_per_step": int(bytes_step), "achieved_gbps": round(gbps, 1),
             "peak_gbps": PEAK_HBM_GBPS, "frac": round(gbps / PEAK_HBM_GBPS, 4),
+            "read_ceiling_gbps": ceiling["gbps"], "frac_of_read_ceiling": round(gbps / ceiling["gbps"], 4),
             "kernels": "per step decode_mfma_kernel (new-row quantisation + split-K decode) + decode_merge_kernel"}
 
 
-def sparse_decode_leg(dev, seed):
+def sparse_decode_leg(dev, seed, ceiling):
     """Sparse decode after a 128K prefill (the reference's kernels/bigger_bird_decode.py + bigger_bird_route.py):
     bf16 cache of 131072 tokens (+1 per step), 32 q / 8 KV heads, d=128; a step appends the new K/V row at the
     device-side length, routes (pooled decode routing over every cached key, top 512 per KV head outside the sink
@@ -333,6 +365,8 @@ def sparse_decode_leg(dev, seed):
     res["achieved_gbps"] = round(res["bytes_per_step"] / (us * 1e-6) / 1e9, 1)
     res["peak_gbps"] = PEAK_HBM_GBPS
     res["frac"] = round(res["achieved_gbps"] / PEAK_HBM_GBPS, 4)
+    res["read_ceiling_gbps"] = ceiling["gbps"]
+    res["frac_of_read_ceiling"] = round(res["achieved_gbps"] / ceiling["gbps"], 4)
     return res
 
 
@@ -371,6 +405,22 @@ def short_arm_leg(dev, seed):
     with torch.inference_mode():
         sparse_ms = timed(lambda: attn.sparse_prefill(q, k, v))
         res["sparse_ms"] = round(sparse_ms, 3)
+        # the same launches one stage at a time (checked bit-identical to sparse_prefill): best of 3 per stage
+        ref = attn.sparse_prefill(q, k, v)
+        mk = lambda: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))  # noqa: E731
+        stages = ("routes", "transpose_v", "main", "tail")
+        best = {st: float("inf") for st in stages}
+        for i in range(4):
+            ev = {st: mk() for st in stages}
+            out, _ = staged_prefill(attn, q, k, v, ev)
+            torch.cuda.synchronize()
+            if i == 0 and not torch.equal(out, ref):
+                raise SystemExit("staged prefill (B=4) differs from sparse_prefill")
+            if i > 0:
+                for st in stages:
+                    best[st] = min(best[st], ev[st][0].elapsed_time(ev[st][1]))
+        del ref, out
+        res["stage_ms"] = {st: round(x, 3) for st, x in best.items()}
         # 4 d FLOP per attended (q, k) pair, pairs counted from each batch element's actual routes
         flop = sum(4 * d * attended_pairs(T, H, cfg["sink"], cfg["window"], attn.last_routes[b].cpu(),
                                           cfg["exact_tail"]) for b in range(B))
@@ -625,6 +675,7 @@ def main():
         ms_per_step = t_start.elapsed_time(t_end) / args.steps
         stage_avg = {s: sum(e[s][0].elapsed_time(e[s][1]) for e in evs) / args.steps for s in ev}
 
+    ceiling = None if args.no_decode else hbm_read_ceiling(dev)
     r = cfg["exact_tail"]
     pairs_total = attended_pairs(T, H, cfg["sink"], cfg["window"], routes, r)
     pairs_tail = H * sum(i + 1 for i in range(T - r, T))
@@ -670,8 +721,9 @@ def main():
                           "hbm_gbps": round(tail_bytes / (stage_avg["tail"] * 1e-3) / 1e9, 1),
                           "hbm_frac": round(tail_bytes / (stage_avg["tail"] * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
                           "bytes": tail_bytes},
-        "decode": None if args.no_decode else decode_leg(dev, args.seed),
-        "sparse_decode": None if args.no_decode else sparse_decode_leg(dev, args.seed),
+        "decode": None if args.no_decode else decode_leg(dev, args.seed, ceiling),
+        "sparse_decode": None if args.no_decode else sparse_decode_leg(dev, args.seed, ceiling),
+        "hbm_read_ceiling": ceiling,
         "short_arm": None if args.no_short_arm else short_arm_leg(dev, args.seed),
         "cpu_baseline": None,
     }
