@@ -27,8 +27,9 @@ extern "C" {
 /* Library version (major * 10000 + minor * 100 + patch). The minor number changes with every change of an entry
  * point's parameter list, so a caller built against another header can refuse the library:
  *   100  first release
- *   200  bb_sparse_flash takes is_f16 (after D); bb_sparse_flash_workspace takes n_groups (after route_k) and
- *        has_key_mask (last); bb_rope_inplace takes is_f16 (before stream) */
+ *   200  bb_sparse_flash and bb_routes take is_f16 (after D); bb_sparse_flash_workspace takes n_groups (after
+ *        route_k) and has_key_mask (last); bb_rope_inplace takes is_f16 (before stream); bb_init and bb_stream_read
+ *        added */
 #define BB_ABI_VERSION 200
 int bb_version(void);
 
@@ -98,13 +99,15 @@ int64_t bb_transpose_v_cols(int64_t N);
  * ascending as int32 in idx_out [B*H, budget]. Replaces RDAttention.routes (modal_rd/attention.py:143-174).
  *   q [B*H, n, D] (strides sq[2]: head, token), k [B*Hkv, n, D] (strides sk[2]); qpos [r] int64 on the device.
  *   pooled_out: optional [B*H, n] uint64 copy of the pooled scores in units of 2^-40 (NULL to skip).
- *   Arithmetic is deterministic: bf16 scores rounded from fp32 sums in the accumulation order of the reference's
- *   CPU matmul (oneDNN AMX-BF16: per 32-element block of d, even and odd fp32 chains), fixed-point softmax sums;
- *   results are identical on every run.
+ *   q and k are bf16 (is_f16 = 0) or fp16 (is_f16 = 1), as the reference's routes() runs in the model dtype.
+ *   Arithmetic is deterministic: scores rounded from fp32 sums in the accumulation order of the reference's CPU
+ *   matmul (bf16: oneDNN AMX-BF16, per 32-element block of d even and odd fp32 chains, rounded to bf16; fp16: one
+ *   sequential fp32 chain over d, rounded to fp16), fixed-point softmax sums; results are identical on every run.
  */
 int bb_routes(const void* q, const int64_t* sq, const void* k, const int64_t* sk, const int64_t* qpos, int r,
-              int B, int H, int Hkv, int64_t n, int D, int64_t sink, int64_t window, int budget, float scaling,
-              int pool_max, int32_t* idx_out, uint64_t* pooled_out, void* ws, size_t ws_bytes, void* stream);
+              int B, int H, int Hkv, int64_t n, int D, int is_f16, int64_t sink, int64_t window, int budget,
+              float scaling, int pool_max, int32_t* idx_out, uint64_t* pooled_out, void* ws, size_t ws_bytes,
+              void* stream);
 
 size_t bb_routes_workspace(int64_t n, int H, int Hkv, int B, int r);
 

@@ -19,6 +19,7 @@
  * fp32 accumulation order is the library's; on the CPU that produced the golden routes (torch 2.10, oneDNN, AMX-BF16)
  * that order is fixed and reproduced exactly by amx_dot() below.  Every later step is fixed here as well:
  *   s    = bf16_rne(amx_dot(q, k))                     d even; score mode 1 uses bf16_rne(exact q.k) instead
+ *          fp16_rne(f16_seq_dot(q, k))               fp16 q and k: torch's CPU fp16 matmul, one sequential fp32 chain
  *   x    = fp32(s * scaling)
  *   M_i  = max_j x_ij over causal keys j <= qpos_i
  *   e_ij = det_exp2(fp32(fp32(x_ij - M_i) * LOG2E))    det_exp2: rint reduction + degree-7 Horner with fmaf
@@ -152,6 +153,38 @@ static inline float amx_dot(const uint16_t* a, const uint16_t* b, int d) {
   return acc;
 }
 
+/*
+ * fp32 score of one query row against one key row for fp16 inputs, in the accumulation order of torch's CPU fp16
+ * matmul (the reference's modal_rd/attention.py:164 on fp16 tensors): one sequential fp32 chain over d in order. An
+ * fp16 x fp16 product is exact in fp32, so every step is one fp32 rounding. (Pinned against torch.matmul on fp16 CPU
+ * tensors.)
+ */
+static inline float f16_seq_dot(const uint16_t* a, const uint16_t* b, int d) {
+  float acc = 0.0f;
+  for (int i = 0; i < d; ++i) acc = acc + f16_to_f32(a[i]) * f16_to_f32(b[i]);
+  return acc;
+}
+
+/* fp32 -> the nearest fp16 value (ties to even), returned as fp32 (exact): 11 significant bits, subnormal spacing
+ * 2^-24, magnitudes from 65520 up rounding to infinity. */
+static inline float f16_round(float x) {
+  if (x == 0.0f || isnan(x) || isinf(x)) return x;
+  double ax = fabs((double)x);
+  double quantum;
+  if (ax < 0x1p-14) {
+    quantum = 0x1p-24;
+  } else {
+    int e;
+    frexp(ax, &e); /* ax = m * 2^e, m in [0.5, 1) */
+    quantum = ldexp(1.0, e - 11);
+  }
+  double r = nearbyint((double)x / quantum) * quantum;
+  if (fabs(r) > 65504.0) r = copysign(INFINITY, r);
+  return (float)r;
+}
+float orc_f16_round(float x) { return f16_round(x); }
+float orc_f16_dot(const uint16_t* a, const uint16_t* b, int d) { return f16_seq_dot(a, b, d); }
+
 /* Exact float64 dot product (bf16 inputs, d <= 128: every partial sum is exact). */
 static inline double exact_dot(const uint16_t* a, const uint16_t* b, int d) {
   double s = 0.0;
@@ -174,7 +207,7 @@ float orc_amx_dot(const uint16_t* a, const uint16_t* b, int d) { return amx_dot(
  */
 int orc_routes(const uint16_t* q, int64_t sq0, int64_t sq1, const uint16_t* k, int64_t sk0, int64_t sk1,
                int H, int Hkv, int n, int d, const int64_t* qpos, int r, int sink, int window, int budget,
-               float scaling, int pool_max, uint64_t* pooled_out, int32_t* idx_out, int nthreads) {
+               float scaling, int pool_max, uint64_t* pooled_out, int32_t* idx_out, int nthreads, int is_f16) {
   if (H <= 0 || Hkv <= 0 || H % Hkv || n <= 0 || d <= 0 || r <= 0 || budget < 0) return -1;
   int G = H / Hkv;
   int lo = sink < n ? (sink < 0 ? 0 : sink) : n;
@@ -219,9 +252,15 @@ int orc_routes(const uint16_t* q, int64_t sq0, int64_t sq1, const uint16_t* k, i
       float m = -INFINITY;
       for (int j = 0; j <= last; ++j) {
         const uint16_t* krow = k + g * sk0 + (int64_t)j * sk1;
-        uint16_t sb = g_score_mode ? orc_bf16_from_double(exact_dot(qrow, krow, d))
-                                   : f32_to_bf16_rne(amx_dot(qrow, krow, d));
-        float xv = bf16_to_f32(sb) * scaling;
+        float sv;
+        if (is_f16) {
+          sv = f16_round(f16_seq_dot(qrow, krow, d));
+        } else {
+          uint16_t sb = g_score_mode ? orc_bf16_from_double(exact_dot(qrow, krow, d))
+                                     : f32_to_bf16_rne(amx_dot(qrow, krow, d));
+          sv = bf16_to_f32(sb);
+        }
+        float xv = sv * scaling;
         x[j] = xv;
         if (xv > m) m = xv;
       }

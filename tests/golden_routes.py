@@ -36,7 +36,7 @@ def case(name):
     c = next(c for c in meta["cases"] if c["name"] == name)
     cfg = c["cfg"]
     inp = make_inputs(c["T"], c["H"], c["Hkv"], c["d"], seed=c["seed"], planted=c["planted"], sink=cfg["sink"],
-                      window=cfg["window"])
+                      window=cfg["window"], dtype=getattr(torch, c.get("dtype", "bfloat16")))
     if _sha(inp["q"]) != c["q_sha256"] or _sha(inp["k"]) != c["k_sha256"]:
         raise AssertionError(f"{name}: regenerated inputs differ from the ones the reference saw (RNG drift)")
     T = c["T"]

@@ -80,7 +80,7 @@ def test_routes_argument_errors():
     L = _lib.lib()
     s2 = _lib.i64s(128 * 1000, 128)
     rc = L.bb_routes(ctypes.c_void_p(16), s2, ctypes.c_void_p(16), s2, ctypes.c_void_p(16), 64, 1, 32, 8, 1000, 128,
-                     64, 512, 600, 0.1, 0, ctypes.c_void_p(16), None, ctypes.c_void_p(16), 1 << 30, None)
+                     0, 64, 512, 600, 0.1, 0, ctypes.c_void_p(16), None, ctypes.c_void_p(16), 1 << 30, None)
     assert rc == -1 and "exceeds" in L.bb_last_error().decode()
 
 

@@ -1,7 +1,8 @@
 """Pins the routing oracle (oracle/bb_oracle.c orc_routes) before it is trusted as the GPU router's checker.
 
-  * against the reference's own routes() indices (tests/golden, written by golden/make_golden.py) -- set-exact;
-  * the score arithmetic against torch's CPU bf16 matmul (the library routine the reference calls);
+  * against the reference's own routes() indices (tests/golden, written by golden/make_golden.py) -- set-exact, for
+    bf16 and for fp16 inputs;
+  * the score arithmetic against torch's CPU bf16 and fp16 matmuls (the library routine the reference calls);
   * the pooled probabilities against float64 brute force and against the reference's pooled values;
   * closed-form special cases (full budget, ties, planted keys) and planted mistakes that those checks must catch.
 """
@@ -28,7 +29,8 @@ def _route_case_kwargs(g):
                 route_pool=g["route_pool"], qpos=g["qpos"])
 
 
-SMALL_GOLDEN = ["config1", "small_mean", "odd_planted", "max_pool", "spread", "mha_d32", "vertical_sqrt"]
+SMALL_GOLDEN = ["config1", "small_mean", "odd_planted", "max_pool", "spread", "mha_d32", "vertical_sqrt", "config1_f16",
+                "small_mean_f16", "max_pool_f16"]
 
 
 @pytest.mark.parametrize("name", SMALL_GOLDEN)
@@ -36,13 +38,15 @@ def test_oracle_matches_reference_routes(name):
     g = golden_routes.case(name)
     got, pooled = oracle.routes(g["q"][0], g["k"][0], return_pooled=True, **_route_case_kwargs(g))
     golden_routes.check_against_golden(got, g, pooled=pooled, what=name)
-    if name != "max_pool":
+    if not name.startswith("max_pool"):
         assert torch.equal(got, g["routes"]), name
 
 
-def test_oracle_matches_reference_routes_128k():
-    """BASELINE config 2 (T=131072, 32/8 heads, 64 planted keys per KV head): set-exact at the production shape."""
-    g = golden_routes.case("config2")
+@pytest.mark.parametrize("name", ["config2", "config2_f16"])
+def test_oracle_matches_reference_routes_128k(name):
+    """BASELINE config 2 (T=131072, 32/8 heads, 64 planted keys per KV head): set-exact at the production shape, for
+    bf16 and fp16 inputs."""
+    g = golden_routes.case(name)
     got = oracle.routes(g["q"][0], g["k"][0], **_route_case_kwargs(g))
     assert torch.equal(got, g["routes"])
     for h in range(g["H"]):
@@ -66,6 +70,47 @@ def test_score_order_matches_torch_cpu_matmul(d):
                 v = L.orc_amx_dot(qn[b, i].data_ptr(), kn[b, j].data_ptr(), d)
                 mism += torch.tensor(v).to(torch.bfloat16).item() != s[b, i, j].item()
     assert mism == 0
+
+
+@pytest.mark.parametrize("d,n", [(32, 1024), (64, 1024), (128, 4096)])
+def test_f16_score_order_matches_torch_cpu_matmul(d, n):
+    """fp16 inputs: orc_f16_dot (one sequential fp32 chain over d) rounded to fp16 reproduces torch.matmul on fp16 CPU
+    tensors bit for bit, with K passed as a transposed view as the reference does (modal_rd/attention.py:164)."""
+    gen = torch.Generator().manual_seed(d + n)
+    q = torch.randn(2, 256, d, generator=gen).to(torch.float16)
+    k = (2 * torch.randn(2, n, d, generator=gen)).to(torch.float16)
+    s = torch.matmul(q, k.transpose(-1, -2))
+    L = oracle.lib()
+    mism = 0
+    for b in range(2):
+        for i in range(0, 256, 5):
+            for j in range(0, n, 7):
+                v = L.orc_f16_round(L.orc_f16_dot(q[b, i].data_ptr(), k[b, j].data_ptr(), d))
+                mism += v != s[b, i, j].item()
+    assert mism == 0
+
+
+def test_f16_score_order_is_not_the_bf16_order():
+    """Planted check for the fp16 score model: the bf16 path's block order (even / odd chains per 32 elements) on the
+    same fp16 values differs from torch's fp16 matmul on some scores, so mixing the two orders is caught."""
+    gen = torch.Generator().manual_seed(3)
+    q = torch.randn(64, 128, generator=gen).to(torch.float16)
+    k = (3 * torch.randn(2048, 128, generator=gen)).to(torch.float16)
+    s = torch.matmul(q[None], k.T[None])[0].float().numpy()
+    qf, kf = q.float().numpy(), k.float().numpy()
+    L = oracle.lib()
+    flips = 0
+    for i in range(0, 64, 3):
+        for j in range(0, 2048, 3):
+            acc = np.float32(0)
+            for b0 in range(0, 128, 32):
+                e, o = np.float32(0), np.float32(0)
+                for t in range(b0, b0 + 32, 2):
+                    e = np.float32(e + np.float32(qf[i, t] * kf[j, t]))
+                    o = np.float32(o + np.float32(qf[i, t + 1] * kf[j, t + 1]))
+                acc = np.float32(acc + np.float32(e + o))
+            flips += L.orc_f16_round(float(acc)) != s[i, j]
+    assert flips > 0
 
 
 def test_score_order_is_not_exact_rounding():

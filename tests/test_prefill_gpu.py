@@ -1,6 +1,7 @@
 """End-to-end RDAttention.sparse_prefill on the GPU (routes + sparse kernel + exact tail, modal_rd/attention.py:176-206)
-at BASELINE config 1 (T=8192, {64, 2048, 128, 256}) and config 2 (T=131072, {64, 16384, 512, 256}, 64 planted keys
-per KV head) on the inputs the reference's routes() saw (tests/golden): routes set-exact against the reference, and
+at BASELINE config 1 (T=8192, {64, 2048, 128, 256}; also with fp16 inputs) and config 2 (T=131072,
+{64, 16384, 512, 256}, 64 planted keys per KV head) on the inputs the reference's routes() saw (tests/golden): routes
+set-exact against the reference, and
 output rows within max-abs 2e-2 / mean-abs 2e-3 of the float64 oracle over the union mask -- every (head, row) at
 config 1; at config 2, 8 heads (one per KV group) at every 64-row tile boundary, the window edges, routed keys' first
 rows, 4096 random rows and every exact-tail row. Config 4 (B=4) checks sampled rows of all 32 heads, and each
@@ -24,7 +25,8 @@ def _base(H, Hkv, d):
 
 
 CFG = {"config1": dict(sink=64, window=2048, vertical=128, exact_tail=256),
-       "config2": dict(sink=64, window=16384, vertical=512, exact_tail=256)}
+       "config2": dict(sink=64, window=16384, vertical=512, exact_tail=256),
+       "config1_f16": dict(sink=64, window=2048, vertical=128, exact_tail=256)}
 
 
 def _rows_for(name, T, H, cfg, routes, gen):
@@ -33,7 +35,7 @@ def _rows_for(name, T, H, cfg, routes, gen):
     config2: 8 heads (one per KV group): every 64-row tile boundary (rows 64j - 1 and 64j), the window edges, the
     first row each of every 8th routed key reaches, 4096 random rows, and all 256 exact-tail rows."""
     W, r = cfg["window"], cfg["exact_tail"]
-    if name == "config1":
+    if name.startswith("config1"):
         return torch.stack(torch.meshgrid(torch.arange(H), torch.arange(T), indexing="ij"), -1).reshape(-1, 2)
     heads = torch.arange(0, H, 4) + torch.arange(H // 4) % 4  # 0, 5, 10, 15, 16, 21, 26, 31
     edges = torch.tensor([0, 1, 2, W - 2, W - 1, W, W + 1, W + 63, W + 64, T - r - 1])
@@ -49,7 +51,7 @@ def _rows_for(name, T, H, cfg, routes, gen):
     return torch.cat(pairs)
 
 
-@pytest.mark.parametrize("name", ["config1", "config2"])
+@pytest.mark.parametrize("name", ["config1", "config2", "config1_f16"])
 def test_sparse_prefill_matches_oracle(name, dev):
     print(f"case prefill {name}", flush=True)
     g = golden_routes.case(name)
@@ -57,8 +59,8 @@ def test_sparse_prefill_matches_oracle(name, dev):
     cfg = CFG[name]
     attn = RDAttention(_base(H, Hkv, d), **cfg)
     gen = torch.Generator().manual_seed(7)
-    v = torch.randn(1, Hkv, T, d, generator=gen).to(torch.bfloat16)
     q, k = g["q"], g["k"]
+    v = torch.randn(1, Hkv, T, d, generator=gen).to(q.dtype)
     with torch.inference_mode():
         out = attn.sparse_prefill(q.to(dev), k.to(dev), v.to(dev))
     torch.cuda.synchronize()

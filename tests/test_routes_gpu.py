@@ -1,5 +1,6 @@
 """bb_routes (HIP) against the CPU oracle: the deterministic contract makes them bit-identical, so route indices
-are compared set-exactly (sorted int32 equality) and the pooled fixed-point scores value-exactly."""
+are compared set-exactly (sorted int32 equality) and the pooled fixed-point scores value-exactly; for bf16 and for
+fp16 inputs (fp16 scores follow torch's CPU fp16 matmul order, checked against the reference's fp16 golden routes)."""
 import pytest
 import torch
 
@@ -20,11 +21,12 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
-def test_routes_bit_exact(case, dev):
+def test_routes_bit_exact(case, dtype, dev):
     name, T, H, Hkv, d, sink, window, budget, nr, pool, qmode, planted = case
-    print(f"case {name}", flush=True)
-    inp = make_inputs(T, H, Hkv, d, seed=3, window=window, sink=sink, planted=planted)
+    print(f"case {name} {dtype}", flush=True)
+    inp = make_inputs(T, H, Hkv, d, seed=3, window=window, sink=sink, planted=planted, dtype=dtype)
     q, k = inp["q"], inp["k"]
     idx, pooled = hip_routes(q.to(dev), k.to(dev), num_heads=H, num_kv_heads=Hkv, sink=sink, window=window,
                              budget=budget, n_route=nr, route_pool=pool, route_queries=qmode, scaling=d ** -0.5,
@@ -69,7 +71,8 @@ def test_budget_covers_all_eligible(dev):
     assert torch.equal(idx, torch.arange(sink, T - window, dtype=torch.int32).expand(H, -1))
 
 
-GOLDEN = ["config1", "small_mean", "odd_planted", "max_pool", "spread", "mha_d32", "vertical_sqrt", "config2"]
+GOLDEN = ["config1", "small_mean", "odd_planted", "max_pool", "spread", "mha_d32", "vertical_sqrt", "config2",
+          "config1_f16", "config2_f16", "small_mean_f16", "max_pool_f16"]
 
 
 @pytest.mark.parametrize("name", GOLDEN)
@@ -85,7 +88,7 @@ def test_routes_match_reference_golden(name, dev):
                              route_queries=g["route_queries"], scaling=g["scaling"], return_pooled=True)
     torch.cuda.synchronize()
     tied = golden_routes.check_against_golden(idx.cpu(), g, pooled=pooled.cpu(), what=name)
-    if name != "max_pool":
+    if not name.startswith("max_pool"):
         assert tied == 0 and torch.equal(idx.cpu(), g["routes"])
     if g["planted"] is not None:
         G = g["H"] // g["Hkv"]

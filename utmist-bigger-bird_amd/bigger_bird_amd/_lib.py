@@ -29,8 +29,8 @@ SIGNATURES = {
     "bb_exact_attention_workspace": (_sz, [_i32, _i64, _i64, _i32, _i32, _i32, _i32]),
     "bb_transpose_v": (_i32, [_vp, c_i64p, _i32, _i64, _i32, _vp, _vp]),
     "bb_transpose_v_cols": (_i64, [_i64]),
-    "bb_routes": (_i32, [_vp, c_i64p, _vp, c_i64p, _vp, _i32, _i32, _i32, _i32, _i64, _i32, _i64, _i64, _i32, _f32,
-                         _i32, _vp, _vp, _vp, _sz, _vp]),
+    "bb_routes": (_i32, [_vp, c_i64p, _vp, c_i64p, _vp, _i32, _i32, _i32, _i32, _i64, _i32, _i32, _i64, _i64, _i32,
+                         _f32, _i32, _vp, _vp, _vp, _sz, _vp]),
     "bb_routes_workspace": (_sz, [_i64, _i32, _i32, _i32, _i32]),
     "bb_int8_quantize": (_i32, [_vp, _i32, _i64, _i64, _i32, _i64, _i32, _f32, _vp, _vp, _i32, _vp]),
     "bb_int8_dequantize": (_i32, [_vp, _vp, _i32, _i64, _i32, _vp, _i32, _vp]),

@@ -83,9 +83,9 @@ def routes(q, k, *, num_heads, num_kv_heads, sink, window, budget, n_route=64, r
     Returns int32 [B * H, budget], ascending per head (and the pooled scores [B * H, n] as float probabilities
     when `return_pooled`)."""
     _lib.require_gpu(q, k, what="routes")
-    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16:
-        # The score contract (bf16 scores in the reference's accumulation order) is defined for bf16 only.
-        raise ValueError("routes: bf16 q and k required")
+    if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype:
+        # the reference runs routes() in the model dtype (modal_rd/attention.py:164): bf16 or fp16 scores
+        raise ValueError("routes: bf16 or fp16 q and k of one dtype required")
     bsz = q.shape[0]
     n, d = k.shape[-2], k.shape[-1]
     r = min(n_route, n)
@@ -104,7 +104,7 @@ def routes(q, k, *, num_heads, num_kv_heads, sink, window, budget, n_route=64, r
     ws = _lib.workspace(ws_bytes, q.device)
     _lib.check(L.bb_routes(_lib.ptr(Q), _lib.i64s(Q.stride(0), Q.stride(1)), _lib.ptr(K),
                            _lib.i64s(K.stride(0), K.stride(1)), _lib.ptr(qpos), r, bsz, num_heads, num_kv_heads, n, d,
-                           sink, window, budget, float(scaling), int(route_pool == "max"),
+                           int(q.dtype == torch.float16), sink, window, budget, float(scaling), int(route_pool == "max"),
                            _lib.ptr(idx) if budget else None, _lib.ptr(pooled), _lib.ptr(ws), ws_bytes,
                            _lib.stream_of(q)))
     if not return_pooled:

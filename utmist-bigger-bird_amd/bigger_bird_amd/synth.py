@@ -1,7 +1,8 @@
 """Synthetic Llama-3-8B-geometry attention inputs (the benchmark workloads).
 
 Q [B, H, T, d], K/V [B, Hkv, T, d] ~ N(0, 1) drawn on the host from a seeded torch.Generator (identical bytes on
-every machine running this torch build), rounded to bf16, with HF Llama RoPE (theta 500000) applied to Q and K.
+every machine running this torch build), rounded to bf16 (or fp16), with HF Llama RoPE (theta 500000) applied to Q
+and K.
 Optionally `planted` keys per KV head: key m is 4 x the mean over the group's query heads of post-RoPE Q at position
 T - planted + m, written post-RoPE at `planted` distinct seeded positions in [sink, T - window) -- they must be routed.
 """
@@ -26,8 +27,8 @@ def rope_host(x, cos, sin):
 
 
 def make_inputs(T, H=32, Hkv=8, d=128, *, batch=1, seed=0, theta=500000.0, rope=True, planted=0, sink=64,
-                window=16384, device="cpu", rope_on_device=True, rng="host"):
-    """Returns dict(q, k, v, planted_pos) with q [B,H,T,d], k/v [B,Hkv,T,d] bf16 on `device`.
+                window=16384, device="cpu", rope_on_device=True, rng="host", dtype=torch.bfloat16):
+    """Returns dict(q, k, v, planted_pos) with q [B,H,T,d], k/v [B,Hkv,T,d] in `dtype` (bf16 or fp16) on `device`.
 
     rng="host" draws Q/K/V from a CPU generator (identical bytes on every machine); rng="device" draws them with the
     device's generator (fast at 128K tokens, reproducible on one torch build and GPU model). Planted positions always
@@ -36,13 +37,13 @@ def make_inputs(T, H=32, Hkv=8, d=128, *, batch=1, seed=0, theta=500000.0, rope=
     g = torch.Generator().manual_seed(seed)
     if rng == "device":
         gd = torch.Generator(device=device).manual_seed(seed)
-        q = torch.randn(batch, H, T, d, generator=gd, device=device).to(torch.bfloat16)
-        k = torch.randn(batch, Hkv, T, d, generator=gd, device=device).to(torch.bfloat16)
-        v = torch.randn(batch, Hkv, T, d, generator=gd, device=device).to(torch.bfloat16)
+        q = torch.randn(batch, H, T, d, generator=gd, device=device).to(dtype)
+        k = torch.randn(batch, Hkv, T, d, generator=gd, device=device).to(dtype)
+        v = torch.randn(batch, Hkv, T, d, generator=gd, device=device).to(dtype)
     elif rng == "host":
-        q = torch.randn(batch, H, T, d, generator=g).to(torch.bfloat16)
-        k = torch.randn(batch, Hkv, T, d, generator=g).to(torch.bfloat16)
-        v = torch.randn(batch, Hkv, T, d, generator=g).to(torch.bfloat16)
+        q = torch.randn(batch, H, T, d, generator=g).to(dtype)
+        k = torch.randn(batch, Hkv, T, d, generator=g).to(dtype)
+        v = torch.randn(batch, Hkv, T, d, generator=g).to(dtype)
     else:
         raise ValueError("rng must be 'host' or 'device'")
     pos = None
@@ -56,7 +57,7 @@ def make_inputs(T, H=32, Hkv=8, d=128, *, batch=1, seed=0, theta=500000.0, rope=
     if on_gpu:
         q, k, v = q.to(device), k.to(device), v.to(device)
     if rope:
-        cos, sin = rope_cos_sin(T, d, theta)
+        cos, sin = rope_cos_sin(T, d, theta, dtype)
         if on_gpu and rope_on_device:
             from .attention import rope_inplace
             cos, sin = cos.to(device), sin.to(device)
@@ -68,7 +69,7 @@ def make_inputs(T, H=32, Hkv=8, d=128, *, batch=1, seed=0, theta=500000.0, rope=
     if planted:
         G = H // Hkv
         tail = q[:, :, T - planted:, :].float().view(batch, Hkv, G, planted, d).mean(2)  # [B, Hkv, planted, d]
-        keys = (4.0 * tail).to(torch.bfloat16)
+        keys = (4.0 * tail).to(dtype)
         p = pos.to(k.device)
         k.scatter_(2, p[..., None].expand(-1, -1, -1, d), keys)
     return dict(q=q, k=k, v=v, planted_pos=pos)

@@ -309,8 +309,8 @@ static int routes_reference_order() {
 }
 
 int bb_routes(const void* q, const int64_t* sq, const void* k, const int64_t* sk, const int64_t* qpos, int r, int B,
-              int H, int Hkv, int64_t n, int D, int64_t sink, int64_t window, int budget, float scaling, int pool_max,
-              int32_t* idx_out, uint64_t* pooled_out, void* ws, size_t ws_bytes, void* stream) {
+              int H, int Hkv, int64_t n, int D, int is_f16, int64_t sink, int64_t window, int budget, float scaling,
+              int pool_max, int32_t* idx_out, uint64_t* pooled_out, void* ws, size_t ws_bytes, void* stream) {
   g_err[0] = 0;
   if (!q || !k || !qpos || !sq || !sk) return fail("routes: null argument");
   if (H <= 0 || Hkv <= 0 || H % Hkv || B <= 0 || n <= 0 || r <= 0) return fail("routes: bad head/sequence sizes");
@@ -339,6 +339,7 @@ int bb_routes(const void* q, const int64_t* sq, const void* k, const int64_t* sk
   p.budget = budget; p.pool_max = pool_max; p.scaling = scaling;
   p.out_idx = idx_out;
   p.scores_reference_order = routes_reference_order();
+  p.f16 = is_f16 ? 1 : 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e = bb::launch_routes(p, ws, ws_bytes, st);
   if (e != hipSuccess) return hip_status(e, "bb_routes");

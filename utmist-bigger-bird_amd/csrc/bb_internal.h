@@ -47,6 +47,7 @@ struct RoutesParams {
   int64_t n;
   int H, Hkv, B, D, r, sink, window, budget, pool_max;
   int scores_reference_order;  // 1: every score by the reference-order chain (no MFMA), for cross-checks
+  int f16;              // q and k are fp16 (scores in torch's CPU fp16 order, stored as fp16); else bf16
   float scaling;
   uint16_t* scores;     // [B*Hkv][G*r][n] bf16 workspace
   uint32_t* rowmax;     // [B*H*r] row maxima (fp32 bits)

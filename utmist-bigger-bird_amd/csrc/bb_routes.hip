@@ -6,6 +6,8 @@
 //   s    = bf16_rne(q.k in the reference's order)   torch's CPU bf16 matmul (oneDNN, AMX-BF16): per 32-element block
 //                                                   of d, fp32 chains over the even and the odd elements, then
 //                                                   acc = acc + (even + odd); one RNE step to bf16
+//          fp16_rne(q.k, one sequential fp32 chain) fp16 q and k: torch's CPU fp16 matmul; the workspace then holds
+//                                                   fp16 scores
 //   x    = fp32(s * scaling); M = row max over causal keys j <= qpos
 //   e    = det_exp2(fp32(fp32(x - M) * log2e))
 //   Z    = sum floor(e * 2^40) (uint64)    p = fp32(e * fp32(2^40 / double(Z)))
@@ -43,6 +45,20 @@ constexpr float kFixOne = 1099511627776.0f;  // 2^40
 
 BB_DEV uint64_t fix40(float v) { return (uint64_t)(v * kFixOne); }
 
+// A stored score (bf16 bits, or fp16 bits for fp16 inputs) as fp32; -inf marks a masked key in either type.
+template <bool F16>
+BB_DEV float score_f32(uint16_t s) {
+  if constexpr (F16) return (float)__builtin_bit_cast(_Float16, s);
+  else return bf16_to_f32(s);
+}
+template <bool F16>
+BB_DEV uint16_t score_bits(float x) {
+  if constexpr (F16) return __builtin_bit_cast(uint16_t, (_Float16)x);  // round to nearest even
+  else return f32_to_bf16(x);
+}
+template <bool F16>
+constexpr uint16_t kScoreNegInf = F16 ? 0xfc00u : 0xff80u;
+
 struct RouteGeom {
   int G, rows, n_kb1, n_kb2, row_blocks;
   int sum_rows, sum_splits;  // rowsum_kernel: rows per workgroup (a multiple of 4) and row slices
@@ -53,8 +69,9 @@ struct RouteGeom {
 // Q^T stays in LDS for the whole key range; each key block is staged as fp32 K^T. Thread t owns rows
 // 8*(t%32)..+7 and keys 4*(t/32)..+3 of a block. Every score is built in the reference's accumulation order: per
 // 32-element block of d, two sequential fp32 chains over the even and the odd elements (fmaf of two bf16 values is
-// one rounding of the exact product sum), then acc = acc + (even + odd).
-template <int D>
+// one rounding of the exact product sum), then acc = acc + (even + odd); for fp16 inputs (F16) one sequential chain
+// over d (an fp16 product is exact in fp32 as well) and the result rounded to fp16.
+template <int D, bool F16>
 __global__ __launch_bounds__(256) void scores_kernel(RoutesParams p, RouteGeom g, float* __restrict__ pmax) {
   static_assert(D % 32 == 0, "head_dim must be a multiple of 32");
   __shared__ __attribute__((aligned(16))) uint16_t qs[D][kMaxRows];        // Q^T (bf16)
@@ -105,8 +122,8 @@ __global__ __launch_bounds__(256) void scores_kernel(RoutesParams p, RouteGeom g
       const u32x4_t v = j < p.n ? ld16(kbase + j * p.sk1 + 8 * c8) : u32x4_t{0, 0, 0, 0};
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        ks[8 * c8 + 2 * w][key] = bf16_to_f32((uint16_t)(v[w] & 0xffffu));
-        ks[8 * c8 + 2 * w + 1][key] = bf16_to_f32((uint16_t)(v[w] >> 16));
+        ks[8 * c8 + 2 * w][key] = score_f32<F16>((uint16_t)(v[w] & 0xffffu));
+        ks[8 * c8 + 2 * w + 1][key] = score_f32<F16>((uint16_t)(v[w] >> 16));
       }
     }
     __syncthreads();
@@ -116,7 +133,20 @@ __global__ __launch_bounds__(256) void scores_kernel(RoutesParams p, RouteGeom g
     for (int a = 0; a < 8; ++a)
 #pragma unroll
       for (int b = 0; b < 4; ++b) acc[a][b] = 0.0f;
-    for (int d0 = 0; d0 < D; d0 += 32) {
+    if constexpr (F16) {
+#pragma unroll 2
+      for (int dd = 0; dd < D; ++dd) {
+        const u32x4_t qv = *reinterpret_cast<const u32x4_t*>(&qs[dd][8 * rg]);
+        const f32x4_t kv = *reinterpret_cast<const f32x4_t*>(&ks[dd][4 * kg]);
+#pragma unroll
+        for (int a = 0; a < 8; ++a) {
+          const float fq = score_f32<true>((uint16_t)(qv[a >> 1] >> (16 * (a & 1))));
+#pragma unroll
+          for (int b = 0; b < 4; ++b) acc[a][b] = __builtin_fmaf(fq, kv[b], acc[a][b]);
+        }
+      }
+    }
+    for (int d0 = 0; !F16 && d0 < D; d0 += 32) {
       float ev[8][4], od[8][4];
 #pragma unroll
       for (int a = 0; a < 8; ++a)
@@ -155,10 +185,10 @@ __global__ __launch_bounds__(256) void scores_kernel(RoutesParams p, RouteGeom g
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         const int64_t j = jj + b;
-        sb[b] = 0xff80u;  // -inf
+        sb[b] = kScoreNegInf<F16>;
         if (j < p.n && j <= qp[a]) {
-          sb[b] = f32_to_bf16(acc[a][b]);
-          rmax[a] = fmaxf(rmax[a], bf16_to_f32(sb[b]) * p.scaling);
+          sb[b] = score_bits<F16>(acc[a][b]);
+          rmax[a] = fmaxf(rmax[a], score_f32<F16>(sb[b]) * p.scaling);
         }
       }
       if (row < nrows) {
@@ -490,6 +520,7 @@ BB_DEV float fix40_exp2(float y, float scale) {
 // Fixed-point partial row sums: one wave per row (4 rows in flight per workgroup), 16 keys per lane. The rows of a
 // key block may be cut into blockIdx.z slices of g.sum_rows rows, so short sequences still fill the chip. The terms
 // are integers below 2^41, so their sums stay exact in double precision (1024 terms per workgroup row < 2^51).
+template <bool F16>
 __global__ __launch_bounds__(256) void rowsum_kernel(RoutesParams p, RouteGeom g, uint64_t* __restrict__ psum) {
   const int kb = blockIdx.x, bkv = blockIdx.y;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -517,12 +548,12 @@ __global__ __launch_bounds__(256) void rowsum_kernel(RoutesParams p, RouteGeom g
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const uint16_t sb = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
-        const float x = bf16_to_f32(sb) * p.scaling;
+        const float x = score_f32<F16>(sb) * p.scaling;
         acc += (double)fix40_exp2((x - M) * kLog2e, 1.0f);
       }
     } else {
       for (int e = 0; e < 16 && j0 + e < p.n; ++e) {
-        const float x = bf16_to_f32(src[e]) * p.scaling;
+        const float x = score_f32<F16>(src[e]) * p.scaling;
         acc += (double)fix40_exp2((x - M) * kLog2e, 1.0f);
       }
     }
@@ -558,6 +589,7 @@ __global__ __launch_bounds__(64) void invz_kernel(RoutesParams p, RouteGeom g, c
 // Pooled fixed-point probability per (query head, key): two consecutive keys per thread (one 4-byte score load per
 // route row, eight rows' loads in flight), the head's r rows in a loop, sums exact in double precision (64 rows x
 // 2^41 < 2^53).
+template <bool F16>
 __global__ __launch_bounds__(256) void pooled_kernel(RoutesParams p, RouteGeom g, const float* __restrict__ invz) {
   const int64_t j0 = 2 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
   const int head = blockIdx.y;  // over B * H
@@ -582,8 +614,8 @@ __global__ __launch_bounds__(256) void pooled_kernel(RoutesParams p, RouteGeom g
       for (int u = 0; u < 8; ++u) {
         if (u >= nb) break;
         const float M = mrow[i + u], iz = zrow[i + u];
-        const float x0 = bf16_to_f32((uint16_t)(w[u] & 0xffffu)) * p.scaling;
-        const float x1 = bf16_to_f32((uint16_t)(w[u] >> 16)) * p.scaling;
+        const float x0 = score_f32<F16>((uint16_t)(w[u] & 0xffffu)) * p.scaling;
+        const float x1 = score_f32<F16>((uint16_t)(w[u] >> 16)) * p.scaling;
         const double f0 = (double)fix40_exp2((x0 - M) * kLog2e, iz);
         const double f1 = (double)fix40_exp2((x1 - M) * kLog2e, iz);
         if (p.pool_max) {
@@ -1020,17 +1052,22 @@ template <int D>
 hipError_t launch_routes_d(RoutesParams& p, const RouteGeom& g, float* pmax, uint64_t* psum, float* invz,
                            const TopWs& tw, hipStream_t stream) {
   const int nbkv = p.B * p.Hkv;
-  if (D == 128 && !p.scores_reference_order)
-    hipLaunchKernelGGL(scores_mfma_kernel<128>, dim3(g.n_kb1, g.row_blocks, nbkv), dim3(64 * kMsWaves), 0, stream, p,
-                       g, pmax);
+  const dim3 sgrid(g.n_kb1, g.row_blocks, nbkv);
+  // fp16 scores (8x finer rounding than bf16) are computed in the reference order directly
+  if (p.f16)
+    hipLaunchKernelGGL((scores_kernel<D, true>), sgrid, dim3(256), 0, stream, p, g, pmax);
+  else if (D == 128 && !p.scores_reference_order)
+    hipLaunchKernelGGL(scores_mfma_kernel<128>, sgrid, dim3(64 * kMsWaves), 0, stream, p, g, pmax);
   else
-    hipLaunchKernelGGL(scores_kernel<D>, dim3(g.n_kb1, g.row_blocks, nbkv), dim3(256), 0, stream, p, g, pmax);
+    hipLaunchKernelGGL((scores_kernel<D, false>), sgrid, dim3(256), 0, stream, p, g, pmax);
   hipLaunchKernelGGL(rowmax_kernel, dim3(g.rows, nbkv), dim3(64), 0, stream, p, g, pmax);
-  hipLaunchKernelGGL(rowsum_kernel, dim3(g.n_kb2, nbkv, g.sum_splits), dim3(256), 0, stream, p, g, psum);
+  if (p.f16) hipLaunchKernelGGL(rowsum_kernel<true>, dim3(g.n_kb2, nbkv, g.sum_splits), dim3(256), 0, stream, p, g, psum);
+  else hipLaunchKernelGGL(rowsum_kernel<false>, dim3(g.n_kb2, nbkv, g.sum_splits), dim3(256), 0, stream, p, g, psum);
   hipLaunchKernelGGL(invz_kernel, dim3(g.rows, nbkv), dim3(64), 0, stream, p, g, psum, invz, tw.hist,
                      reinterpret_cast<uint32_t*>(tw.meta));
-  hipLaunchKernelGGL(pooled_kernel, dim3((unsigned)((p.n + kPoolKeys - 1) / kPoolKeys), p.B * p.H), dim3(256), 0,
-                     stream, p, g, invz);
+  const dim3 pgrid((unsigned)((p.n + kPoolKeys - 1) / kPoolKeys), p.B * p.H);
+  if (p.f16) hipLaunchKernelGGL(pooled_kernel<true>, pgrid, dim3(256), 0, stream, p, g, invz);
+  else hipLaunchKernelGGL(pooled_kernel<false>, pgrid, dim3(256), 0, stream, p, g, invz);
   if (p.budget > 0) {
     int64_t lo = p.sink < p.n ? (p.sink > 0 ? p.sink : 0) : p.n, hi = p.n - p.window < p.n ? p.n - p.window : p.n;
     const int64_t cnt = hi > lo ? hi - lo : 0;
