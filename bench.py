@@ -308,8 +308,7 @@ def sparse_decode_leg(dev, seed, ceiling):
     so 8 steps need no host work between them; a replay has a fixed cost of about 5 us that 8 steps share); bytes =
     the K rows the routing reads + its fp32 score round trip + the K/V rows the sparse decode reads."""
     import torch
-    from bigger_bird_amd import bigger_bird_decode, bigger_bird_route
-    from bigger_bird_amd.decode import kv_append
+    from bigger_bird_amd.decode import decode_step
 
     n0, steps, H, Hkv, d = 131072, 64, 32, 8, 128
     front, window, routed = 64, 16384, 512
@@ -323,9 +322,10 @@ def sparse_decode_leg(dev, seed, ceiling):
     scale = d ** -0.5
 
     def step(length):
-        kv_append(k, v, kb, vb, length)  # the new row at the device-side length, then length += 1, one launch
-        idx = bigger_bird_route(qb, k, routed, front=front, window=window, scale=scale, n=length)
-        return bigger_bird_decode(qb, k, v, idx, front=front, window=window, scale=scale, n=length)
+        # length counts the new row: it becomes row length - 1 inside the routing scores pass, and the sparse decode's
+        # merge advances the length for the next step (bb_decode_step: 6 launches)
+        return decode_step(qb, k, v, kb, vb, length, routed=routed, front=front, window=window, scale=scale,
+                           advance=1)
 
     def timed(fn, reps=steps):
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -341,24 +341,24 @@ def sparse_decode_leg(dev, seed, ceiling):
                        "pooled decode routing (top 512 per KV head) + split-K decode over sink 64 + window 16384 + 512 "
                        "routed keys"}
     with torch.inference_mode():
-        length = torch.tensor([n0], device=dev)
+        length = torch.tensor([n0 + 1], device=dev)
         for _ in range(4):
             step(length)
-        length.fill_(n0)
+        length.fill_(n0 + 1)
         res["eager_us_per_step"] = timed(lambda: step(length))
-        length.fill_(n0)
+        length.fill_(n0 + 1)
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
             step(length)
         torch.cuda.current_stream().wait_stream(s)
         for per, key in ((1, "graph_us_per_step"), (8, "graph8_us_per_step")):
-            length.fill_(n0)
+            length.fill_(n0 + 1)
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
                 for _ in range(per):
                     step(length)
-            length.fill_(n0)
+            length.fill_(n0 + 1)
             res[key] = round(timed(graph.replay, steps // per) / per, 2)
             del graph
     n_mean = n0 + (steps + 1) / 2

@@ -29,8 +29,9 @@ extern "C" {
  *   100  first release
  *   200  bb_sparse_flash and bb_routes take is_f16 (after D); bb_sparse_flash_workspace takes n_groups (after
  *        route_k) and has_key_mask (last); bb_rope_inplace takes is_f16 (before stream); bb_init and bb_stream_read
- *        added */
-#define BB_ABI_VERSION 200
+ *        added
+ *   201  bb_decode_step and bb_decode_step_workspace added */
+#define BB_ABI_VERSION 201
 int bb_version(void);
 
 /* Message of the last failed call on this host thread ("" if none). */
@@ -212,6 +213,26 @@ size_t bb_decode_route_workspace(int64_t cap, int H, int Hkv, int splits, int k_
 int bb_kv_append(void* k, const int64_t* sk, void* v, const int64_t* sv, const void* knew, int64_t sknew,
                  const void* vnew, int64_t svnew, int Hkv, int D, int64_t cap, int64_t* n_dev, int64_t n_inc,
                  void* stream);
+
+/*
+ * One whole decode step over a bf16 / fp16 cache whose length n = *n_dev already counts the step's new row: the new
+ * K / V rows (knew / vnew, as in bb_kv_append) become row n - 1 of every KV head (when 1 <= n <= cap), the step
+ * attends (routed > 0: pooled decode routing of the top `routed` keys per KV head outside front and the last
+ * `window` keys, indices to idx_out [Hkv, routed], then the sparse decode over front | window | routed; routed = 0:
+ * dense decode over all n rows, front and window ignored), and afterwards *n_dev += advance when the row was
+ * appended. Results are bit-identical to bb_kv_append (at n - 1, n_inc 0) followed by bb_decode_route and
+ * bb_sparse_decode (or bb_sparse_decode with front 0 and window cap), with default splits, and the length add; the
+ * append and the add ride in the kernels that first read the cache and that end the step, so the step is two
+ * launches fewer (the two index_copy_ calls and the length add of modal_rd/graph_decode.py's step, followed by
+ * kernels/bigger_bird_route.py:83-115 and kernels/bigger_bird_decode.py:66-108). Workspace from
+ * bb_decode_step_workspace.
+ */
+int bb_decode_step(const void* q, int64_t sq, void* k, const int64_t* sk, void* v, const int64_t* sv, const void* knew,
+                   int64_t sknew, const void* vnew, int64_t svnew, int64_t* n_dev, int64_t advance, int64_t cap, int H,
+                   int Hkv, int D, int front, int window, int routed, float scale, int is_f16, int32_t* idx_out,
+                   void* out, int64_t so, void* ws, size_t ws_bytes, void* stream);
+
+size_t bb_decode_step_workspace(int64_t cap, int H, int Hkv, int D, int front, int window, int routed);
 
 /*
  * Cache compaction for kv_evict: dst[h, i, :] = src[h, idx[h, i], :] for heads x m rows of D 16-bit elements

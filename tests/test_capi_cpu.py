@@ -30,7 +30,7 @@ def test_library_exports_every_declared_function():
 
 def test_version_and_sizes():
     L = _lib.lib()
-    assert L.bb_version() == 200  # the parameter lists of include/bb_attn.h (BB_ABI_VERSION)
+    assert L.bb_version() == 201  # the parameter lists of include/bb_attn.h (BB_ABI_VERSION)
     assert L.bb_transpose_v_cols(1) == 64 and L.bb_transpose_v_cols(64) == 64 and L.bb_transpose_v_cols(65) == 128
     assert L.bb_routes_workspace(131072, 32, 8, 1, 64) > 32 * 131072 * 8
     assert L.bb_decode_workspace(131072, 32, 8, 128) > 0
@@ -172,3 +172,29 @@ def test_decode_append_and_kv_append_argument_errors():
     assert rc == -1 and "16-byte units" in L.bb_last_error().decode()
     rc = L.bb_kv_append(p, _lib.i64s(128 * 64, 129), p, s2, p, 128, p, 128, 8, 128, 64, p, 1, None)
     assert rc == -1 and "16-byte aligned" in L.bb_last_error().decode()
+    # bb_decode_step: q, sq, k, sk, v, sv, knew, skn, vnew, svn, n_dev, advance, cap, H, Hkv, D, front, window,
+    # routed, scale, is_f16, idx_out, out, so, ws, ws_bytes, stream
+    def step(**over):
+        a = dict(q=p, sq=128, k=p, sk=s2, v=p, sv=s2, knew=p, skn=128, vnew=p, svn=128, n_dev=p, advance=1, cap=64,
+                 H=32, Hkv=8, D=128, front=4, window=16, routed=8, scale=0.1, is_f16=0, idx=p, out=p, so=128, ws=p,
+                 ws_bytes=1 << 30, stream=None)
+        a.update(over)
+        return L.bb_decode_step(*a.values()), L.bb_last_error().decode()
+    assert step(knew=None) == (-1, "decode step: null argument")
+    rc, msg = step(H=24)
+    assert rc == -1 and "groups 3 unsupported" in msg
+    rc, msg = step(D=96)
+    assert rc == -1 and "head_dim 96 unsupported" in msg
+    rc, msg = step(idx=None)
+    assert rc == -1 and "index output" in msg
+    rc, msg = step(advance=-1)
+    assert rc == -1 and "advance" in msg
+    rc, msg = step(skn=129)
+    assert rc == -1 and "16-byte aligned" in msg
+    rc, msg = step(ws_bytes=16)
+    assert rc == -1 and "workspace" in msg
+    # dense (routed 0) needs no routing workspace; routed adds the routing workspace and the probabilities
+    dense = L.bb_decode_step_workspace(131072, 32, 8, 128, 64, 16384, 0)
+    routed = L.bb_decode_step_workspace(131072, 32, 8, 128, 64, 16384, 512)
+    assert 0 < dense < routed
+    assert routed >= L.bb_decode_route_workspace(131072, 32, 8, 0, 512) + 8 * 131072 * 4

@@ -217,3 +217,94 @@ def test_kv_append_matches_index_copy(dtype, dev):
     kv_append(k, v, kn, vn, full)
     torch.cuda.synchronize()
     assert torch.equal(arena, before) and int(full.item()) == cap
+
+
+@pytest.mark.parametrize("routed,dtype,d,hk", [
+    (256, torch.bfloat16, 128, 8),
+    (300, torch.float16, 128, 8),
+    (128, torch.bfloat16, 64, 4),    # head_dim 64, 8 query heads per KV head
+    (0, torch.bfloat16, 128, 8),     # dense: every cached row
+    (0, torch.float16, 64, 16),      # dense, 2 query heads per KV head
+])
+def test_decode_step_matches_separate_launches(routed, dtype, d, hk, dev):
+    """bb_decode_step (the new row appended by the first kernel that reads the cache, the length advanced by the
+    last) against the same step as separate launches: kv_append at length - 1, then routing + sparse decode (or dense
+    decode over the cache), then the length add. Bitwise on the output, the routed indices, the whole cache buffer
+    (strided views) and the length, over consecutive steps up to and past the capacity (a length past it appends
+    nothing and stays)."""
+    print(f"case decode_step routed={routed} {dtype} d={d} hk={hk}", flush=True)
+    from bigger_bird_amd.decode import decode_step
+    h, cap = 32, 5000
+    front, window = 64, 1024
+    g = torch.Generator().manual_seed(21)
+    arena = torch.randn(2, hk, cap, 2 * d, generator=g).to(dtype).to(dev)
+    ref = arena.clone()
+    k, v = arena[0, :, :, :d], arena[1, :, :, d:]  # [hk, cap, d] views, row stride 2 d
+    kr, vr = ref[0, :, :, :d], ref[1, :, :, d:]
+    scale = d ** -0.5
+    length, lref = torch.tensor([cap - 3], device=dev), torch.tensor([cap - 3], device=dev)
+    for i in range(5):  # lengths cap - 3 .. cap, then cap + 1 (no append)
+        q = torch.randn(h, d, generator=g).to(dtype).to(dev)
+        rows = torch.randn(2, hk, d, generator=g).to(dtype).to(dev)
+        kn, vn = rows[0], rows[1]
+        res = decode_step(q, k, v, kn, vn, length, routed=routed, front=front, window=window, scale=scale, advance=1)
+        kv_append(kr, vr, kn, vn, lref - 1, advance=0)
+        if routed:
+            idx_r = bigger_bird_route(q, kr, routed, front=front, window=window, scale=scale, n=lref)
+            out_r = bigger_bird_decode(q, kr, vr, idx_r, front=front, window=window, scale=scale, n=lref)
+            out, idx = res
+            assert torch.equal(idx, idx_r), i
+        else:
+            out_r = bigger_bird_decode(q, kr, vr, torch.empty(hk, 0, dtype=torch.int32, device=dev), front=0,
+                                       window=cap, scale=scale, n=lref)
+            out = res
+        appended = 1 <= int(lref.item()) <= cap
+        if appended:
+            lref.add_(1)
+        torch.cuda.synchronize()
+        assert torch.equal(out, out_r), i
+        assert torch.equal(arena, ref), i
+        assert int(length.item()) == int(lref.item()), i
+    assert int(length.item()) == cap + 1
+
+
+def test_decode_step_in_graph(dev):
+    """The fused step captured once and replayed with the length advancing on the device: every replay equals the
+    same fused step run eagerly (the kernels write the new row and the length themselves; no memset or copy nodes)."""
+    print("case decode_step_graph", flush=True)
+    from bigger_bird_amd.decode import decode_step
+    h, hk, d, cap, n0 = 32, 8, 128, 12000, 9001
+    front, window, routed = 64, 2048, 256
+    g = torch.Generator().manual_seed(12)
+    k0 = torch.randn(hk, cap, d, generator=g).to(torch.bfloat16).to(dev)
+    v0 = torch.randn(hk, cap, d, generator=g).to(torch.bfloat16).to(dev)
+    steps = [tuple(torch.randn(*shape, generator=g).to(torch.bfloat16).to(dev) for shape in ((h, d), (hk, d), (hk, d)))
+             for _ in range(4)]
+    scale = d ** -0.5
+
+    def step(k, v, length, q, kn, vn):
+        return decode_step(q, k, v, kn, vn, length, routed=routed, front=front, window=window, scale=scale, advance=1)
+
+    ke, ve, le = k0.clone(), v0.clone(), torch.tensor([n0], device=dev)
+    eager = [tuple(t.clone() for t in step(ke, ve, le, *s)) for s in steps]
+    kg, vg, lg = k0.clone(), v0.clone(), torch.tensor([n0], device=dev)
+    qs, ks_, vs_ = (torch.empty_like(t) for t in steps[0])
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step(kg.clone(), vg.clone(), lg.clone(), *steps[0])
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_g, idx_g = step(kg, vg, lg, qs, ks_, vs_)
+    for i, (q, kn, vn) in enumerate(steps):
+        qs.copy_(q)
+        ks_.copy_(kn)
+        vs_.copy_(vn)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert int(lg.item()) == n0 + i + 1
+        assert torch.equal(idx_g, eager[i][1]), i
+        assert torch.equal(out_g, eager[i][0]), i
+        _ = torch.zeros(1, device=dev).sum().item()  # unrelated eager work between replays
+    assert torch.equal(kg, ke) and torch.equal(vg, ve)

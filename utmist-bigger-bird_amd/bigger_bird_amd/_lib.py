@@ -51,6 +51,9 @@ SIGNATURES = {
     "bb_decode_route_workspace": (_sz, [_i64, _i32, _i32, _i32, _i32]),
     "bb_gather_rows": (_i32, [_vp, c_i64p, _i64, _i32, _vp, _i64, _i32, _i32, _vp, c_i64p, _vp]),
     "bb_kv_append": (_i32, [_vp, c_i64p, _vp, c_i64p, _vp, _i64, _vp, _i64, _i32, _i32, _i64, _vp, _i64, _vp]),
+    "bb_decode_step": (_i32, [_vp, _i64, _vp, c_i64p, _vp, c_i64p, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i32, _i32,
+                              _i32, _i32, _i32, _i32, _f32, _i32, _vp, _vp, _i64, _vp, _sz, _vp]),
+    "bb_decode_step_workspace": (_sz, [_i64, _i32, _i32, _i32, _i32, _i32, _i32]),
     "bb_topk_f32": (_i32, [_vp, _i64, _i32, _i64, _i32, _i32, _i32, _vp, _vp, _sz, _vp]),
     "bb_topk_f32_workspace": (_sz, [_i32, _i64]),
     "bb_argmax": (_i32, [_vp, _i64, _i32, _vp, _vp]),

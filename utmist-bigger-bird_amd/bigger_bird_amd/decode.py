@@ -149,6 +149,45 @@ def kv_append(k, v, knew, vnew, length, advance=1):
                                        _lib.stream_of(k)))
 
 
+def decode_step(q, k, v, knew, vnew, length, *, routed=0, front=64, window=4096, scale=1.0, advance=0, out=None):
+    """One decode step over a cache whose length (an int64 GPU tensor of one element) already counts the new row:
+    knew / vnew [Hkv, D] become row length - 1 of k / v [Hkv, cap, D] (a length outside [1, cap] appends nothing),
+    the token q [H, D] attends (routed > 0: top `routed` keys per KV head by pooled decode routing outside the front
+    and the last `window` keys, then sparse decode over front | window | routed; routed = 0: all rows), and length +=
+    advance afterwards (only when the row was appended). Bit-identical to kv_append(..., advance=0) at length - 1,
+    bigger_bird_route and bigger_bird_decode (or bigger_bird_decode with front 0, window cap), in two launches fewer.
+    Returns out [H, D], and the routed indices [Hkv, routed] (int32, ascending) when routed > 0."""
+    if not q.is_cuda or q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("decode_step requires CUDA FP16/BF16")
+    h, d = q.shape
+    hk, cap, _ = k.shape
+    if k.shape != v.shape or h % hk or k.shape[-1] != d:
+        raise ValueError("q [H,D] and k/v [Hkv,N,D] must match")
+    if tuple(knew.shape) != (hk, d) or tuple(vnew.shape) != (hk, d):
+        raise ValueError("decode_step: new rows must be [Hkv, D]")
+    if any(x.dtype != q.dtype for x in (k, v, knew, vnew)):
+        raise ValueError("q, k, v and the new rows must share a dtype")
+    if not isinstance(length, torch.Tensor) or length.dtype != torch.int64 or length.numel() != 1:
+        raise ValueError("decode_step: length must be one int64 GPU tensor")
+    _lib.require_gpu(k, v, knew, vnew, length, what="decode_step")
+    if any(x.stride(-1) != 1 or any(s % 8 for s in x.stride()[:-1]) or x.data_ptr() % 16 for x in (k, v, knew, vnew)):
+        raise ValueError("decode_step: k / v and the new rows need 16-byte aligned rows (the cache is written in place)")
+    q = q if q.stride(-1) == 1 else q.contiguous()
+    routed = int(routed)
+    idx = torch.empty(hk, routed, dtype=torch.int32, device=q.device) if routed > 0 else None
+    if out is None:
+        out = torch.empty(h, d, dtype=q.dtype, device=q.device)
+    L = _lib.lib()
+    ws_bytes = L.bb_decode_step_workspace(cap, h, hk, d, int(front), int(window), routed)
+    ws = _lib.workspace(ws_bytes, q.device)
+    _lib.check(L.bb_decode_step(
+        _lib.ptr(q), q.stride(0), _lib.ptr(k), _lib.i64s(*k.stride()[:2]), _lib.ptr(v), _lib.i64s(*v.stride()[:2]),
+        _lib.ptr(knew), knew.stride(0), _lib.ptr(vnew), vnew.stride(0), _lib.ptr(length), int(advance), cap, h, hk, d,
+        int(front), int(window), routed, float(scale), int(q.dtype == torch.float16), _lib.ptr(idx), _lib.ptr(out),
+        out.stride(0), _lib.ptr(ws), ws_bytes, _lib.stream_of(q)))
+    return (out, idx) if routed > 0 else out
+
+
 def topk_columns(vals, budget, *, front=0, tail=0):
     """Per row of vals [rows, n] (fp32): the `budget` columns of [front, n - tail) with the largest values (values
     <= 0 and NaN last, ties to the lower index), ascending int32 [rows, budget], -1 past the eligible count: the

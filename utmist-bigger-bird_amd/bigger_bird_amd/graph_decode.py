@@ -14,12 +14,14 @@ generate / EOS / rewind / feed protocol. The design is this package's own:
   shape and reads its varying values from device memory: the step is captured once and replayed per token.
 * Step (one token through the model): embedding; per layer RMSNorm -> one fused QKV projection (the q, k and v
   weights concatenated once at construction when they are plain bias-free Linear layers of one dtype) -> RoPE on q and
-  k in place -> the new K and V row into the arena at `slot` (one bb_kv_append) -> attention -> o_proj, residual ->
-  RMSNorm -> MLP, residual; final norm, lm_head, greedy token by a one-workgroup HIP argmax written straight into
-  the control block.
-* Attention per layer: split-K flash decoding over the filled rows (bigger_bird_decode with front 0, window =
-  capacity, no routes, length read on the GPU). `sparse_decode={"front", "window", "routed"}` switches the
-  non-dense RDAttention layers to fused decode routing (bigger_bird_route, pooled per KV head) + sparse decode.
+  k in place -> attention, which also writes the new K and V row into the arena at `slot` = n - 1 -> o_proj,
+  residual -> RMSNorm -> MLP, residual; final norm, lm_head, greedy token by a one-workgroup HIP argmax written
+  straight into the control block.
+* Attention per layer: one bb_decode_step. Dense layers run split-K flash decoding over the filled rows (front 0,
+  window = capacity, no routes, length read on the GPU); `sparse_decode={"front", "window", "routed"}` switches the
+  non-dense RDAttention layers to fused decode routing (pooled per KV head) + sparse decode. The first kernel that
+  reads the cache takes the new row from the projection output and stores it in the arena, so the append needs no
+  launch of its own (bit-identical to bb_kv_append followed by bigger_bird_decode / bigger_bird_route).
 * On bf16 / fp16 models the RMSNorms run as one bb_rms_norm launch each and RoPE as bb_rope_inplace (bit-identical to
   HF apply_rotary_pos_emb): at batch 1 the HF modules' elementwise launches cost more than their arithmetic.
 * A captured step holds no memset node and no multi-workgroup reduction of torch's (those have given wrong results
@@ -34,7 +36,7 @@ from transformers.cache_utils import DynamicLayer
 from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
 
 from .attention import rope_inplace
-from .decode import argmax_index, bigger_bird_decode, bigger_bird_route, kv_append, rms_norm
+from .decode import argmax_index, decode_step, rms_norm
 
 # Control block: slot indices and the per-step / per-token increments.
 N, POS, TOK, MADE, SLOT = range(5)
@@ -210,17 +212,15 @@ class StaticDecoder:
             kv = None
         return q.view(1, h, 1, d), k.view(1, hk, 1, d), v.view(1, hk, 1, d), kv
 
-    def _attend(self, i, plan, q):
-        """q [H, d] of the new token (its K/V row already in the arena) -> [H, d]."""
+    def _attend(self, i, plan, q, kn, vn):
+        """q [H, d] of the new token, its K / V rows kn / vn [Hkv, d] -> [H, d]. The rows become arena row
+        length - 1 (the write slot: the step's claim has already counted them) inside the step's first kernel."""
         K, V = self.k[i], self.v[i]
         if not plan.sparse:
-            return bigger_bird_decode(q, K, V, self.no_routes, front=0, window=self.capacity, scale=plan.scaling,
-                                      n=self.length)
+            return decode_step(q, K, V, kn, vn, self.length, routed=0, scale=plan.scaling)
         c = self.sparse_cfg
-        idx = bigger_bird_route(q, K, c["routed"], front=c["front"], window=c["window"], scale=plan.scaling,
-                                n=self.length)
-        return bigger_bird_decode(q, K, V, idx, front=c["front"], window=c["window"], scale=plan.scaling,
-                                  n=self.length)
+        return decode_step(q, K, V, kn, vn, self.length, routed=c["routed"], front=c["front"], window=c["window"],
+                           scale=plan.scaling)[0]
 
     def step(self):
         """One greedy token: fixed shapes, all varying state read from the control block (capturable)."""
@@ -238,8 +238,7 @@ class StaticDecoder:
                 kv = None
             if kv is None:
                 kv = torch.stack((k[0], v[0]))
-            kv_append(self.arena[i][0], self.arena[i][1], kv[0, :, 0], kv[1, :, 0], self._slot, advance=0)
-            o = self._attend(i, plan, q[0, :, 0])
+            o = self._attend(i, plan, q[0, :, 0], kv[0, :, 0], kv[1, :, 0])
             hid = hid + plan.base.o_proj(o.reshape(1, 1, -1))
             hid = hid + layer.mlp(self._norm(layer.post_attention_layernorm, hid))
         self.logits = self.model.lm_head(self._norm(self.core.norm, hid))[0, -1]

@@ -587,10 +587,24 @@ size_t bb_decode_route_workspace(int64_t cap, int H, int Hkv, int splits, int k_
   return b;
 }
 
+// Decode routing for bb_decode_route and bb_decode_step (app: the step's new row, appended by the scores pass).
+static int route_impl(const void* q, int64_t sq, const void* k, const int64_t* sk, int64_t n, const int64_t* n_dev,
+                      int64_t cap, int H, int Hkv, int D, int front, int window, float scale, int splits, int is_f16,
+                      float* probs_out, int k_route, int32_t* idx_out, void* ws, size_t ws_bytes,
+                      const bb::RowAppend* app, hipStream_t st);
+
 int bb_decode_route(const void* q, int64_t sq, const void* k, const int64_t* sk, int64_t n, const int64_t* n_dev,
                     int64_t cap, int H, int Hkv, int D, int front, int window, float scale, int splits, int is_f16,
                     float* probs_out, int k_route, int32_t* idx_out, void* ws, size_t ws_bytes, void* stream) {
   g_err[0] = 0;
+  return route_impl(q, sq, k, sk, n, n_dev, cap, H, Hkv, D, front, window, scale, splits, is_f16, probs_out, k_route,
+                    idx_out, ws, ws_bytes, nullptr, static_cast<hipStream_t>(stream));
+}
+
+static int route_impl(const void* q, int64_t sq, const void* k, const int64_t* sk, int64_t n, const int64_t* n_dev,
+                      int64_t cap, int H, int Hkv, int D, int front, int window, float scale, int splits, int is_f16,
+                      float* probs_out, int k_route, int32_t* idx_out, void* ws, size_t ws_bytes,
+                      const bb::RowAppend* app, hipStream_t st) {
   if (!q || !k || !sk || !probs_out) return fail("q [H,D] and k [Hkv,CAP,D] must match");
   if (H <= 0 || Hkv <= 0 || H % Hkv || cap <= 0) return fail("q [H,D] and k [Hkv,CAP,D] must match");
   const int G = H / Hkv;
@@ -625,7 +639,7 @@ int bb_decode_route(const void* q, int64_t sq, const void* k, const int64_t* sk,
     w += align256((size_t)Hkv * cap * 8);
     bb::topk_hist_meta(w, cap, Hkv, &p.top_hist, &p.top_meta);  // filled by the pool pass
   }
-  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (app) p.app = *app;
   int rc = hip_status(bb::launch_decode_route_probs(p, st), "bb_decode_route");
   if (rc != BB_OK || k_route == 0) return rc;
   return hip_status(bb::launch_topk_rows(p.keys, Hkv, cap, p.n, n_dev, front, window, k_route, idx_out, w,
@@ -648,6 +662,80 @@ int bb_kv_append(void* k, const int64_t* sk, void* v, const int64_t* sv, const v
                                          static_cast<const uint16_t*>(vnew), svnew, Hkv, D, cap, n_dev, n_inc,
                                          static_cast<hipStream_t>(stream)),
                     "bb_kv_append");
+}
+
+size_t bb_decode_step_workspace(int64_t cap, int H, int Hkv, int D, int front, int window, int routed) {
+  if (cap <= 0 || H <= 0 || Hkv <= 0 || H % Hkv || routed < 0) return 0;
+  const int fr = routed > 0 ? front : 0, win = routed > 0 ? window : (int)std::min<int64_t>(cap, 0x7fffffff);
+  size_t b = align256(bb_sparse_decode_workspace(H, Hkv, D, Hkv, fr, win, routed, 0));
+  if (routed > 0) b += align256((size_t)Hkv * cap * 4) + bb_decode_route_workspace(cap, H, Hkv, 0, routed);
+  return b;
+}
+
+int bb_decode_step(const void* q, int64_t sq, void* k, const int64_t* sk, void* v, const int64_t* sv, const void* knew,
+                   int64_t sknew, const void* vnew, int64_t svnew, int64_t* n_dev, int64_t advance, int64_t cap, int H,
+                   int Hkv, int D, int front, int window, int routed, float scale, int is_f16, int32_t* idx_out,
+                   void* out, int64_t so, void* ws, size_t ws_bytes, void* stream) {
+  g_err[0] = 0;
+  if (!q || !k || !v || !sk || !sv || !knew || !vnew || !n_dev || !out) return fail("decode step: null argument");
+  if (H <= 0 || Hkv <= 0 || H % Hkv || cap <= 0) return fail("q [H,D] and k/v [Hkv,N,D] must match");
+  const int G = H / Hkv;
+  if (G != 1 && G != 2 && G != 4 && G != 8) return fail("decode: groups %d unsupported", G);
+  if (D != 64 && D != 128) return fail("decode: head_dim %d unsupported (64 or 128)", D);
+  if (routed < 0 || (routed > 0 && !idx_out)) return fail("decode step: routed must be >= 0 with an index output");
+  if (routed > 0 && (front < 0 || window < 0)) return fail("front >= 0 and window >= 0 required");
+  if (!(scale > 0.0f)) return fail("scale must be positive");
+  if (advance < 0) return fail("decode step: advance must be >= 0");
+  if (!aligned(q, 2) || !aligned(k, 16) || !aligned(v, 16) || !aligned(knew, 16) || !aligned(vnew, 16) || sk[0] % 8 ||
+      sk[1] % 8 || sv[0] % 8 || sv[1] % 8 || sknew % 8 || svnew % 8)
+    return fail("q/k/v need a contiguous head_dim and 16-byte aligned rows");
+  if (!aligned(n_dev, 8)) return fail("decode step: misaligned length");
+  const size_t need = bb_decode_step_workspace(cap, H, Hkv, D, front, window, routed);
+  if (!ws || ws_bytes < need) return fail("workspace of %zu bytes required", need);
+  bb::RowAppend app;
+  app.knew = static_cast<const uint16_t*>(knew);
+  app.vnew = static_cast<const uint16_t*>(vnew);
+  app.k = static_cast<uint16_t*>(k);
+  app.v = static_cast<uint16_t*>(v);
+  app.skn = sknew; app.svn = svnew; app.sk0 = sk[0]; app.sk1 = sk[1]; app.sv0 = sv[0]; app.sv1 = sv[1];
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  char* w = static_cast<char*>(ws);
+  const int fr = routed > 0 ? front : 0, win = routed > 0 ? window : (int)std::min<int64_t>(cap, 0x7fffffff);
+  const size_t part_bytes = bb_sparse_decode_workspace(H, Hkv, D, Hkv, fr, win, routed, 0);
+  float* part = reinterpret_cast<float*>(w);
+  w += align256(part_bytes);
+  if (routed > 0) {  // decode routing appends the row (its scores pass is the first to read the cache)
+    float* probs = reinterpret_cast<float*>(w);
+    w += align256((size_t)Hkv * cap * 4);
+    const size_t rws = bb_decode_route_workspace(cap, H, Hkv, 0, routed);
+    int rc = route_impl(q, sq, k, sk, cap, n_dev, cap, H, Hkv, D, front, window, scale, 0, is_f16, probs, routed,
+                        idx_out, w, rws, &app, st);
+    if (rc != BB_OK) return rc;
+  }
+  bb::SparseDecodeParams p;
+  memset(&p, 0, sizeof(p));
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.idx = routed > 0 ? idx_out : nullptr;
+  p.n_dev = n_dev;
+  p.out = static_cast<uint16_t*>(out);
+  p.sq = sq; p.sk0 = sk[0]; p.sk1 = sk[1]; p.sv0 = sv[0]; p.sv1 = sv[1];
+  p.si0 = routed; p.si1 = 1;
+  p.so = so;
+  p.n = cap;
+  p.cap = cap;
+  p.H = H; p.Hkv = Hkv; p.G = G; p.D = D; p.rows = Hkv;
+  p.front = fr; p.window = win; p.route_k = routed; p.f16 = is_f16 ? 1 : 0;
+  const int64_t total = (int64_t)fr + win + routed;
+  p.split_len = decode_chunk_len(total, Hkv, 0, 0);
+  p.n_splits = (int)cdiv(total > 0 ? total : 1, p.split_len);
+  p.c = (float)((double)scale * 1.4426950408889634);
+  p.part = part;
+  if (routed == 0) p.app = app;  // dense: the decode kernel is the first to read the cache
+  p.n_advance = advance > 0 ? n_dev : nullptr;
+  p.advance = advance;
+  return hip_status(bb::launch_sparse_decode(p, st), "bb_decode_step");
 }
 
 int bb_gather_rows(const void* src, const int64_t* ss, int64_t n_src, int heads, const int64_t* idx, int64_t si0, int m,

@@ -51,6 +51,24 @@ BB_DEV int64_t current_length(int64_t n, const int64_t* n_dev, int64_t cap) {
   return v < 0 ? 0 : v;
 }
 
+// Position of the step's new row (RowAppend): n - 1 when it is appended (1 <= n <= cap), else -1.
+BB_DEV int64_t appended_row(const RowAppend& a, int64_t n, const int64_t* n_dev, int64_t cap) {
+  const int64_t v = n_dev ? *n_dev : n;
+  return a.knew && v >= 1 && v <= cap ? v - 1 : -1;
+}
+
+// The 16-byte units [DPL sub, DPL (sub + 1)) of the new K row of KV head kv (already loaded into kw) and of its V row
+// to cache row j: each of the 8 lanes of the key slot that read the row writes its own units.
+template <int DPL>
+BB_DEV void store_appended(const RowAppend& a, int kv, int64_t j, int sub, const u32x4_t (&kw)[DPL / 8]) {
+#pragma unroll
+  for (int e0 = 0; e0 < DPL / 8; ++e0) {
+    st16(a.k + (int64_t)kv * a.sk0 + j * a.sk1 + DPL * sub + 8 * e0, kw[e0]);
+    st16(a.v + (int64_t)kv * a.sv0 + j * a.sv1 + DPL * sub + 8 * e0,
+         ld16(a.vnew + (int64_t)kv * a.svn + DPL * sub + 8 * e0));
+  }
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // Sparse split-K decode. Workgroup (split, route row r): 4 waves, 8 lanes per key (D / 8 values each), 32 key slots,
 // two keys per slot and step (their K and V rows in flight together). Route row r holds GR query heads (GR = groups
@@ -73,6 +91,7 @@ __global__ __launch_bounds__(kSdThreads) void sparse_decode_kernel(SparseDecodeP
   const int kslot = lane / LPK, sub = lane % LPK;
   const int slot = wave * KPW + kslot;
   const int64_t n = current_length(p.n, p.n_dev, p.cap);
+  const int64_t jnew = appended_row(p.app, p.n, p.n_dev, p.cap);  // read from the new rows, -1: none
   const int kv = (r * GR) / p.G;
   const int64_t total = (int64_t)p.front + p.window + p.route_k;
   const int64_t j_begin = (int64_t)split * p.split_len;
@@ -107,15 +126,20 @@ __global__ __launch_bounds__(kSdThreads) void sparse_decode_kernel(SparseDecodeP
     }
     u32x4_t kw[2][DPL / 8], vw[2][DPL / 8];
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int u = 0; u < 2; ++u) {
+      const bool fresh = ok[u] && pos[u] == jnew;
+      const uint16_t* ks = fresh ? p.app.knew + (int64_t)kv * p.app.skn + DPL * sub : kbase + pos[u] * p.sk1;
+      const uint16_t* vs = fresh ? p.app.vnew + (int64_t)kv * p.app.svn + DPL * sub : vbase + pos[u] * p.sv1;
 #pragma unroll
       for (int e0 = 0; e0 < DPL / 8; ++e0) {
-        kw[u][e0] = ld16(kbase + pos[u] * p.sk1 + 8 * e0);
-        vw[u][e0] = ld16(vbase + pos[u] * p.sv1 + 8 * e0);
+        kw[u][e0] = ld16(ks + 8 * e0);
+        vw[u][e0] = ld16(vs + 8 * e0);
       }
+    }
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       if (!ok[u]) continue;
+      if (pos[u] == jnew) store_appended<DPL>(p.app, kv, jnew, sub, kw[u]);
       float s[GR];
 #pragma unroll
       for (int h = 0; h < GR; ++h) {
@@ -240,6 +264,11 @@ __global__ __launch_bounds__(kSdMergeThreads) void sparse_merge_kernel(SparseDec
     }
     p.out[(int64_t)h * p.so + d] = f32_to_elem<F16>(ot / fmaxf(lt, 1.0e-30f));
   }
+  // the step's length advance: no workgroup of this kernel reads the length
+  if (p.n_advance && h == 0 && t == 0) {
+    const int64_t n = *p.n_advance;
+    if (n >= 1 && n <= p.cap) *p.n_advance = n + p.advance;
+  }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -262,6 +291,7 @@ __global__ __launch_bounds__(kSdThreads) void route_scores_kernel(DecodeRoutePar
     if (tid < kTopMetaWords) p.top_meta[(int64_t)kv * kTopMetaWords + tid] = 0u;
   }
   const int64_t n = current_length(p.n, p.n_dev, p.cap);
+  const int64_t jnew = appended_row(p.app, p.n, p.n_dev, p.cap);  // read from the new row, -1: none
   const int64_t j_begin = (int64_t)split * p.split_len;
   const int64_t j_end = j_begin + p.split_len < n ? j_begin + p.split_len : n;
   uint32_t qw[G][DPL / 2];
@@ -279,14 +309,16 @@ __global__ __launch_bounds__(kSdThreads) void route_scores_kernel(DecodeRoutePar
     u32x4_t kw[U][DPL / 8];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t j = j0 + u * SLOTS;
+      const int64_t j = j0 + u * SLOTS < j_end ? j0 + u * SLOTS : j0;
+      const uint16_t* ks = j == jnew ? p.app.knew + (int64_t)kv * p.app.skn + DPL * sub : kbase + j * p.sk1;
 #pragma unroll
-      for (int e0 = 0; e0 < DPL / 8; ++e0) kw[u][e0] = ld16(kbase + (j < j_end ? j : j0) * p.sk1 + 8 * e0);
+      for (int e0 = 0; e0 < DPL / 8; ++e0) kw[u][e0] = ld16(ks + 8 * e0);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t j = j0 + u * SLOTS;
       if (j >= j_end) break;  // the 8 lanes of a key slot agree
+      if (j == jnew) store_appended<DPL>(p.app, kv, jnew, sub, kw[u]);
       float sc[G];
 #pragma unroll
       for (int h = 0; h < G; ++h) {

@@ -103,6 +103,18 @@ size_t decode_workspace_bytes(int H, int D, int n_splits);
 bool decode_fuses_append(const DecodeParams& p);
 hipError_t launch_decode(const DecodeParams& p, hipStream_t stream);
 
+// A decode step's new K / V row folded into the first kernel that reads the cache: the row at position n - 1 (n the
+// current length, which already counts it) is read from knew / vnew instead of the cache, and the lanes that read it
+// also write it to the cache rows (k, v), so that later kernels find it there. Only when 1 <= n <= cap; knew = null
+// switches it off.
+struct RowAppend {
+  const uint16_t* knew;  // [Hkv, D] (head stride skn)
+  const uint16_t* vnew;  // [Hkv, D] (head stride svn)
+  uint16_t* k;           // the cache [Hkv, cap, D] (strides sk0 head, sk1 token), writable
+  uint16_t* v;           // (strides sv0, sv1)
+  int64_t skn, svn, sk0, sk1, sv0, sv1;
+};
+
 // Split-K sparse decode over a bf16 / fp16 KV cache (front | window | routed keys per route row).
 struct SparseDecodeParams {
   const uint16_t* q;     // [H, D] (row stride sq)
@@ -116,6 +128,9 @@ struct SparseDecodeParams {
   int64_t n, cap, split_len;
   int H, Hkv, G, D, rows, front, window, route_k, n_splits, f16;
   float c;               // scale * log2(e)
+  RowAppend app;         // the step's new row (dense decode without routing), or app.knew = null
+  int64_t* n_advance;    // after the merge: *n_advance += advance when the row was appended (n_advance = n_dev), or null
+  int64_t advance;
 };
 hipError_t launch_sparse_decode(const SparseDecodeParams& p, hipStream_t stream);
 
@@ -135,6 +150,7 @@ struct DecodeRouteParams {
   int64_t n, cap, split_len;
   int H, Hkv, D, front, window, n_splits, f16;
   float c;
+  RowAppend app;         // the step's new row (the scores pass appends it), or app.knew = null
 };
 hipError_t launch_decode_route_probs(const DecodeRouteParams& p, hipStream_t stream);
 // Top-`budget` of 64-bit keys per row over [front, n - window) (n from n_dev when set), ascending int32 indices;
