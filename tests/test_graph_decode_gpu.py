@@ -25,7 +25,7 @@ EVICT = dict(kv_evict=True)
 N, STEPS = 400, 12
 
 
-def _tiny(dev):
+def _tiny(dev, dtype=torch.bfloat16):
     from transformers import LlamaConfig, LlamaForCausalLM
 
     # head_dim 64: the decode kernels take 64 or 128
@@ -33,7 +33,7 @@ def _tiny(dev):
                       num_attention_heads=8, num_key_value_heads=2, max_position_embeddings=8192,
                       attn_implementation="sdpa")
     torch.manual_seed(0)
-    return LlamaForCausalLM(cfg).to(dev, torch.bfloat16).eval()
+    return LlamaForCausalLM(cfg).to(dev, dtype).eval()
 
 
 def _ids(dev):
@@ -44,11 +44,12 @@ def _ids(dev):
 SPARSE = dict(front=8, window=64, routed=32)
 
 
-@pytest.mark.parametrize("arm,extra,sparse", [("dense_rd", {}, None), ("rd", {}, None), ("rd", EVICT, None),
-                                              ("rd", {}, SPARSE)])
-def test_graph_matches_eager_step_bitwise(arm, extra, sparse, dev):
-    print(f"case graph_vs_eager_step {arm} evict={bool(extra)} sparse={bool(sparse)}", flush=True)
-    model = _tiny(dev)
+@pytest.mark.parametrize("arm,extra,sparse,dtype", [("dense_rd", {}, None, torch.bfloat16), ("rd", {}, None, torch.bfloat16),
+                                                    ("rd", EVICT, None, torch.bfloat16), ("rd", {}, SPARSE, torch.bfloat16),
+                                                    ("rd", {}, SPARSE, torch.float16)])
+def test_graph_matches_eager_step_bitwise(arm, extra, sparse, dtype, dev):
+    print(f"case graph_vs_eager_step {arm} evict={bool(extra)} sparse={bool(sparse)} {dtype}", flush=True)
+    model = _tiny(dev, dtype)
     install(model, arm, **KW, **extra)
     ids = _ids(dev)
     dec, out, _ = graph_prefill(model, ids, STEPS + 4, headroom=64, sparse_decode=sparse)

@@ -6,7 +6,8 @@ same layer input with the same projections, the HF rotary embedding and the mask
   * "rd": sink | window | the layer's chosen routes (before the window) for rows below n - exact_tail, causal for the
     exact tail (modal_rd/attention.py:176-206);
   * one decode step after the prefill: attention of the new token over every cached key.
-Bar: max-abs 2e-2 and mean-abs 2e-3 per layer. Logits are not compared across precisions: with the enlarged q/k
+The model runs in bf16 and in fp16 (routes, RoPE, the flash kernels and decode on fp16 inputs). Bar: max-abs 2e-2
+and mean-abs 2e-3 per layer. Logits are not compared across precisions: with the enlarged q/k
 projections below the bf16 and float32 models diverge by themselves (last-token cosine 0.17 for HF's own bf16 model),
 so the per-layer comparison from a common bf16 input is the meaningful one.
 """
@@ -21,7 +22,7 @@ T = 2048
 SPARSE = dict(sink=64, window=512, vertical=128, exact_tail=64)
 
 
-def _model(dev):
+def _model(dev, dtype=torch.bfloat16):
     from transformers import LlamaConfig, LlamaForCausalLM
 
     cfg = LlamaConfig(vocab_size=512, hidden_size=1024, intermediate_size=1024, num_hidden_layers=2,
@@ -34,7 +35,7 @@ def _model(dev):
         for layer in m32.model.layers:
             layer.self_attn.q_proj.weight.mul_(4.0)
             layer.self_attn.k_proj.weight.mul_(4.0)
-    return m32.to(dev, torch.bfloat16)
+    return m32.to(dev, dtype)
 
 
 class _Capture:
@@ -134,10 +135,11 @@ def _check(calls, mask_fn, what):
         assert err.max().item() <= 2e-2 and err.mean().item() <= 2e-3, (what, c["layer"])
 
 
-@pytest.mark.parametrize("arm", ["dense_rd", "rd"])
-def test_installed_model_layers_match_reference(arm, dev):
-    print(f"case model {arm} T={T}", flush=True)
-    mbf = _model(dev)
+@pytest.mark.parametrize("arm,dtype", [("dense_rd", torch.bfloat16), ("rd", torch.bfloat16), ("dense_rd", torch.float16),
+                                       ("rd", torch.float16)])
+def test_installed_model_layers_match_reference(arm, dtype, dev):
+    print(f"case model {arm} {dtype} T={T}", flush=True)
+    mbf = _model(dev, dtype)
     g = torch.Generator(device=dev).manual_seed(1)
     ids = torch.randint(0, 512, (1, T + 1), generator=g, device=dev)
     install(mbf, arm, **SPARSE)

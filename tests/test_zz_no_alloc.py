@@ -1,8 +1,6 @@
 """bb_decode_noalloc (static device scratch, no workspace argument, no allocation) against bb_decode (caller
 workspace) through the C ABI: same kernels, so the outputs must be bitwise equal. Two calls in a row, the second
 over a smaller cache (fewer splits), so a stale partial left by the first call would show; plus the size limit."""
-import ctypes
-
 import pytest
 import torch
 

@@ -146,7 +146,7 @@ class StaticDecoder:
             self.k = [self.arena[i, 0] for i in range(len(layers))]
             self.v = [self.arena[i, 1] for i in range(len(layers))]
             self.length, self.position = self.ctl[N:N + 1], self.ctl[POS:POS + 1]
-            self.step_i, self._slot = self.ctl[MADE:MADE + 1], self.ctl[SLOT:SLOT + 1]
+            self.step_i = self.ctl[MADE:MADE + 1]
             self.token = self.ctl[TOK:TOK + 1].view(1, 1)
             self._token_flat = self.ctl[TOK:TOK + 1]
         self.plans = [_LayerPlan(layer, layer.self_attn,
