@@ -112,21 +112,40 @@ __global__ __launch_bounds__(256) void scores_kernel(RoutesParams p, RouteGeom g
   const uint16_t* kbase = p.k + (int64_t)bkv * p.sk0;
   uint16_t* srow_base = p.scores + (int64_t)bkv * g.rows * g.ns;
 
+  // K blocks: thread t holds the 16-byte units t, t + 256, ... of a block; the next block's loads are in flight
+  // while the current one is scored
+  constexpr int KPT = (kScoreKeys * (D / 8) + 255) / 256;
+  auto kload = [&](int it, u32x4_t (&dst)[KPT]) {
+    const int64_t jb = ((int64_t)kchunk * kScoreIters + it) * kScoreKeys;
+#pragma unroll
+    for (int u = 0; u < KPT; ++u) {
+      const int e = tid + 256 * u;
+      const int64_t j = jb + e / (D / 8);
+      dst[u] = e < kScoreKeys * (D / 8) && j < p.n ? ld16(kbase + j * p.sk1 + 8 * (e % (D / 8))) : u32x4_t{0, 0, 0, 0};
+    }
+  };
+  u32x4_t knext[KPT];
+  kload(0, knext);
+
   for (int it = 0; it < kScoreIters; ++it) {
     const int64_t j0 = ((int64_t)kchunk * kScoreIters + it) * kScoreKeys;
     if (j0 >= p.n) break;
     __syncthreads();  // previous block's K^T fully consumed (and Q^T staged on the first pass)
-    for (int e = tid; e < kScoreKeys * (D / 8); e += 256) {
-      const int key = e / (D / 8), c8 = e % (D / 8);
-      const int64_t j = j0 + key;
-      const u32x4_t v = j < p.n ? ld16(kbase + j * p.sk1 + 8 * c8) : u32x4_t{0, 0, 0, 0};
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        ks[8 * c8 + 2 * w][key] = score_f32<F16>((uint16_t)(v[w] & 0xffffu));
-        ks[8 * c8 + 2 * w + 1][key] = score_f32<F16>((uint16_t)(v[w] >> 16));
+    for (int u = 0; u < KPT; ++u) {
+      const int e = tid + 256 * u;
+      if (e < kScoreKeys * (D / 8)) {
+        const int key = e / (D / 8), c8 = e % (D / 8);
+        const u32x4_t v = knext[u];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          ks[8 * c8 + 2 * w][key] = score_f32<F16>((uint16_t)(v[w] & 0xffffu));
+          ks[8 * c8 + 2 * w + 1][key] = score_f32<F16>((uint16_t)(v[w] >> 16));
+        }
       }
     }
     __syncthreads();
+    if (it + 1 < kScoreIters) kload(it + 1, knext);
 
     float acc[8][4];
 #pragma unroll
