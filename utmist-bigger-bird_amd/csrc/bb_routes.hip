@@ -71,12 +71,31 @@ struct RouteGeom {
 // 32-element block of d, two sequential fp32 chains over the even and the odd elements (fmaf of two bf16 values is
 // one rounding of the exact product sum), then acc = acc + (even + odd); for fp16 inputs (F16) one sequential chain
 // over d (an fp16 product is exact in fp32 as well) and the result rounded to fp16.
+// LDS of scores_kernel. bf16: K^T staged in fp32 (the chains take fp32 operands). fp16: K^T kept in fp16 (the FMAs take
+// fp16 operands directly) and the row-max partials share its space after the last block, so that two workgroups fit
+// a CU (74 KB each at head_dim 128).
+template <int D, bool F16>
+struct ScoresSmem {
+  uint16_t qs[D][kMaxRows];                              // Q^T (16-bit)
+  float ks[D][kScoreKeys + 4];                           // K^T (fp32), padded rows
+  float rmax_part[kMaxRows][kScoreKeys / 4 + 1];
+};
+template <int D>
+struct ScoresSmem<D, true> {
+  uint16_t qs[D][kMaxRows];
+  union {
+    uint16_t ks[D][kScoreKeys + 8];                      // K^T (fp16), padded rows
+    float rmax_part[kMaxRows][kScoreKeys / 4 + 1];       // after the last block
+  };
+};
+
 template <int D, bool F16>
 __global__ __launch_bounds__(256) void scores_kernel(RoutesParams p, RouteGeom g, float* __restrict__ pmax) {
   static_assert(D % 32 == 0, "head_dim must be a multiple of 32");
-  __shared__ __attribute__((aligned(16))) uint16_t qs[D][kMaxRows];        // Q^T (bf16)
-  __shared__ __attribute__((aligned(16))) float ks[D][kScoreKeys + 4];     // K^T (fp32), padded rows
-  __shared__ float rmax_part[kMaxRows][kScoreKeys / 4 + 1];
+  __shared__ __attribute__((aligned(16))) ScoresSmem<D, F16> sm;
+  auto& qs = sm.qs;
+  auto& ks = sm.ks;
+  auto& rmax_part = sm.rmax_part;
   const int tid = threadIdx.x;
   const int kchunk = blockIdx.x, rblk = blockIdx.y, bkv = blockIdx.z;
   const int batch = bkv / p.Hkv, kvh = bkv % p.Hkv;
@@ -139,8 +158,13 @@ __global__ __launch_bounds__(256) void scores_kernel(RoutesParams p, RouteGeom g
         const u32x4_t v = knext[u];
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-          ks[8 * c8 + 2 * w][key] = score_f32<F16>((uint16_t)(v[w] & 0xffffu));
-          ks[8 * c8 + 2 * w + 1][key] = score_f32<F16>((uint16_t)(v[w] >> 16));
+          if constexpr (F16) {
+            ks[8 * c8 + 2 * w][key] = (uint16_t)(v[w] & 0xffffu);
+            ks[8 * c8 + 2 * w + 1][key] = (uint16_t)(v[w] >> 16);
+          } else {
+            ks[8 * c8 + 2 * w][key] = bf16_to_f32((uint16_t)(v[w] & 0xffffu));
+            ks[8 * c8 + 2 * w + 1][key] = bf16_to_f32((uint16_t)(v[w] >> 16));
+          }
         }
       }
     }
@@ -156,12 +180,13 @@ __global__ __launch_bounds__(256) void scores_kernel(RoutesParams p, RouteGeom g
 #pragma unroll 2
       for (int dd = 0; dd < D; ++dd) {
         const u32x4_t qv = *reinterpret_cast<const u32x4_t*>(&qs[dd][8 * rg]);
-        const f32x4_t kv = *reinterpret_cast<const f32x4_t*>(&ks[dd][4 * kg]);
+        const u32x2_t kv = *reinterpret_cast<const u32x2_t*>(&ks[dd][4 * kg]);
 #pragma unroll
         for (int a = 0; a < 8; ++a) {
           const float fq = score_f32<true>((uint16_t)(qv[a >> 1] >> (16 * (a & 1))));
 #pragma unroll
-          for (int b = 0; b < 4; ++b) acc[a][b] = __builtin_fmaf(fq, kv[b], acc[a][b]);
+          for (int b = 0; b < 4; ++b)
+            acc[a][b] = __builtin_fmaf(fq, score_f32<true>((uint16_t)(kv[b >> 1] >> (16 * (b & 1)))), acc[a][b]);
         }
       }
     }
@@ -221,6 +246,7 @@ __global__ __launch_bounds__(256) void scores_kernel(RoutesParams p, RouteGeom g
       }
     }
   }
+  if constexpr (F16) __syncthreads();  // rmax_part shares the K^T space
 #pragma unroll
   for (int a = 0; a < 8; ++a) rmax_part[8 * rg + a][kg] = rmax[a];
   __syncthreads();
