@@ -161,3 +161,50 @@ def test_installed_model_layers_match_reference(arm, dtype, dev):
                     assert r.shape[0] == 8 and r.shape[1] > 0 and bool((r[:, 1:] > r[:, :-1]).all())
     finally:
         cap.close()
+
+
+def test_autograd_mode_as_the_reference(dev):
+    """forward with autograd on (modal_rd/attention.py:118-119, 140-141): exact layers run RoPE out of place and
+    torch's differentiable SDPA, so an installed dense_rd model backpropagates like the unmodified HF model (same
+    loss, same weight gradients within float32 rounding); sparse layers run the HIP prefill forward-only, so their
+    logits equal the inference-mode logits bit for bit and no gradient reaches q / k / v through them."""
+    import copy
+
+    print("case model autograd", flush=True)
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    cfg = LlamaConfig(vocab_size=256, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=4096,
+                      rope_theta=500000.0, attn_implementation="sdpa")
+    torch.manual_seed(3)
+    ref = LlamaForCausalLM(cfg).to(dev).train(False)
+    mine = copy.deepcopy(ref)
+    install(mine, "dense_rd", **SPARSE)
+    ids = torch.randint(0, 256, (1, 300), device=dev)
+    losses, grads = [], []
+    for m in (ref, mine):
+        m.zero_grad()
+        loss = m(input_ids=ids, use_cache=False).logits.float().square().mean()
+        loss.backward()
+        losses.append(loss.item())
+        grads.append({n: p.grad.clone() for n, p in m.named_parameters() if p.grad is not None})
+    assert abs(losses[0] - losses[1]) <= 1e-5 * abs(losses[0])
+    assert set(grads[0]) == set(grads[1])
+    for name, g0 in grads[0].items():
+        torch.testing.assert_close(grads[1][name], g0, rtol=1e-3, atol=1e-6, msg=name)
+
+    # sparse layers (bf16, T > sink + window): forward-only through the HIP path
+    mbf = _model(dev)
+    install(mbf, "rd", **SPARSE)
+    g = torch.Generator(device=dev).manual_seed(2)
+    ids = torch.randint(0, 512, (1, T), generator=g, device=dev)
+    with torch.inference_mode():
+        want = mbf(input_ids=ids, use_cache=False).logits
+    mbf.zero_grad()
+    out = mbf(input_ids=ids, use_cache=False).logits
+    assert torch.equal(out.detach(), want)
+    out.float().square().mean().backward()
+    for layer in mbf.model.layers:
+        a = layer.self_attn
+        assert a.o_proj.weight.grad is not None and a.o_proj.weight.grad.abs().sum() > 0
+        assert a.q_proj.weight.grad is None or not a.q_proj.weight.grad.any()

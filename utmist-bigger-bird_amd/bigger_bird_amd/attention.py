@@ -156,7 +156,7 @@ class RDAttention(nn.Module):
         k = self.k_proj(hidden_states).view(b, t, self.num_kv_heads, self.head_dim).transpose(1, 2)
         v = self.v_proj(hidden_states).view(b, t, self.num_kv_heads, self.head_dim).transpose(1, 2)
         if torch.is_grad_enabled() and q.requires_grad:
-            raise NotImplementedError("RDAttention on MI355X is inference-only (no autograd through HIP kernels)")
+            return self._forward_autograd(q, k, v, position_embeddings, past_key_values)
         q, k = rope_inplace(q, *position_embeddings), rope_inplace(k, *position_embeddings)
         if past_key_values is not None:
             # the cache kwargs tell an Int8KVLayer that this module takes fused decode handles (exact_attention)
@@ -170,6 +170,35 @@ class RDAttention(nn.Module):
             out = self.sparse_prefill(q, k, v)
             if self.kv_evict and past_key_values is not None:
                 self.evict(past_key_values, q, k, v)
+        out = out.transpose(1, 2).reshape(b, t, -1)
+        return self.o_proj(out), None
+
+    def _forward_autograd(self, q, k, v, position_embeddings, past_key_values):
+        """forward with autograd on, as the reference takes it (modal_rd/attention.py:118-119, 127-129, 140-141): RoPE
+        out of place (HF apply_rotary_pos_emb), and the exact layers (dense, cached decode, short prompts) through
+        torch's differentiable SDPA, so they backpropagate. The sparse prefill has no backward here, as the
+        reference's Triton kernel has none: it runs the HIP path on detached tensors and its output carries no
+        gradient to q, k and v."""
+        import torch.nn.functional as F
+        from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
+
+        _lib.lib()  # the HIP library is required in every mode
+        b, _, t, _ = q.shape
+        q, k = apply_rotary_pos_emb(q, k, *position_embeddings)
+        if past_key_values is not None:
+            k, v = past_key_values.update(k, v, self.layer_idx)
+        n = k.shape[-2]
+        if b != 1:
+            raise ValueError("batch size 1 only")
+        if self.dense or t < n or n <= self.sink + self.window:
+            out = F.scaled_dot_product_attention(q, k, v, is_causal=t == n and t > 1, scale=self.scaling,
+                                                 enable_gqa=True)
+        else:
+            with torch.no_grad():
+                qd, kd, vd = q.detach(), k.detach(), v.detach()
+                out = self.sparse_prefill(qd, kd, vd)
+                if self.kv_evict and past_key_values is not None:
+                    self.evict(past_key_values, qd, kd, vd)
         out = out.transpose(1, 2).reshape(b, t, -1)
         return self.o_proj(out), None
 
