@@ -3,8 +3,8 @@ operators refuse CPU tensors loudly (no CPU fallback), and the graph decoder val
 import pytest
 import torch
 
-from bigger_bird_amd.decode import argmax_index, bigger_bird_decode, bigger_bird_route, gather_rows, rms_norm, \
-    topk_columns
+from bigger_bird_amd.decode import argmax_index, bigger_bird_decode, bigger_bird_route, decode_step, gather_rows, \
+    rms_norm, topk_columns
 from bigger_bird_amd.kv_int8 import quantize_pair
 
 
@@ -15,6 +15,8 @@ def test_decode_ops_refuse_cpu_tensors():
         bigger_bird_decode(q, k, k, torch.zeros(8, 4, dtype=torch.long), front=8, window=8)
     with pytest.raises(ValueError, match="requires CUDA"):
         bigger_bird_route(q, k, 16, front=8, window=8)
+    with pytest.raises(ValueError, match="requires CUDA"):
+        decode_step(q, k, k, k[:, 0], k[:, 0], torch.tensor([10]), routed=16, front=8, window=8)
     with pytest.raises(ValueError, match="GPU"):
         gather_rows(k, torch.zeros(8, 4, dtype=torch.long))
     with pytest.raises(ValueError, match="GPU"):
