@@ -177,6 +177,8 @@ def decode_step(q, k, v, knew, vnew, length, *, routed=0, front=64, window=4096,
     idx = torch.empty(hk, routed, dtype=torch.int32, device=q.device) if routed > 0 else None
     if out is None:
         out = torch.empty(h, d, dtype=q.dtype, device=q.device)
+    elif tuple(out.shape) != (h, d) or out.dtype != q.dtype or out.stride(-1) != 1 or out.device != q.device:
+        raise ValueError("decode_step: out must be [H, D] in q's dtype with a contiguous head_dim")
     L = _lib.lib()
     ws_bytes = L.bb_decode_step_workspace(cap, h, hk, d, int(front), int(window), routed)
     ws = _lib.workspace(ws_bytes, q.device)
