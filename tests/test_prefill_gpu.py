@@ -86,15 +86,17 @@ def test_sparse_prefill_matches_oracle(name, dev):
         assert err.max().item() < 2e-2 and err.mean().item() < 2e-3
 
 
-def test_config4_batch_sampled_rows(dev):
-    """BASELINE configs[3] shape: B=4, T=32768, {64, 4096, 512, 256}; each batch element against the float64 oracle
-    on sampled rows (main pass, window edges, tail) of all 32 heads, with that element's own routes."""
-    print("case prefill config4 B=4 T=32768", flush=True)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_config4_batch_sampled_rows(dtype, dev):
+    """BASELINE configs[3] shape: B=4, T=32768, {64, 4096, 512, 256}, bf16 and fp16 inputs; each batch element against
+    the float64 oracle on sampled rows (main pass, window edges, tail) of all 32 heads, with that element's own
+    routes, and the routes themselves against the oracle's."""
+    print(f"case prefill config4 B=4 T=32768 {dtype}", flush=True)
     from bigger_bird_amd.synth import make_inputs
     B, H, Hkv, T, d = 4, 32, 8, 32768, 128
     cfg = dict(sink=64, window=4096, vertical=512, exact_tail=256)
     inp = make_inputs(T, H, Hkv, d, batch=B, seed=4, sink=cfg["sink"], window=cfg["window"], device=dev,
-                      rng="device")
+                      rng="device", dtype=dtype)
     attn = RDAttention(_base(H, Hkv, d), **cfg)
     with torch.inference_mode():
         out = attn.sparse_prefill(inp["q"], inp["k"], inp["v"])
@@ -146,18 +148,20 @@ def test_config4_batch_sampled_rows(dev):
             assert err.max().item() < 2e-2 and err.mean().item() < 2e-3
 
 
-def test_vertical_scope_matches_oracle(dev):
+@pytest.mark.parametrize("name", ["config1", "config1_f16"])
+def test_vertical_scope_matches_oracle(name, dev):
     """vertical_scope (modal_rd/attention.py:187-196): routed keys only for the query chunks of `scope_chunk` rows that
     end inside the last `vertical_scope` rows; earlier chunks attend sink + window only. The oracle gets the same
-    per-chunk route lists ([H, groups, K], -1 for inactive chunks) and route_chunk = scope_chunk."""
-    print("case prefill vertical_scope", flush=True)
-    g = golden_routes.case("config1")
+    per-chunk route lists ([H, groups, K], -1 for inactive chunks) and route_chunk = scope_chunk. bf16 and fp16
+    inputs (the routes equal the reference's golden routes for each)."""
+    print(f"case prefill vertical_scope {name}", flush=True)
+    g = golden_routes.case(name)
     H, Hkv, T, d = g["H"], g["Hkv"], g["T"], g["d"]
     cfg = dict(sink=64, window=2048, vertical=128, exact_tail=256, vertical_scope=3000, scope_chunk=1024)
     attn = RDAttention(_base(H, Hkv, d), **cfg)
     gen = torch.Generator().manual_seed(9)
-    v = torch.randn(1, Hkv, T, d, generator=gen).to(torch.bfloat16)
     q, k = g["q"], g["k"]
+    v = torch.randn(1, Hkv, T, d, generator=gen).to(q.dtype)
     with torch.inference_mode():
         out = attn.sparse_prefill(q.to(dev), k.to(dev), v.to(dev))
     torch.cuda.synchronize()
