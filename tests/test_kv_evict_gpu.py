@@ -15,14 +15,14 @@ KW = dict(sink=8, window=96, vertical=24, n_route=16, exact_tail=24, block_m=16,
 N = 400
 
 
-def _tiny(dev):
+def _tiny(dev, dtype=torch.bfloat16):
     from transformers import LlamaConfig, LlamaForCausalLM
 
     cfg = LlamaConfig(vocab_size=512, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
                       num_attention_heads=16, num_key_value_heads=4, max_position_embeddings=8192,
                       attn_implementation="sdpa")
     torch.manual_seed(0)
-    return LlamaForCausalLM(cfg).to(dev, torch.bfloat16).eval()
+    return LlamaForCausalLM(cfg).to(dev, dtype).eval()
 
 
 def _prefill(model, ids):
@@ -34,11 +34,12 @@ def _prefill(model, ids):
     return logits, cache
 
 
-def test_prefill_unchanged_cache_shrinks_and_retained_set(dev):
-    print("case kv_evict_model", flush=True)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_prefill_unchanged_cache_shrinks_and_retained_set(dtype, dev):
+    print(f"case kv_evict_model {dtype}", flush=True)
     torch.manual_seed(4)
     ids = torch.randint(0, 512, (1, N), device=dev)
-    model = _tiny(dev)
+    model = _tiny(dev, dtype)
     install(model, "rd", **KW)
     want, full = _prefill(model, ids)
     install(model, "rd", kv_evict=True, **KW)
@@ -152,21 +153,22 @@ def test_evict_options_match_torch_topk(dev, monkeypatch):
             assert kept[0].shape[-1] == N and got.layers[0].keys.shape[-2] == N
 
 
-def test_decode_matches_masked_full_cache(dev):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_decode_matches_masked_full_cache(dtype, dev):
     """tests/test_kv_evict.py:67-100 of the reference: 6 greedy tokens through HF generate on the evicted cache (the
     HIP decode over the compacted rows; this also checks that RoPE positions continue from the prompt length) equal
     those of a full-cache model whose decode attention is masked to the same kept positions plus every generated
-    token. The masked reference runs float32 SDPA; scores within 2e-2 (bf16), sequences equal."""
+    token. The masked reference runs float32 SDPA; scores within 2e-2, sequences equal; bf16 and fp16 models."""
     import types
 
     import torch.nn.functional as F
 
-    print("case kv_evict_decode", flush=True)
+    print(f"case kv_evict_decode {dtype}", flush=True)
     torch.manual_seed(4)
     ids = torch.randint(0, 512, (1, N), device=dev)
     gen = dict(max_new_tokens=6, min_new_tokens=6, do_sample=False, use_cache=True, pad_token_id=0,
                output_scores=True, return_dict_in_generate=True)
-    ev = _tiny(dev)
+    ev = _tiny(dev, dtype)
     install(ev, "rd", kv_evict=True, **KW)
     with torch.inference_mode():
         out = ev.generate(ids, **gen)
@@ -175,7 +177,7 @@ def test_decode_matches_masked_full_cache(dev):
     m = KW["sink"] + KW["window"] + g * KW["vertical"]
     assert all(kp.shape[-1] == m for kp in kept)
 
-    ref = _tiny(dev)
+    ref = _tiny(dev, dtype)
     install(ref, "rd", **KW)
     for layer, kp in zip(ref.model.layers, kept):
         attn = layer.self_attn
