@@ -30,8 +30,11 @@ extern "C" {
  *   200  bb_sparse_flash and bb_routes take is_f16 (after D); bb_sparse_flash_workspace takes n_groups (after
  *        route_k) and has_key_mask (last); bb_rope_inplace takes is_f16 (before stream); bb_init and bb_stream_read
  *        added
- *   201  bb_decode_step and bb_decode_step_workspace added */
-#define BB_ABI_VERSION 201
+ *   201  bb_decode_step and bb_decode_step_workspace added
+ *   202  bb_int8_quantize / bb_int8_quantize_pair take an element kind (0 bf16, 1 fp32, 2 fp16) where they took
+ *        x_is_f32, and bb_int8_dequantize an output kind where it took out_is_f32 (the old values keep their
+ *        meaning) */
+#define BB_ABI_VERSION 202
 int bb_version(void);
 
 /* Message of the last failed call on this host thread ("" if none). */
@@ -114,23 +117,25 @@ size_t bb_routes_workspace(int64_t n, int H, int Hkv, int B, int r);
 
 /*
  * Per-row symmetric int8 quantisation of rows (outer, inner) at x + outer*row_stride + inner*inner_stride,
- * D contiguous elements each, written token-major: q [outer*inner, D], scale [outer*inner] (fp16 or fp32).
- * Replaces modal_rd/kv_int8.py:19-22 / kernels/kv_int8_triton.py:36-51.
+ * D contiguous elements each (x_kind: 0 bf16, 1 fp32, 2 fp16), written token-major: q [outer*inner, D],
+ * scale [outer*inner] (fp16 or fp32). Replaces modal_rd/kv_int8.py:19-22 / kernels/kv_int8_triton.py:36-51 (which
+ * quantise whatever float dtype the model runs in).
  */
-int bb_int8_quantize(const void* x, int x_is_f32, int64_t outer, int64_t row_stride, int inner, int64_t inner_stride,
+int bb_int8_quantize(const void* x, int x_kind, int64_t outer, int64_t row_stride, int inner, int64_t inner_stride,
                      int D, float min_scale, int8_t* q, void* scale, int scale_is_f16, void* stream);
 
-/* q [rows, D] int8 * scale [rows] -> out [rows, D] (bf16 or fp32). Replaces modal_rd/kv_int8.py:25-26. */
+/* q [rows, D] int8 * scale [rows] in fp32 -> out [rows, D] (out_kind: 0 bf16, 1 fp32, 2 fp16; 16-bit outputs
+ * rounded to nearest even). Replaces modal_rd/kv_int8.py:25-26. */
 /*
  * bb_int8_quantize of a decode step's new K rows and V rows in one launch: xk and xv share the shape and strides,
  * results to (qk, sk) and (qv, sv). Replaces the per-tensor quantize loop of Int8KVLayer.update
  * (modal_rd/kv_int8.py:107-111).
  */
-int bb_int8_quantize_pair(const void* xk, const void* xv, int x_is_f32, int64_t outer, int64_t row_stride, int inner,
+int bb_int8_quantize_pair(const void* xk, const void* xv, int x_kind, int64_t outer, int64_t row_stride, int inner,
                           int64_t inner_stride, int D, float min_scale, int8_t* qk, void* sk, int8_t* qv, void* sv,
                           int scale_is_f16, void* stream);
 int bb_int8_dequantize(const int8_t* q, const void* scale, int scale_is_f16, int64_t rows, int D, void* out,
-                       int out_is_f32, void* stream);
+                       int out_kind, void* stream);
 
 /*
  * Exact attention of one decode token over the first n rows of a KV cache: out [H, D] bf16 from q [H, D] bf16.

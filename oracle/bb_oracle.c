@@ -409,20 +409,27 @@ int orc_attn_rows(const uint16_t* q, int64_t sq0, int64_t sq1, const uint16_t* k
   return err;
 }
 
-/* Per-row symmetric int8: x is bf16 (in_f32 == 0) or fp32 rows of length d with row stride sx. */
-int orc_quantize(const void* x, int in_f32, int64_t sx, int64_t rows, int d, float min_scale, int8_t* qo,
+/* Per-row symmetric int8 (modal_rd/kv_int8.py:19-22): x is bf16 (kind 0), fp32 (kind 1) or fp16 (kind 2) rows of
+ * length d with row stride sx; 16-bit elements are exact in fp32. */
+static float orc_elem(const void* x, int kind, int64_t i) {
+  if (kind == 1) return ((const float*)x)[i];
+  const uint16_t h = ((const uint16_t*)x)[i];
+  return kind == 2 ? f16_to_f32(h) : bf16_to_f32(h);
+}
+
+int orc_quantize(const void* x, int in_kind, int64_t sx, int64_t rows, int d, float min_scale, int8_t* qo,
                  float* scale_f32, uint16_t* scale_f16) {
   for (int64_t r = 0; r < rows; ++r) {
     float amax = 0.0f;
     for (int c = 0; c < d; ++c) {
-      float xv = in_f32 ? ((const float*)x)[r * sx + c] : bf16_to_f32(((const uint16_t*)x)[r * sx + c]);
+      float xv = orc_elem(x, in_kind, r * sx + c);
       float a = fabsf(xv);
       if (a > amax) amax = a;
     }
     float sc = amax / 127.0f;
     if (sc < min_scale) sc = min_scale;
     for (int c = 0; c < d; ++c) {
-      float xv = in_f32 ? ((const float*)x)[r * sx + c] : bf16_to_f32(((const uint16_t*)x)[r * sx + c]);
+      float xv = orc_elem(x, in_kind, r * sx + c);
       float qv = nearbyintf(xv / sc);
       if (qv > 127.0f) qv = 127.0f;
       if (qv < -127.0f) qv = -127.0f;

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_function():
 
 def test_version_and_sizes():
     L = _lib.lib()
-    assert L.bb_version() == 201  # the parameter lists of include/bb_attn.h (BB_ABI_VERSION)
+    assert L.bb_version() == 202  # the parameter lists of include/bb_attn.h (BB_ABI_VERSION)
     assert L.bb_transpose_v_cols(1) == 64 and L.bb_transpose_v_cols(64) == 64 and L.bb_transpose_v_cols(65) == 128
     assert L.bb_routes_workspace(131072, 32, 8, 1, 64) > 32 * 131072 * 8
     assert L.bb_decode_workspace(131072, 32, 8, 128) > 0

@@ -33,6 +33,23 @@ def test_quantize_bitwise(scale_dtype, dev):
     assert torch.equal(deq, oracle.dequantize(want_q, want_s))
 
 
+def test_quantize_fp16_input_and_output(dev):
+    """An fp16 model's cache: fp16 rows quantised bitwise as the oracle (the reference's formula on x.float()), and
+    dequantised to fp16 as torch rounds the fp32 product (modal_rd/kv_int8.py:25-26, `.to(dtype)`)."""
+    print("case quantize_fp16", flush=True)
+    g = torch.Generator().manual_seed(5)
+    x = (torch.randn(1, 8, 513, 128, generator=g) * torch.rand(1, 8, 513, 1, generator=g) * 4).to(torch.float16)
+    x[0, 2, 7] = 0
+    x[0, 1, 9, :3] = torch.tensor([6e-8, -3e-5, 65504.0], dtype=torch.float16)
+    q8, s = quantize(x.to(dev)[0].transpose(0, 1))  # strided rows -> token-major
+    want_q, want16, _ = oracle.quantize(x[0].transpose(0, 1).contiguous())
+    assert torch.equal(q8.cpu(), want_q) and torch.equal(s.cpu().view(torch.int16), want16.view(torch.int16))
+    deq = dequantize(q8, s, torch.float16).cpu()
+    assert torch.equal(deq.view(torch.int16), oracle.dequantize(want_q, want16).to(torch.float16).view(torch.int16))
+    deq_bf = dequantize(q8, s, torch.bfloat16).cpu()
+    assert torch.equal(deq_bf.view(torch.int16), oracle.dequantize(want_q, want16).to(torch.bfloat16).view(torch.int16))
+
+
 def test_quantize_fp32_input(dev):
     print("case quantize_fp32", flush=True)
     g = torch.Generator().manual_seed(2)
@@ -131,7 +148,8 @@ def test_rope_inplace_bitwise(dtype, dev):
     assert torch.equal(y.cpu(), rope_host(x, cos, sin))
 
 
-@pytest.mark.parametrize("scale_dtype,f32", [(torch.float16, False), (torch.float32, False), (torch.float32, True)])
+@pytest.mark.parametrize("scale_dtype,f32", [(torch.float16, False), (torch.float32, False), (torch.float32, True),
+                                             (torch.float16, "f16")])
 def test_quantize_pair_matches_oracle(scale_dtype, f32, dev):
     """K and V rows quantised in one launch (bb_int8_quantize_pair) equal the oracle for each tensor, bitwise, into
     slices of cache buffers; inputs that differ in strides take the two-launch path with the same results."""
@@ -139,7 +157,9 @@ def test_quantize_pair_matches_oracle(scale_dtype, f32, dev):
     from bigger_bird_amd.kv_int8 import quantize_pair
 
     k, v = _rand((1, 8, 5, 128), 3, 3.0), _rand((1, 8, 5, 128), 4, 0.5)
-    if f32:
+    if f32 == "f16":  # fp16 inputs
+        k, v = (_rand((1, 8, 5, 128), 3, 3.0).float() * 1.37).half(), (_rand((1, 8, 5, 128), 4, 0.5).float() * 0.71).half()
+    elif f32:
         k, v = k.float(), v.float()
     kd, vd = k.to(dev)[0].transpose(0, 1), v.to(dev)[0].transpose(0, 1)  # [t, Hkv, d] strided views
     qk = torch.zeros(20, 8, 128, dtype=torch.int8, device=dev)

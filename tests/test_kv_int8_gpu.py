@@ -26,7 +26,7 @@ KW = dict(sink=8, window=96, vertical=24, n_route=16, exact_tail=24, block_m=16,
 N = 400
 
 
-def _tiny(dev):
+def _tiny(dev, dtype=torch.bfloat16):
     from transformers import LlamaConfig, LlamaForCausalLM
 
     # 8 query / 2 KV heads, head_dim 64 (the decode kernels take 64 or 128)
@@ -34,7 +34,7 @@ def _tiny(dev):
                       num_attention_heads=8, num_key_value_heads=2, max_position_embeddings=8192,
                       attn_implementation="sdpa")
     torch.manual_seed(0)
-    return LlamaForCausalLM(cfg).to(dev, torch.bfloat16).eval()
+    return LlamaForCausalLM(cfg).to(dev, dtype).eval()
 
 
 def _prompt(dev):
@@ -88,6 +88,32 @@ def test_prefill_unchanged_and_decode_close(installed, dev, monkeypatch):
     assert all(isinstance(x, Int8KVLayer) and x.get_seq_length() == N + 5 for x in cache.layers)
     # RDAttention opts in to the fused decode (5 decode steps x 2 layers); a stock HF module never gets handles
     assert counter.calls == (10 if installed else 0)
+
+
+@pytest.mark.parametrize("installed", [True, False])
+def test_fp16_model(installed, dev, monkeypatch):
+    """An fp16 model with the int8 cache (the reference's layer quantises any float dtype and dequantises to it): the
+    fp16 rows quantise and dequantise on the HIP kernels, prefill logits are identical to an fp16 DynamicCache and
+    greedy decode stays within 0.05 of it. The fused int8 decode takes bf16 queries, so an fp16 model's decode
+    attends the dequantised fp16 cache (RDAttention's exact path, or the stock HF module)."""
+    print(f"case int8_layer_fp16 installed={installed}", flush=True)
+    from transformers import DynamicCache
+
+    model = _tiny(dev, torch.float16)
+    if installed:
+        install(model, "rd", **KW)
+    ids = _prompt(dev)
+    want = _gen(model, ids, DynamicCache(config=model.config))
+    counter = _CountAttend(monkeypatch)
+    cache = make_int8_cache(model.config)
+    got = _gen(model, ids, cache)
+    assert torch.equal(got.scores[0], want.scores[0]), "prefill logits must be identical"
+    diffs = [_max_diff(a, b) for a, b in zip(got.scores, want.scores)]
+    print("max |logit diff| per step, int8 vs fp16 cache:", [round(d, 5) for d in diffs], flush=True)
+    assert max(diffs) < 0.05
+    assert counter.calls == 0
+    layer = cache.layers[0]
+    assert layer.keys.dtype == torch.float16 and layer.get_seq_length() == N + 5
 
 
 def test_fused_off_gives_tensors_to_rd_attention(dev, monkeypatch):

@@ -33,6 +33,13 @@ def test_quantize_bitwise_matches_torch_formula():
     q, s16, _ = oracle.quantize(xf)
     tq, t16, _ = _torch_quantize(xf)
     assert torch.equal(q, tq) and torch.equal(s16.view(torch.int16), t16.view(torch.int16))
+    # fp16 input (an fp16 model's cache): values down to fp16 subnormals and up to its largest finite magnitudes
+    xh = (torch.randn(200, 8, 128, generator=g) * torch.rand(200, 8, 1, generator=g) * 3).to(torch.float16)
+    xh[0, 0, :3] = torch.tensor([6e-8, -3e-5, 65504.0], dtype=torch.float16)
+    xh[1, 2] = 0
+    q, s16, s32 = oracle.quantize(xh)
+    tq, t16, t32 = _torch_quantize(xh)
+    assert torch.equal(q, tq) and torch.equal(s16.view(torch.int16), t16.view(torch.int16)) and torch.equal(s32, t32)
 
 
 def test_quantize_error_bounds_and_storage():

@@ -21,6 +21,9 @@ MIN_SCALE = 1e-4
 GROW = 256
 
 
+_KINDS = {torch.bfloat16: 0, torch.float32: 1, torch.float16: 2}  # element kinds of the quantise / dequantise ABI
+
+
 def _scale_flag(scale_dtype):
     if scale_dtype == torch.float16:
         return 1
@@ -60,15 +63,16 @@ def _outputs(x, out, scale_dtype):
 
 
 def quantize(x, out=None, scale_dtype=torch.float16, min_scale=MIN_SCALE):
-    """[..., d] (bf16 or fp32, rows may be strided) -> int8 [..., d], scales [..., 1]; one row per leading index.
+    """[..., d] (bf16, fp16 or fp32, rows may be strided) -> int8 [..., d], scales [..., 1]; one row per leading
+    index (the reference quantises whatever float dtype the model runs in, modal_rd/kv_int8.py:19-22).
 
     `out` = (q, s): contiguous tensors to write into (e.g. the next rows of a cache buffer)."""
     _lib.require_gpu(x, what="quantize")
-    if x.dtype not in (torch.bfloat16, torch.float32):
-        raise ValueError("quantize: bf16 or fp32 input")
+    if x.dtype not in _KINDS:
+        raise ValueError("quantize: bf16, fp16 or fp32 input")
     q, s = _outputs(x, out, scale_dtype)
     x3, outer, inner, so, si = _rows(x)
-    _lib.check(_lib.lib().bb_int8_quantize(_lib.ptr(x3), int(x.dtype == torch.float32), outer, so, inner, si,
+    _lib.check(_lib.lib().bb_int8_quantize(_lib.ptr(x3), _KINDS[x.dtype], outer, so, inner, si,
                                            x.shape[-1], float(min_scale), _lib.ptr(q), _lib.ptr(s),
                                            _scale_flag(s.dtype), _lib.stream_of(x)))
     return q, s
@@ -78,7 +82,7 @@ def quantize_pair(xk, xv, out_k, out_v, scale_dtype=torch.float16, min_scale=MIN
     """quantize(xk, out_k) and quantize(xv, out_v) in one launch when the two inputs share shape, dtype and strides
     (a decode step's new K and V rows); two launches otherwise."""
     _lib.require_gpu(xk, xv, what="quantize")
-    if xk.dtype not in (torch.bfloat16, torch.float32) or xv.dtype != xk.dtype or xv.shape != xk.shape:
+    if xk.dtype not in _KINDS or xv.dtype != xk.dtype or xv.shape != xk.shape:
         return quantize(xk, out_k, scale_dtype, min_scale), quantize(xv, out_v, scale_dtype, min_scale)
     (qk, sk), (qv, sv) = _outputs(xk, out_k, scale_dtype), _outputs(xv, out_v, scale_dtype)
     a, b = _rows(xk), _rows(xv)
@@ -86,22 +90,22 @@ def quantize_pair(xk, xv, out_k, out_v, scale_dtype=torch.float16, min_scale=MIN
         return quantize(xk, (qk, sk), scale_dtype, min_scale), quantize(xv, (qv, sv), scale_dtype, min_scale)
     _, outer, inner, so, si = a
     _lib.check(_lib.lib().bb_int8_quantize_pair(
-        _lib.ptr(a[0]), _lib.ptr(b[0]), int(xk.dtype == torch.float32), outer, so, inner, si, xk.shape[-1],
+        _lib.ptr(a[0]), _lib.ptr(b[0]), _KINDS[xk.dtype], outer, so, inner, si, xk.shape[-1],
         float(min_scale), _lib.ptr(qk), _lib.ptr(sk), _lib.ptr(qv), _lib.ptr(sv), _scale_flag(sk.dtype),
         _lib.stream_of(xk)))
     return (qk, sk), (qv, sv)
 
 
 def dequantize(q, scale, dtype):
-    """int8 [..., d] * scale [..., 1] -> dtype (bf16 or fp32)."""
+    """int8 [..., d] * scale [..., 1] -> dtype (bf16, fp16 or fp32; the fp32 product rounded to nearest even)."""
     _lib.require_gpu(q, scale, what="dequantize")
-    if dtype not in (torch.bfloat16, torch.float32):
-        raise ValueError("dequantize: bf16 or fp32 output")
+    if dtype not in _KINDS:
+        raise ValueError("dequantize: bf16, fp16 or fp32 output")
     q, scale = q.contiguous(), scale.contiguous()
     out = torch.empty(q.shape, device=q.device, dtype=dtype)
     rows = q.numel() // q.shape[-1]
     _lib.check(_lib.lib().bb_int8_dequantize(_lib.ptr(q), _lib.ptr(scale), _scale_flag(scale.dtype), rows, q.shape[-1],
-                                             _lib.ptr(out), int(dtype == torch.float32), _lib.stream_of(q)))
+                                             _lib.ptr(out), _KINDS[dtype], _lib.stream_of(q)))
     return out
 
 

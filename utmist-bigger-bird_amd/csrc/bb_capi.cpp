@@ -350,41 +350,44 @@ int bb_routes(const void* q, const int64_t* sq, const void* k, const int64_t* sk
   return BB_OK;
 }
 
-int bb_int8_quantize(const void* x, int x_is_f32, int64_t outer, int64_t row_stride, int inner, int64_t inner_stride,
+int bb_int8_quantize(const void* x, int x_kind, int64_t outer, int64_t row_stride, int inner, int64_t inner_stride,
                      int D, float min_scale, int8_t* q, void* scale, int scale_is_f16, void* stream) {
   g_err[0] = 0;
   if (!x || !q || !scale) return fail("quantize: null argument");
   if (D != 32 && D != 64 && D != 128 && D != 256) return fail("quantize: head_dim %d unsupported", D);
-  const int64_t el = x_is_f32 ? 4 : 2;
+  if (x_kind < 0 || x_kind > 2) return fail("quantize: element kind %d unsupported (0 bf16, 1 fp32, 2 fp16)", x_kind);
+  const int64_t el = x_kind == 1 ? 4 : 2;
   if (!aligned(x, 16) || (row_stride * el) % 16 || (inner_stride * el) % 16 || !aligned(q, 8))
     return fail("quantize: rows must be 16-byte aligned");
-  return hip_status(bb::launch_int8_quantize(x, x_is_f32, outer, row_stride, inner, inner_stride, D, min_scale, q, scale,
+  return hip_status(bb::launch_int8_quantize(x, x_kind, outer, row_stride, inner, inner_stride, D, min_scale, q, scale,
                                              scale_is_f16, static_cast<hipStream_t>(stream)),
                     "bb_int8_quantize");
 }
 
-int bb_int8_quantize_pair(const void* xk, const void* xv, int x_is_f32, int64_t outer, int64_t row_stride, int inner,
+int bb_int8_quantize_pair(const void* xk, const void* xv, int x_kind, int64_t outer, int64_t row_stride, int inner,
                           int64_t inner_stride, int D, float min_scale, int8_t* qk, void* sk, int8_t* qv, void* sv,
                           int scale_is_f16, void* stream) {
   g_err[0] = 0;
   if (!xk || !xv || !qk || !sk || !qv || !sv) return fail("quantize: null argument");
   if (D != 32 && D != 64 && D != 128 && D != 256) return fail("quantize: head_dim %d unsupported", D);
-  const int64_t el = x_is_f32 ? 4 : 2;
+  if (x_kind < 0 || x_kind > 2) return fail("quantize: element kind %d unsupported (0 bf16, 1 fp32, 2 fp16)", x_kind);
+  const int64_t el = x_kind == 1 ? 4 : 2;
   if (!aligned(xk, 16) || !aligned(xv, 16) || (row_stride * el) % 16 || (inner_stride * el) % 16 || !aligned(qk, 8) ||
       !aligned(qv, 8))
     return fail("quantize: rows must be 16-byte aligned");
-  return hip_status(bb::launch_int8_quantize(xk, x_is_f32, outer, row_stride, inner, inner_stride, D, min_scale, qk, sk,
+  return hip_status(bb::launch_int8_quantize(xk, x_kind, outer, row_stride, inner, inner_stride, D, min_scale, qk, sk,
                                              scale_is_f16, static_cast<hipStream_t>(stream), xv, qv, sv),
                     "bb_int8_quantize_pair");
 }
 
 int bb_int8_dequantize(const int8_t* q, const void* scale, int scale_is_f16, int64_t rows, int D, void* out,
-                       int out_is_f32, void* stream) {
+                       int out_kind, void* stream) {
   g_err[0] = 0;
   if (!q || !scale || !out) return fail("dequantize: null argument");
   if (D != 32 && D != 64 && D != 128 && D != 256) return fail("dequantize: head_dim %d unsupported", D);
+  if (out_kind < 0 || out_kind > 2) return fail("dequantize: element kind %d unsupported (0 bf16, 1 fp32, 2 fp16)", out_kind);
   if (!aligned(q, 8) || !aligned(out, 16)) return fail("dequantize: misaligned buffers");
-  return hip_status(bb::launch_int8_dequantize(q, scale, scale_is_f16, rows, D, out, out_is_f32,
+  return hip_status(bb::launch_int8_dequantize(q, scale, scale_is_f16, rows, D, out, out_kind,
                                                static_cast<hipStream_t>(stream)),
                     "bb_int8_dequantize");
 }

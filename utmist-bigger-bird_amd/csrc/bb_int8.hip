@@ -55,8 +55,11 @@ BB_DEV void store_scale(void* s, int64_t i, float scale, int is_f16) {
   else reinterpret_cast<float*>(s)[i] = scale;
 }
 
+// Element kinds of the quantise input and the dequantise output (bb_int8_quantize / bb_int8_dequantize).
+constexpr int kKindBf16 = 0, kKindF32 = 1, kKindF16 = 2;
+
 template <int D>
-__global__ __launch_bounds__(256) void quantize_kernel(QuantSet set0, QuantSet set1, int x_is_f32, int64_t rows,
+__global__ __launch_bounds__(256) void quantize_kernel(QuantSet set0, QuantSet set1, int x_kind, int64_t rows,
                                                        int64_t row_stride, int inner, int64_t inner_stride,
                                                        float min_scale, int scale_is_f16) {
   const QuantSet& set = blockIdx.y ? set1 : set0;
@@ -73,17 +76,17 @@ __global__ __launch_bounds__(256) void quantize_kernel(QuantSet set0, QuantSet s
   if (valid) {
     const int64_t outer = r / inner, in = r % inner;
     const int64_t off = outer * row_stride + in * inner_stride + 8 * lane_in_row;
-    if (x_is_f32) {
+    if (x_kind == kKindF32) {
       const float* xp = reinterpret_cast<const float*>(x) + off;
       const f32x4_t a = *reinterpret_cast<const f32x4_t*>(xp), b = *reinterpret_cast<const f32x4_t*>(xp + 4);
 #pragma unroll
       for (int i = 0; i < 4; ++i) { v[i] = a[i]; v[4 + i] = b[i]; }
-    } else {
+    } else {  // 16-bit elements, exact in fp32
       const u32x4_t a = ld16(reinterpret_cast<const uint16_t*>(x) + off);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v[2 * i] = bf16_to_f32((uint16_t)(a[i] & 0xffffu));
-        v[2 * i + 1] = bf16_to_f32((uint16_t)(a[i] >> 16));
+      for (int i = 0; i < 8; ++i) {
+        const uint16_t h = (uint16_t)(a[i >> 1] >> (16 * (i & 1)));
+        v[i] = x_kind == kKindF16 ? (float)__builtin_bit_cast(_Float16, h) : bf16_to_f32(h);
       }
     }
   } else {
@@ -100,7 +103,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(QuantSet set0, QuantSet s
 template <int D>
 __global__ __launch_bounds__(256) void dequantize_kernel(const int8_t* __restrict__ q, const void* __restrict__ s,
                                                          int scale_is_f16, int64_t rows, void* __restrict__ out,
-                                                         int out_is_f32) {
+                                                         int out_kind) {
   constexpr int LPR = D / 8;
   constexpr int RPB = 256 / LPR;
   const int lane_in_row = threadIdx.x % LPR;
@@ -111,10 +114,17 @@ __global__ __launch_bounds__(256) void dequantize_kernel(const int8_t* __restric
   float v[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) v[i] = (float)(int8_t)((w[i >> 2] >> (8 * (i & 3))) & 0xffu) * sc;
-  if (out_is_f32) {
+  if (out_kind == kKindF32) {
     float* o = reinterpret_cast<float*>(out) + r * D + 8 * lane_in_row;
     *reinterpret_cast<f32x4_t*>(o) = f32x4_t{v[0], v[1], v[2], v[3]};
     *reinterpret_cast<f32x4_t*>(o + 4) = f32x4_t{v[4], v[5], v[6], v[7]};
+  } else if (out_kind == kKindF16) {  // round to nearest even, as torch's .to(torch.float16)
+    uint32_t w2[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w2[i] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2 * i]) |
+              ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2 * i + 1]) << 16);
+    st16(reinterpret_cast<uint16_t*>(out) + r * D + 8 * lane_in_row, u32x4_t{w2[0], w2[1], w2[2], w2[3]});
   } else {
     uint16_t* o = reinterpret_cast<uint16_t*>(out) + r * D + 8 * lane_in_row;
     st16(o, u32x4_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])});
@@ -637,7 +647,7 @@ __global__ __launch_bounds__(256) void rope_kernel(uint16_t* __restrict__ x, int
 
 }  // namespace
 
-hipError_t launch_int8_quantize(const void* x, int x_is_f32, int64_t rows, int64_t row_stride, int inner,
+hipError_t launch_int8_quantize(const void* x, int x_kind, int64_t rows, int64_t row_stride, int inner,
                                 int64_t inner_stride, int D, float min_scale, int8_t* q, void* scale, int scale_is_f16,
                                 hipStream_t stream, const void* x1, int8_t* q1, void* scale1) {
   const int64_t total = rows * inner;
@@ -646,25 +656,25 @@ hipError_t launch_int8_quantize(const void* x, int x_is_f32, int64_t rows, int64
   const dim3 grid((unsigned)((total + rpb - 1) / rpb), x1 ? 2u : 1u);
   const QuantSet s0{x, q, scale}, s1{x1 ? x1 : x, x1 ? q1 : q, x1 ? scale1 : scale};
   switch (D) {
-    case 32: hipLaunchKernelGGL(quantize_kernel<32>, grid, dim3(256), 0, stream, s0, s1, x_is_f32, rows, row_stride, inner, inner_stride, min_scale, scale_is_f16); break;
-    case 64: hipLaunchKernelGGL(quantize_kernel<64>, grid, dim3(256), 0, stream, s0, s1, x_is_f32, rows, row_stride, inner, inner_stride, min_scale, scale_is_f16); break;
-    case 128: hipLaunchKernelGGL(quantize_kernel<128>, grid, dim3(256), 0, stream, s0, s1, x_is_f32, rows, row_stride, inner, inner_stride, min_scale, scale_is_f16); break;
-    case 256: hipLaunchKernelGGL(quantize_kernel<256>, grid, dim3(256), 0, stream, s0, s1, x_is_f32, rows, row_stride, inner, inner_stride, min_scale, scale_is_f16); break;
+    case 32: hipLaunchKernelGGL(quantize_kernel<32>, grid, dim3(256), 0, stream, s0, s1, x_kind, rows, row_stride, inner, inner_stride, min_scale, scale_is_f16); break;
+    case 64: hipLaunchKernelGGL(quantize_kernel<64>, grid, dim3(256), 0, stream, s0, s1, x_kind, rows, row_stride, inner, inner_stride, min_scale, scale_is_f16); break;
+    case 128: hipLaunchKernelGGL(quantize_kernel<128>, grid, dim3(256), 0, stream, s0, s1, x_kind, rows, row_stride, inner, inner_stride, min_scale, scale_is_f16); break;
+    case 256: hipLaunchKernelGGL(quantize_kernel<256>, grid, dim3(256), 0, stream, s0, s1, x_kind, rows, row_stride, inner, inner_stride, min_scale, scale_is_f16); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
 hipError_t launch_int8_dequantize(const int8_t* q, const void* scale, int scale_is_f16, int64_t rows, int D, void* out,
-                                  int out_is_f32, hipStream_t stream) {
+                                  int out_kind, hipStream_t stream) {
   if (rows <= 0) return hipSuccess;
   const int rpb = 256 / (D / 8);
   const unsigned blocks = (unsigned)((rows + rpb - 1) / rpb);
   switch (D) {
-    case 32: hipLaunchKernelGGL(dequantize_kernel<32>, dim3(blocks), dim3(256), 0, stream, q, scale, scale_is_f16, rows, out, out_is_f32); break;
-    case 64: hipLaunchKernelGGL(dequantize_kernel<64>, dim3(blocks), dim3(256), 0, stream, q, scale, scale_is_f16, rows, out, out_is_f32); break;
-    case 128: hipLaunchKernelGGL(dequantize_kernel<128>, dim3(blocks), dim3(256), 0, stream, q, scale, scale_is_f16, rows, out, out_is_f32); break;
-    case 256: hipLaunchKernelGGL(dequantize_kernel<256>, dim3(blocks), dim3(256), 0, stream, q, scale, scale_is_f16, rows, out, out_is_f32); break;
+    case 32: hipLaunchKernelGGL(dequantize_kernel<32>, dim3(blocks), dim3(256), 0, stream, q, scale, scale_is_f16, rows, out, out_kind); break;
+    case 64: hipLaunchKernelGGL(dequantize_kernel<64>, dim3(blocks), dim3(256), 0, stream, q, scale, scale_is_f16, rows, out, out_kind); break;
+    case 128: hipLaunchKernelGGL(dequantize_kernel<128>, dim3(blocks), dim3(256), 0, stream, q, scale, scale_is_f16, rows, out, out_kind); break;
+    case 256: hipLaunchKernelGGL(dequantize_kernel<256>, dim3(blocks), dim3(256), 0, stream, q, scale, scale_is_f16, rows, out, out_kind); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

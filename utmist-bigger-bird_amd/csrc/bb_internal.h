@@ -64,11 +64,12 @@ hipError_t launch_routes(RoutesParams& p, void* ws, size_t ws_bytes, hipStream_t
 
 // INT8 KV cache.
 // With x1 set, a second input of the same shape and strides goes to (q1, scale1) in the same launch.
-hipError_t launch_int8_quantize(const void* x, int x_is_f32, int64_t rows, int64_t row_stride, int inner, int64_t inner_stride,
+// Element kinds: 0 bf16, 1 fp32, 2 fp16 (quantise input, dequantise output).
+hipError_t launch_int8_quantize(const void* x, int x_kind, int64_t rows, int64_t row_stride, int inner, int64_t inner_stride,
                                 int D, float min_scale, int8_t* q, void* scale, int scale_is_f16, hipStream_t stream,
                                 const void* x1 = nullptr, int8_t* q1 = nullptr, void* scale1 = nullptr);
 hipError_t launch_int8_dequantize(const int8_t* q, const void* scale, int scale_is_f16, int64_t rows, int D,
-                                  void* out, int out_is_f32, hipStream_t stream);
+                                  void* out, int out_kind, hipStream_t stream);
 
 struct DecodeParams {
   const uint16_t* q;   // [B*H, D] (row stride sq)
