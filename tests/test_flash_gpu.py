@@ -48,6 +48,10 @@ CASES = [
     ("mha_d128", 4, 4, 513, 513, 128, 3, 100, 33, 0.1),
     ("gqa8_d128", 16, 2, 700, 700, 128, 64, 128, 64, 128 ** -0.5),
     ("offset_d128", 8, 2, 300, 1100, 128, 32, 200, 50, 128 ** -0.5),
+    # the pipelined kernel with 2 and 1 query heads per workgroup (128- and 256-row tiles), and past 512 route slots
+    ("gqa2_d128", 16, 8, 1500, 1500, 128, 64, 256, 130, 128 ** -0.5),
+    ("mha_d128_600routes", 8, 8, 3000, 3000, 128, 64, 512, 600, 128 ** -0.5),
+    ("gqa3_d128", 12, 4, 700, 900, 128, 16, 160, 70, 128 ** -0.5),
 ]
 
 
@@ -78,11 +82,12 @@ def test_grouped_equals_repeated(dev):
     torch.testing.assert_close(grouped, repeated, atol=2e-2, rtol=1e-3)
 
 
+@pytest.mark.parametrize("heads", [(32, 8), (32, 16), (32, 32)], ids=["gqa4", "gqa2", "mha"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
-def test_tail_window_n_is_dense_causal_rows(dtype, dev):
+def test_tail_window_n_is_dense_causal_rows(dtype, heads, dev):
     """Exact tail: front=0, window=N, no routes == dense causal rows (split-key schedule + merge)."""
-    print(f"case tail_split {dtype}", flush=True)
-    H, Hkv, N, r, d = 32, 8, 4096, 256, 128
+    print(f"case tail_split {dtype} {heads}", flush=True)
+    (H, Hkv), N, r, d = heads, 4096, 256, 128
     q, k, v = _rand((H, N, d), 21, dtype), _rand((Hkv, N, d), 22, dtype), _rand((Hkv, N, d), 23, dtype)
     none = torch.full((H, 1, 1), -1, dtype=torch.int32)
     Q = q.to(dev)

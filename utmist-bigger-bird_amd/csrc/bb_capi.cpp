@@ -140,7 +140,7 @@ static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 // itself. K rows of 4 GiB or more per KV head also leave the pipelined kernel; the reservation does not see the row
 // stride and is made anyway (it is small next to such K).
 static bool routed_tiles_wanted(int D, int kv_groups, int route_k, int n_groups, bool key_mask) {
-  return route_k > 0 && n_groups == 1 && !key_mask && D == 128 && kv_groups % 4 == 0 && flash_pipe_enabled();
+  return route_k > 0 && n_groups == 1 && !key_mask && D == 128 && kv_groups > 0 && flash_pipe_enabled();
 }
 
 size_t bb_sparse_flash_workspace(int BH, int64_t T, int64_t N, int D, int num_heads, int kv_groups, int64_t front,
@@ -251,7 +251,7 @@ static int sparse_flash_impl(const void* q, const int64_t* sq, const void* k, co
     if (e != hipSuccess) return hip_status(e, "bb_sparse_flash transpose");
     p.vt = vt_ws;
   }
-  const bool pipe = flash_pipe_enabled() && s.hpw == 4 && bb::flash_pipe_supported(p, D);
+  const bool pipe = flash_pipe_enabled() && bb::flash_pipe_supported(p, D, s.hpw);
   if (routed_tiles_wanted(D, kv_groups, route_k, p.n_groups, key_mask != nullptr)) {
     uint16_t* rt = reinterpret_cast<uint16_t*>(wsp);
     wsp += align256(bb::route_tiles_bytes(BH, p.n_groups, route_k));
@@ -265,11 +265,11 @@ static int sparse_flash_impl(const void* q, const int64_t* sq, const void* k, co
   if (s.split) {
     p.part_o = reinterpret_cast<float*>(wsp);
     p.part_ml = p.part_o + (size_t)s.n_chunks * BH * T * D;
-    hipError_t e = pipe ? bb::launch_flash_pipe(p, st) : bb::launch_flash(p, D, s.hpw, true, st);
+    hipError_t e = pipe ? bb::launch_flash_pipe(p, s.hpw, st) : bb::launch_flash(p, D, s.hpw, true, st);
     if (e != hipSuccess) return hip_status(e, "bb_sparse_flash split kernel");
     return hip_status(bb::launch_flash_merge(p, D, st), "bb_sparse_flash merge kernel");
   }
-  if (pipe) return hip_status(bb::launch_flash_pipe(p, st), "bb_sparse_flash pipelined kernel");
+  if (pipe) return hip_status(bb::launch_flash_pipe(p, s.hpw, st), "bb_sparse_flash pipelined kernel");
   return hip_status(bb::launch_flash(p, D, s.hpw, false, st), "bb_sparse_flash kernel");
 }
 

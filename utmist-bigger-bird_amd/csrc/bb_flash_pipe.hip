@@ -1,9 +1,11 @@
-// Ping-pong sink + causal window + routed sparse flash attention for gfx950 (head_dim 128, four query heads per
-// KV head, no token mask): the main pass of Bigger Bird v3 prefill at production shape.
+// Ping-pong sink + causal window + routed sparse flash attention for gfx950 (head_dim 128, no token mask): the main
+// pass of Bigger Bird v3 prefill at production shape.
 //
 // Same semantics as bb_flash.hip (kernels/bigger_bird_flash.py:42-96 of the reference). Work decomposition:
 //   * a workgroup = 8 waves = the 4 query heads of one KV head x 2 blocks of 32 query rows (64 rows); every K / V^T
-//     tile staged in LDS is read by all 8 waves (GQA reuse inside the workgroup);
+//     tile staged in LDS is read by all 8 waves (GQA reuse inside the workgroup). With 2 query heads per KV head a
+//     workgroup is 2 heads x 4 row blocks (128 rows), with 1 (MHA) one head x 8 row blocks (256 rows), so the tiles
+//     are still shared by all 8 waves;
 //   * waves w and w + 4 share a SIMD. Per 64-key tile a wave runs an MFMA phase  (O^T += V^T(t-1) P(t-1)^T,
 //     S(t) = K(t) Q^T: 32 MFMAs) and a VALU phase (online softmax of S(t) into P(t)), separated by workgroup
 //     barriers. Waves 4..7 start one barrier late, so on every SIMD one wave is in its MFMA phase while the other is
@@ -25,8 +27,7 @@ namespace {
 
 constexpr int PD = 128;                 // head_dim
 constexpr int PNW = 8;                  // waves per workgroup
-constexpr int PHEADS = 4;               // query heads per workgroup
-constexpr int PROWS = 64;               // query rows per workgroup (2 blocks of 32)
+constexpr int PHEADS = 4;               // most query heads per workgroup (HPW = 4, 2 or 1 share each tile)
 constexpr int PTE = kTileKeys * PD;     // elements of one K (or V^T) tile
 constexpr int PST = 4;                  // ring stages, each a K tile and a V^T tile
 constexpr int PBLK = PTE * 2 / 1024;    // 1 KB direct-load blocks per tile (16)
@@ -342,14 +343,17 @@ BB_DEV void ping_softmax_open(PingState& st, float c) {
   st.l += sum;
 }
 
-// Work item of a workgroup and the rows of one wave: (KV head, 64-row tile, key chunk), XCD-aware as in flash_kernel.
+// Work item of a workgroup and the rows of one wave: (KV head, row tile of 32 x 8 / HPW rows, key chunk), XCD-aware as
+// in flash_kernel.
 struct PipeItem {
   int bh, kvbh, chunk;
   int64_t T_eff, r1, qlo, qhi, rw, qw0, qw1, qme;
   bool wave_live;
 };
 
+template <int HPW>
 BB_DEV PipeItem pipe_item(const FlashParams& p, int bid, int hd, int rbk, int li) {
+  constexpr int PROWS = 32 * (PNW / HPW);
   const int lanes_total = p.n_kvbh * p.head_splits;
   const int per_lane = p.row_tiles * p.n_chunks;  // split mode: (row tile, key chunk) pairs
   int lane_id, within;
@@ -367,7 +371,7 @@ BB_DEV PipeItem pipe_item(const FlashParams& p, int bid, int hd, int rbk, int li
   it.kvbh = lane_id / p.head_splits;
   const int hsplit = lane_id % p.head_splits;
   const int batch = it.kvbh / p.Hkv_pb;
-  it.bh = batch * p.H + (it.kvbh % p.Hkv_pb) * p.G + hsplit * PHEADS + hd;
+  it.bh = batch * p.H + (it.kvbh % p.Hkv_pb) * p.G + hsplit * HPW + hd;
   it.T_eff = p.row_end < p.T ? p.row_end : p.T;
   const int64_t r0 = (int64_t)rt * PROWS;
   it.r1 = (r0 + PROWS < it.T_eff ? r0 + PROWS : it.T_eff) - 1;
@@ -383,19 +387,24 @@ BB_DEV PipeItem pipe_item(const FlashParams& p, int bid, int hd, int rbk, int li
 
 // GATHER: the routed phase gathers the rows of its batches itself (route lists with several groups, where no tiles
 // are pre-gathered); a separate instantiation, so that the common kernel's register allocation is not affected.
-template <bool F16, bool GATHER>
+// HPW: query heads per workgroup (4 when a KV head serves a multiple of 4 query heads; 2 and 1 for 2 and 1, with
+// 4 and 8 row blocks of 32 rows), so every staged K / V^T tile is read by all 8 waves in each case.
+template <bool F16, bool GATHER, int HPW>
 __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) {
+  static_assert(HPW == 4 || HPW == 2 || HPW == 1, "4, 2 or 1 query heads per workgroup");
+  constexpr int RB = PNW / HPW;  // row blocks (waves) per head
   __shared__ __attribute__((aligned(1024))) uint16_t smem[PLDS];
-  __shared__ __attribute__((aligned(16))) int32_t route_keys[PHEADS][kRouteCache];
-  __shared__ int head_batches[2][PHEADS];
+  __shared__ __attribute__((aligned(16))) int32_t route_keys[HPW][kRouteCache];
+  __shared__ int head_batches[RB][HPW];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, li = lane & 31;
-  const int hd = wave & 3, rbk = wave >> 2;  // head slot, row block (= ping-pong group)
+  const int hd = wave % HPW, rbk = wave / HPW;  // head slot, row block
+  const int grp = wave >> 2;                    // ping-pong group: waves w and w + 4 share a SIMD
 
-  // ---- work item: (KV head, 64-row tile), XCD-aware as in flash_kernel ----
-  PipeItem it = pipe_item(p, blockIdx.x, hd, rbk, li);
+  // ---- work item: (KV head, row tile), XCD-aware as in flash_kernel ----
+  PipeItem it = pipe_item<HPW>(p, blockIdx.x, hd, rbk, li);
   const int bh = it.bh, kvbh = it.kvbh, chunk = it.chunk;
   const int64_t T_eff = it.T_eff, r1 = it.r1, qlo = it.qlo, qhi = it.qhi, rw = it.rw;
   const bool wave_live = it.wave_live;
@@ -501,7 +510,7 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
     if (ntot > 1) ld.tile(kst(1), vst(1), upos(1));
     vm_wait_tile(ntot > 1);
     ring_barrier();
-    if (rbk == 1) ring_barrier();  // waves 4..7 run one phase behind
+    if (grp == 1) ring_barrier();  // waves 4..7 run one phase behind
     // tile 0: QK only
     if (ntot > 2) ld.tile(kst(2), vst(2), upos(2));
     ping_qk<F16>(st, kst(0), li, h);
@@ -538,7 +547,7 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
       ring_barrier();
     }
     ping_pv<F16>(st, vst(ntot - 1), li, h);
-    if (rbk == 0) ring_barrier();  // realign the two groups
+    if (grp == 0) ring_barrier();  // realign the two groups
   }
 
   // The work item again, from copies of the block and lane indices that the compiler cannot see through: the values
@@ -547,9 +556,9 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
     int bid2 = blockIdx.x, li2 = li;
     asm volatile("" : "+s"(bid2));
     asm volatile("" : "+v"(li2));
-    it = pipe_item(p, bid2, hd, rbk, li2);
+    it = pipe_item<HPW>(p, bid2, hd, rbk, li2);
   }
-  // ---- routed keys: per-head tiles pre-gathered by route_tiles_kernel; the two waves of a head share the loads ----
+  // ---- routed keys: per-head tiles pre-gathered by route_tiles_kernel; the RB waves of a head share the loads ----
   if (p.route_k > 0) {
     __syncthreads();  // every wave is done with the ring
     uint16_t* kl = smem + hd * 2 * PTE;
@@ -560,14 +569,14 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
     for (int64_t g = g_first; g <= g_last; ++g) {
       const int32_t* irow = p.idx + (int64_t)it.bh * p.si0 + g * p.si1;
       // This head's pre-gathered batches of group g: batch b is a K tile at b * 2 PTE and its V^T tile after it.
-      // Each of the head's two waves loads blocks rbk + 2 i (i < 8) of a tile straight into LDS.
+      // Each of the head's RB waves loads blocks rbk + RB i (i < 16 / RB) of a tile straight into LDS.
       const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
           const_cast<uint16_t*>(p.rtiles + ((int64_t)it.bh * p.n_groups + g) * p.rt_batches * 2 * PTE), 0,
           p.rt_batches * 2 * PTE * 2, 0x00020000);
       auto load_tile = [&](int b, uint16_t* dst, int part) {
 #pragma unroll
-        for (int i = 0; i < PBLK / 2; ++i) {
-          const int blk = rbk + 2 * i;
+        for (int i = 0; i < PBLK / RB; ++i) {
+          const int blk = rbk + RB * i;
           __builtin_amdgcn_raw_ptr_buffer_load_lds(
               rrs, reinterpret_cast<__attribute__((address_space(3))) void*>(
                        reinterpret_cast<uintptr_t>(dst + blk * 512)),
@@ -580,20 +589,20 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
       for (int sb = 0; sb < p.route_k; sb += kRouteCache) {
         const int nslots = p.route_k - sb < kRouteCache ? p.route_k - sb : kRouteCache;
         int nbh = 0;
-        for (int s0 = 64 * rbk; s0 < kRouteCache; s0 += 128) {
+        for (int s0 = 64 * rbk; s0 < kRouteCache; s0 += 64 * RB) {
           const int sl = s0 + lane;
           const int64_t key = sl < nslots ? irow[(int64_t)(sb + sl) * p.si2] : -1;
           const bool ok = key >= p.front && key < p.N && key <= it.qhi - p.window;
           route_keys[hd][sl] = ok ? (int32_t)key : -1;
           if (__builtin_amdgcn_ballot_w64(ok)) nbh = s0 / kTileKeys + 1;
         }
-        if (lane == 0) head_batches[rbk][hd] = nbh;  // each of the head's two waves scanned half of the slots
+        if (lane == 0) head_batches[rbk][hd] = nbh;  // each of the head's RB waves scanned 1 / RB of the slots
         __syncthreads();
         int nb = 0, my_nb = 0;
 #pragma unroll
-        for (int x = 0; x < PHEADS; ++x)
+        for (int x = 0; x < HPW; ++x)
 #pragma unroll
-          for (int y = 0; y < 2; ++y) {
+          for (int y = 0; y < RB; ++y) {
             const int v = head_batches[y][x];
             nb = nb > v ? nb : v;
             if (x == hd) my_nb = my_nb > v ? my_nb : v;
@@ -609,18 +618,18 @@ __global__ __launch_bounds__(64 * PNW, 1) void flash_ping_kernel(FlashParams p) 
               load_tile(b0 + bi, vt, 1);
             }
           } else if (work) {
-            // No pre-gathered tiles (several route groups): the head's two waves gather the batch's rows here. K rows
+            // No pre-gathered tiles (several route groups): the head's waves gather the batch's rows here. K rows
             // go straight to LDS (empty slots read row 0, masked out); V rows are transposed through registers in
             // units of 4 keys x 8 d into the permuted V^T layout. Only batches holding a usable key are gathered.
             const uint16_t* kb = p.k + (int64_t)it.kvbh * p.sk0;
             const uint16_t* vb = p.v + (int64_t)it.kvbh * p.sv0;
-            for (int b = rbk; b < PBLK; b += 2) {
+            for (int b = rbk; b < PBLK; b += RB) {
               const int e = b * 512 + 8 * lane;
               const int row = e / PD, chk = ((e % PD) / 8) ^ (row & (PD / 8 - 1));
               const int32_t kr = keys[row];
               lds_dma16(kb + (int64_t)(kr >= 0 ? kr : 0) * p.sk1 + 8 * chk, kl + b * 512);
             }
-            for (int u = lane + 64 * rbk; u < (kTileKeys / 4) * (PD / 8); u += 128) {
+            for (int u = lane + 64 * rbk; u < (kTileKeys / 4) * (PD / 8); u += 64 * RB) {
               const int bq = u % (PD / 8), a4 = u / (PD / 8);
               u32x4_t vr[4];
 #pragma unroll
@@ -759,14 +768,17 @@ __global__ __launch_bounds__(256) void route_tiles_kernel(FlashParams p, uint16_
 
 }  // namespace
 
-bool flash_pipe_supported(const FlashParams& p, int D) {
+bool flash_pipe_supported(const FlashParams& p, int D, int hpw) {
   // Buffer offsets are unsigned 32-bit: every K offset up to the end of the last tile (row N + 63, which reads as
   // zero) and every V^T offset of one KV head must stay below 4 GiB, so that no offset wraps back into the
   // tensor. Split mode needs whole tiles.
   const int64_t lim = (int64_t)1 << 32;
   const bool fits = (p.N + kTileKeys) * p.sk1 * 2 < lim && (int64_t)PD * p.np * 2 < lim;
   const bool chunks_ok = p.n_chunks == 1 || (p.key_chunk % kTileKeys == 0 && p.route_k == 0);
-  return D == PD && p.G % PHEADS == 0 && p.key_mask == nullptr && fits && chunks_ok;
+  // 4, 2 or 1 query heads per workgroup; the in-kernel gather of several route groups is built for 4
+  const bool heads_ok = (hpw == 4 || hpw == 2 || hpw == 1) && p.G % hpw == 0 &&
+                        (hpw == 4 || p.route_k == 0 || p.n_groups == 1);
+  return D == PD && heads_ok && p.key_mask == nullptr && fits && chunks_ok;
 }
 
 size_t route_tiles_bytes(int BH, int n_groups, int route_k) {
@@ -781,17 +793,27 @@ hipError_t launch_route_tiles(const FlashParams& p, uint16_t* rt, hipStream_t st
   return hipGetLastError();
 }
 
-hipError_t launch_flash_pipe(const FlashParams& p, hipStream_t stream) {
+hipError_t launch_flash_pipe(const FlashParams& p, int hpw, hipStream_t stream) {
   const int64_t items = (int64_t)p.n_kvbh * p.head_splits * p.row_tiles * p.n_chunks;
   if (items <= 0) return hipSuccess;
   if (items > 0x7fffffff) return hipErrorInvalidValue;
   const dim3 grid((unsigned)items), block(64 * PNW);
-  if (p.route_k > 0 && !p.rtiles) {
-    if (p.f16) hipLaunchKernelGGL((flash_ping_kernel<true, true>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((flash_ping_kernel<false, true>), grid, block, 0, stream, p);
+  const bool gather = p.route_k > 0 && !p.rtiles;
+  if (gather && hpw != 4) return hipErrorInvalidValue;
+  if (gather) {
+    if (p.f16) hipLaunchKernelGGL((flash_ping_kernel<true, true, 4>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((flash_ping_kernel<false, true, 4>), grid, block, 0, stream, p);
+  } else if (hpw == 4) {
+    if (p.f16) hipLaunchKernelGGL((flash_ping_kernel<true, false, 4>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((flash_ping_kernel<false, false, 4>), grid, block, 0, stream, p);
+  } else if (hpw == 2) {
+    if (p.f16) hipLaunchKernelGGL((flash_ping_kernel<true, false, 2>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((flash_ping_kernel<false, false, 2>), grid, block, 0, stream, p);
+  } else if (hpw == 1) {
+    if (p.f16) hipLaunchKernelGGL((flash_ping_kernel<true, false, 1>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((flash_ping_kernel<false, false, 1>), grid, block, 0, stream, p);
   } else {
-    if (p.f16) hipLaunchKernelGGL((flash_ping_kernel<true, false>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((flash_ping_kernel<false, false>), grid, block, 0, stream, p);
+    return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }

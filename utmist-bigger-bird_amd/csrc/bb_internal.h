@@ -30,8 +30,9 @@ struct FlashParams {
 hipError_t launch_flash(const FlashParams& p, int D, int hpw, bool split, hipStream_t stream);
 hipError_t launch_flash_merge(const FlashParams& p, int D, hipStream_t stream);
 // Software-pipelined main-pass kernel (head_dim 128, kv_groups % 4 == 0, no token mask, 64-aligned route groups).
-bool flash_pipe_supported(const FlashParams& p, int D);
-hipError_t launch_flash_pipe(const FlashParams& p, hipStream_t stream);
+// The pipelined kernel with hpw query heads per workgroup (4, 2 or 1; the schedule's rows per tile 32 x 8 / hpw).
+bool flash_pipe_supported(const FlashParams& p, int D, int hpw);
+hipError_t launch_flash_pipe(const FlashParams& p, int hpw, hipStream_t stream);
 // Bytes of the pre-gathered routed tiles of one call, and the kernel that writes them (p.rtiles) for the main pass.
 size_t route_tiles_bytes(int BH, int n_groups, int route_k);
 hipError_t launch_route_tiles(const FlashParams& p, uint16_t* rt, hipStream_t stream);
