@@ -184,7 +184,9 @@ def test_million_token_rows_match_oracle(dev):
                                                (300, 5000, 32, 8, 128, torch.bfloat16),
                                                (7, 3000, 8, 2, 64, torch.bfloat16),
                                                (300, 5000, 32, 8, 128, torch.float16),
-                                               (7, 3000, 8, 2, 64, torch.float16)])
+                                               (7, 3000, 8, 2, 64, torch.float16),
+                                               (300, 5000, 16, 8, 128, torch.bfloat16),
+                                               (65, 5000, 16, 16, 128, torch.bfloat16)])
 def test_exact_attention_noncausal(t, n, H, Hkv, d, dtype, dev):
     """bb_exact_attention: t query rows, each attending all n cached keys (the reference's SDPA with is_causal=False
     for 1 < t < n, modal_rd/attention.py:140-141), in one call, against float64 SDPA; also through
