@@ -68,9 +68,9 @@ int bb_sparse_flash(const void* q, const int64_t* sq, const void* k, const int64
 
 /* Workspace bytes for bb_sparse_flash (n_groups and route_k as passed to it); have_vt != 0 when the caller passes a
  * precomputed V^T, has_key_mask != 0 when it passes a key_mask. Besides V^T and the split partials it holds the
- * routed K/V^T tiles pre-gathered per query head (32 KB per 64 route slots per head) for head_dim 128 with a
- * multiple of 4 query heads per KV head, a single route group and no key mask; with several route groups the kernel
- * gathers the routed rows itself and no tiles are reserved. */
+ * routed K/V^T tiles pre-gathered per query head (32 KB per 64 route slots per head) for head_dim 128 with a single
+ * route group and no key mask; with several route groups the kernel gathers the routed rows itself (or, with fewer
+ * than 4 query heads per KV head, the generic kernel runs) and no tiles are reserved. */
 size_t bb_sparse_flash_workspace(int BH, int64_t T, int64_t N, int D, int num_heads, int kv_groups, int64_t front,
                                  int64_t window, int route_k, int n_groups, int64_t row_end, int have_vt,
                                  int has_key_mask);
