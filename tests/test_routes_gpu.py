@@ -18,6 +18,10 @@ CASES = [
     ("spread", 2048, 16, 4, 128, 64, 512, 128, 64, "mean", "spread", 0),
     ("mha_d32", 777, 4, 4, 32, 8, 96, 24, 16, "mean", "last", 0),
     ("config1", 8192, 32, 8, 128, 64, 2048, 128, 64, "mean", "last", 64),
+    # head_dim 128 with 48, 128 and 96 route rows per KV head (MFMA scorer workgroups of 2, 4 and 4 waves)
+    ("mha_d128_48rows", 2500, 4, 4, 128, 32, 256, 64, 48, "mean", "last", 8),
+    ("gqa2_d128", 3001, 8, 4, 128, 64, 512, 100, 64, "mean", "spread", 0),
+    ("gqa3_d128_96rows", 2049, 12, 4, 128, 64, 512, 100, 32, "max", "last", 0),
 ]
 
 
@@ -101,17 +105,20 @@ def test_routes_match_reference_golden(name, dev):
     ("large_values", 16384, 40.0, 25.0),
     ("tiny_values", 16384, 1e-3, 2e-3),
     ("mixed_rows", 16384, 1.0, 1.0),
+    ("mixed_rows_gqa2", 16384, 1.0, 1.0),
+    ("mixed_rows_mha", 16384, 1.0, 1.0),
 ])
 def test_mfma_scores_match_reference_order(name, T, scale_q, scale_k, dev, monkeypatch):
     """The MFMA score path with exact fix-up must give the same bf16 scores as computing every score in the
     reference order; compared through the pooled fixed-point values (every unmasked score of a row enters them)
     and the selected indices, at production size and at magnitudes that put many scores near rounding boundaries."""
     print(f"case mfma_scores {name} T={T}", flush=True)
-    H, Hkv, d, sink, window, budget = 32, 8, 128, 64, min(16384, T // 4), 512
+    H, d, sink, window, budget = 32, 128, 64, min(16384, T // 4), 512
+    Hkv = 32 if name.endswith("_mha") else (16 if name.endswith("_gqa2") else 8)
     inp = make_inputs(T, H, Hkv, d, seed=11, planted=64 if name == "config2_shape" else 0, sink=sink, window=window,
                       device=dev, rng="device")
     q, k = inp["q"] * scale_q, inp["k"] * scale_k
-    if name == "mixed_rows":  # rows and keys spanning many binades, some exact zeros and repeated keys
+    if name.startswith("mixed_rows"):  # rows and keys spanning many binades, some exact zeros and repeated keys
         g = torch.Generator(device=dev).manual_seed(3)
         q = q * torch.exp2(torch.randint(-12, 8, (1, H, T, 1), device=dev, generator=g).to(q.dtype))
         k = k * torch.exp2(torch.randint(-12, 8, (1, Hkv, T, 1), device=dev, generator=g).to(k.dtype))

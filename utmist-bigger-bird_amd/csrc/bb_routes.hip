@@ -40,7 +40,7 @@ constexpr int kScoreKeys = 32;    // keys per scores_kernel block (8 key groups 
 constexpr int kScoreIters = 16;   // key blocks per scores_kernel workgroup
 constexpr int kSumKeys = 1024;    // keys per rowsum_kernel workgroup
 constexpr int kPoolKeys = 512;    // keys per pooled_kernel workgroup (2 per thread)
-constexpr int kMaxRows = 256;     // G * r handled by one scores workgroup (rows beyond this use more row blocks)
+constexpr int kMaxRows = 256;     // route rows (G * r) per scores_kernel workgroup (more rows use more row blocks)
 constexpr float kFixOne = 1099511627776.0f;  // 2^40
 
 BB_DEV uint64_t fix40(float v) { return (uint64_t)(v * kFixOne); }
@@ -304,28 +304,29 @@ BB_DEV uint32_t abs_max8(u32x4_t a) {
   return m[0] > m[1] ? m[0] : m[1];
 }
 
-constexpr int kMsWaves = 8;
-
-template <int D>
-__global__ __launch_bounds__(64 * kMsWaves) void scores_mfma_kernel(RoutesParams p, RouteGeom g,
-                                                                  float* __restrict__ pmax) {
+// NW waves of 32 route rows each (NW = 8: 256 rows of one KV head; groups of 1 or 2 query heads have only 64 or 128
+// rows, so their workgroups are 2 or 4 waves and no wave computes rows that do not exist)
+template <int D, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void scores_mfma_kernel(RoutesParams p, RouteGeom g, float* __restrict__ pmax) {
   static_assert(D == 128, "MFMA scores are built for head_dim 128");
-  __shared__ __attribute__((aligned(16))) uint16_t qs[kMaxRows][kMsRowPitch];  // Q rows (bf16)
-  __shared__ __attribute__((aligned(16))) uint16_t kt[kScoreKeys][D];          // K block, chunk c of key j at c ^ (j % 16)
-  __shared__ __attribute__((aligned(16))) float kf[kScoreKeys][D];             // the same block in fp32 (same slots)
-  __shared__ __attribute__((aligned(16))) uint16_t st[kMsWaves][32][kMsTilePitch];  // per-wave score tile (bf16)
-  __shared__ uint16_t flist[kMsWaves * 32 * kScoreKeys];                       // fix-ups: wave << 10 | lane << 4 | r
-  __shared__ uint32_t fcount;                                                  // entries of flist
-  __shared__ uint32_t rmax_fix[kMaxRows];                                      // ordered-float max of fixed-up x
+  static_assert(NW == 2 || NW == 4 || NW == 8, "K staging splits 512 16-byte pieces evenly over the threads");
+  constexpr int ROWS = 32 * NW, NT = 64 * NW, KPT = kScoreKeys * (D / 8) / NT;  // K pieces per thread
+  __shared__ __attribute__((aligned(16))) uint16_t qs[ROWS][kMsRowPitch];   // Q rows (bf16)
+  __shared__ __attribute__((aligned(16))) uint16_t kt[kScoreKeys][D];       // K block, chunk c of key j at c ^ (j % 16)
+  __shared__ __attribute__((aligned(16))) float kf[kScoreKeys][D];          // the same block in fp32 (same slots)
+  __shared__ __attribute__((aligned(16))) uint16_t st[NW][32][kMsTilePitch];  // per-wave score tile (bf16)
+  __shared__ uint16_t flist[NW * 32 * kScoreKeys];                          // fix-ups: wave << 10 | lane << 4 | r
+  __shared__ uint32_t fcount;                                               // entries of flist
+  __shared__ uint32_t rmax_fix[ROWS];                                       // ordered-float max of fixed-up x
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 31, h = lane >> 5;
   const int kchunk = blockIdx.x, rblk = blockIdx.y, bkv = blockIdx.z;
   const int batch = bkv / p.Hkv, kvh = bkv % p.Hkv;
-  const int row0 = rblk * kMaxRows;
-  const int nrows = g.rows - row0 < kMaxRows ? g.rows - row0 : kMaxRows;
+  const int row0 = rblk * ROWS;
+  const int nrows = g.rows - row0 < ROWS ? g.rows - row0 : ROWS;
 
   // stage Q rows: row -> (head slot, route query i)
-  for (int e = tid; e < kMaxRows * (D / 8); e += 64 * kMsWaves) {
+  for (int e = tid; e < ROWS * (D / 8); e += NT) {
     const int row = e / (D / 8), c8 = e % (D / 8);
     u32x4_t v = {0, 0, 0, 0};
     if (row < nrows) {
@@ -335,7 +336,7 @@ __global__ __launch_bounds__(64 * kMsWaves) void scores_mfma_kernel(RoutesParams
     }
     *reinterpret_cast<u32x4_t*>(&qs[row][8 * c8]) = v;
   }
-  for (int e = tid; e < kMaxRows; e += 64 * kMsWaves) rmax_fix[e] = 0u;  // ordered key below every float
+  for (int e = tid; e < ROWS; e += NT) rmax_fix[e] = 0u;  // ordered key below every float
   if (tid == 0) fcount = 0u;
   __syncthreads();
 
@@ -385,14 +386,18 @@ __global__ __launch_bounds__(64 * kMsWaves) void scores_mfma_kernel(RoutesParams
     }
   };
 
-  // K blocks: thread (key tid / 16, chunk tid % 16) holds 16 bytes; the next block's load is in flight while the
-  // current one is processed
-  const int skey = tid >> 4, schunk = tid & 15;
-  auto kload = [&](int it) -> u32x4_t {
-    const int64_t j = ((int64_t)kchunk * kScoreIters + it) * kScoreKeys + skey;
-    return j < p.n ? ld16(kbase + j * p.sk1 + 8 * schunk) : u32x4_t{0, 0, 0, 0};
+  // K blocks: piece e = tid + NT x (key e / 16, chunk e % 16) is 16 bytes; the next block's load is in flight while
+  // the current one is processed
+  auto kload = [&](int it, u32x4_t (&dst)[KPT]) {
+#pragma unroll
+    for (int x = 0; x < KPT; ++x) {
+      const int e = tid + NT * x;
+      const int64_t j = ((int64_t)kchunk * kScoreIters + it) * kScoreKeys + (e >> 4);
+      dst[x] = j < p.n ? ld16(kbase + j * p.sk1 + 8 * (e & 15)) : u32x4_t{0, 0, 0, 0};
+    }
   };
-  u32x4_t knext = kload(0);
+  u32x4_t knext[KPT];
+  kload(0, knext);
   int64_t jlast = -1;  // key of the block whose tile is still to be stored
   for (int it = 0; it < kScoreIters; ++it) {
     const int64_t j0 = ((int64_t)kchunk * kScoreIters + it) * kScoreKeys;
@@ -401,9 +406,11 @@ __global__ __launch_bounds__(64 * kMsWaves) void scores_mfma_kernel(RoutesParams
     if (jlast >= 0) store_tile(jlast);
     jlast = j0;
     if (tid == 0) fcount = 0u;
-    {  // stage the K block: bf16 for the MFMA fragments, fp32 for the fix-ups (chunk c of key j in slot c ^ (j % 16))
-      const int slot = 8 * (schunk ^ (skey & 15));
-      const u32x4_t v = knext;
+#pragma unroll
+    for (int x = 0; x < KPT; ++x) {  // stage the K block: bf16 for the MFMA fragments, fp32 for the fix-ups
+      const int e = tid + NT * x, skey = e >> 4, schunk = e & 15;
+      const int slot = 8 * (schunk ^ (skey & 15));  // chunk c of key j in slot c ^ (j % 16)
+      const u32x4_t v = knext[x];
       *reinterpret_cast<u32x4_t*>(&kt[skey][slot]) = v;
       *reinterpret_cast<f32x4_t*>(&kf[skey][slot]) = f32x4_t{
           __uint_as_float(v[0] << 16), __uint_as_float(v[0] & 0xffff0000u), __uint_as_float(v[1] << 16),
@@ -413,7 +420,7 @@ __global__ __launch_bounds__(64 * kMsWaves) void scores_mfma_kernel(RoutesParams
           __uint_as_float(v[3] & 0xffff0000u)};
     }
     __syncthreads();
-    if (it + 1 < kScoreIters) knext = kload(it + 1);
+    if (it + 1 < kScoreIters) kload(it + 1, knext);
 
     // S^T = K Q^T as eight slice partials (zero accumulators) summed in fp32, and the bound's sum of c_d |q_d| |k_d|
     // (each partial is added one step later, while the next slice's MFMAs run: two partials live at a time)
@@ -489,7 +496,7 @@ __global__ __launch_bounds__(64 * kMsWaves) void scores_mfma_kernel(RoutesParams
 
     // exact recomputation of the flagged scores in the reference order, by every thread of the workgroup
     const uint32_t nfix = fcount;
-    for (uint32_t e = tid; e < nfix; e += 64 * kMsWaves) {
+    for (uint32_t e = tid; e < nfix; e += NT) {
       const uint32_t ent = flist[e];
       const int ew = (int)(ent >> 10), el = (int)((ent >> 4) & 63u), er = (int)(ent & 15u);
       const int lrow = el & 31, kk = 8 * (er >> 2) + 4 * (el >> 5) + (er & 3);
@@ -1101,9 +1108,13 @@ hipError_t launch_routes_d(RoutesParams& p, const RouteGeom& g, float* pmax, uin
   // fp16 scores (8x finer rounding than bf16) are computed in the reference order directly
   if (p.f16)
     hipLaunchKernelGGL((scores_kernel<D, true>), sgrid, dim3(256), 0, stream, p, g, pmax);
-  else if (D == 128 && !p.scores_reference_order)
-    hipLaunchKernelGGL(scores_mfma_kernel<128>, sgrid, dim3(64 * kMsWaves), 0, stream, p, g, pmax);
-  else
+  else if (D == 128 && !p.scores_reference_order) {
+    const int nw = g.rows <= 64 ? 2 : (g.rows <= 128 ? 4 : 8);  // waves of 32 rows per workgroup
+    const dim3 mgrid(g.n_kb1, (g.rows + 32 * nw - 1) / (32 * nw), nbkv);
+    if (nw == 2) hipLaunchKernelGGL((scores_mfma_kernel<128, 2>), mgrid, dim3(128), 0, stream, p, g, pmax);
+    else if (nw == 4) hipLaunchKernelGGL((scores_mfma_kernel<128, 4>), mgrid, dim3(256), 0, stream, p, g, pmax);
+    else hipLaunchKernelGGL((scores_mfma_kernel<128, 8>), mgrid, dim3(512), 0, stream, p, g, pmax);
+  } else
     hipLaunchKernelGGL((scores_kernel<D, false>), sgrid, dim3(256), 0, stream, p, g, pmax);
   hipLaunchKernelGGL(rowmax_kernel, dim3(g.rows, nbkv), dim3(64), 0, stream, p, g, pmax);
   if (p.f16) hipLaunchKernelGGL(rowsum_kernel<true>, dim3(g.n_kb2, nbkv, g.sum_splits), dim3(256), 0, stream, p, g, psum);
