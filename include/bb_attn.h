@@ -33,8 +33,9 @@ extern "C" {
  *   201  bb_decode_step and bb_decode_step_workspace added
  *   202  bb_int8_quantize / bb_int8_quantize_pair take an element kind (0 bf16, 1 fp32, 2 fp16) where they took
  *        x_is_f32, and bb_int8_dequantize an output kind where it took out_is_f32 (the old values keep their
- *        meaning) */
-#define BB_ABI_VERSION 202
+ *        meaning)
+ *   203  bb_add_rms_norm, bb_silu_mul and bb_gemv added */
+#define BB_ABI_VERSION 203
 int bb_version(void);
 
 /* Message of the last failed call on this host thread ("" if none). */
@@ -273,6 +274,32 @@ int bb_argmax(const void* x, int64_t n, int dtype, int64_t* out, void* stream);
  */
 int bb_rms_norm(const void* x, int64_t sx, int rows, int D, const void* w, float eps, int is_f16, void* out,
                 int64_t so, void* stream);
+
+/*
+ * A decoder layer's residual add followed by the next RMSNorm, in one launch: sum = round(x + res) (a 16-bit tensor
+ * add), out = bb_rms_norm(sum). x, res, sum, out are `rows` rows of D values (row strides sx, sr, ssum, so; sum and
+ * out must not overlap x or res). Same limits as bb_rms_norm. Replaces `hidden + attn_out` / `hidden + mlp_out` and
+ * the norm after it in the HF decoder layers that the decode step runs (modal_rd/graph_decode.py:185,199-201).
+ */
+int bb_add_rms_norm(const void* x, int64_t sx, const void* res, int64_t sr, int rows, int D, const void* w, float eps,
+                    int is_f16, void* sum, int64_t ssum, void* out, int64_t so, void* stream);
+
+/*
+ * out = round(round(silu(g)) u) over n 16-bit values (bf16 or fp16 by is_f16; n % 8 == 0; 16-byte aligned buffers):
+ * the arithmetic of F.silu(gate) * up in a Llama MLP (silu in fp32 as g / (1 + exp(-g))), one launch. Replaces
+ * `act_fn(gate_proj(x)) * up_proj(x)` of the decode step's MLP (modal_rd/graph_decode.py:200, the HF module).
+ */
+int bb_silu_mul(const void* g, const void* u, int64_t n, int is_f16, void* out, void* stream);
+
+/*
+ * One token through a linear layer: y[N] = W[N, K] x[K] (W row stride sw >= K elements; 16-bit W, x, y, bf16 or
+ * fp16 by is_f16; fp32 accumulation, y rounded once). K % 8 == 0, K <= 16384; W rows and x 16-byte aligned. With
+ * glu, W holds 2N rows (a Llama MLP's gate rows [0, N) above its up rows [N, 2N)) and y[i] = bb_silu_mul of the
+ * rounded gate and up outputs i: the MLP's down-projection input in one launch. Replaces the bias-free projections
+ * of the decode step (q/k/v, o, gate / up, down: vendor GEMMs through nn.Linear in
+ * modal_rd/graph_decode.py:186-188,199-200); HBM-bound on streaming W once.
+ */
+int bb_gemv(const void* w, int64_t sw, int N, int K, const void* x, int glu, int is_f16, void* y, void* stream);
 
 /*
  * In-place RoPE on x [B, Hh, T, D] (strides sx[3]) with cos/sin [B, T, D] (strides sc[2]; 0 to broadcast), with

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_function():
 
 def test_version_and_sizes():
     L = _lib.lib()
-    assert L.bb_version() == 202  # the parameter lists of include/bb_attn.h (BB_ABI_VERSION)
+    assert L.bb_version() == 203  # the parameter lists of include/bb_attn.h (BB_ABI_VERSION)
     assert L.bb_transpose_v_cols(1) == 64 and L.bb_transpose_v_cols(64) == 64 and L.bb_transpose_v_cols(65) == 128
     assert L.bb_routes_workspace(131072, 32, 8, 1, 64) > 32 * 131072 * 8
     assert L.bb_decode_workspace(131072, 32, 8, 128) > 0
@@ -126,6 +126,29 @@ def test_argmax_argument_checks():
     assert L.bb_argmax(ctypes.c_void_p(16), 10, 3, out, None) != 0
     assert "dtype must be" in L.bb_last_error().decode()
     assert L.bb_argmax(None, 10, 1, out, None) != 0
+
+
+def test_decode_step_op_argument_checks():
+    """The decode step's fused residual-add + RMSNorm, SiLU-gate and one-token GEMV entry points refuse bad shapes
+    and alignment before touching the GPU."""
+    L = _lib.lib()
+    p, q = ctypes.c_void_p(256), ctypes.c_void_p(8)
+    assert L.bb_add_rms_norm(p, 4096, p, 4096, 1, 4100, p, 1e-5, 0, p, 4096, p, 4096, None) != 0
+    assert "hidden size" in L.bb_last_error().decode()
+    assert L.bb_add_rms_norm(p, 4096, q, 4096, 1, 4096, p, 1e-5, 0, p, 4096, p, 4096, None) != 0
+    assert "16-byte aligned" in L.bb_last_error().decode()
+    assert L.bb_add_rms_norm(p, 4096, None, 4096, 1, 4096, p, 1e-5, 0, p, 4096, p, 4096, None) != 0
+    assert "null" in L.bb_last_error().decode()
+    assert L.bb_silu_mul(p, p, 14340, 0, p, None) != 0
+    assert "multiple of 8" in L.bb_last_error().decode()
+    assert L.bb_silu_mul(p, q, 14336, 0, p, None) != 0
+    assert "aligned" in L.bb_last_error().decode()
+    assert L.bb_gemv(p, 16392, 4096, 16392, p, 0, 0, p, None) != 0  # K above 16384
+    assert "K = 16392" in L.bb_last_error().decode()
+    assert L.bb_gemv(p, 4100, 4096, 4096, p, 0, 0, p, None) != 0  # row stride not 16-byte aligned
+    assert "16-byte aligned" in L.bb_last_error().decode()
+    assert L.bb_gemv(p, 4096, 4096, 4096, None, 1, 0, p, None) != 0
+    assert "null" in L.bb_last_error().decode()
 
 
 def test_int8_layer_host_state_without_gpu():

@@ -171,3 +171,101 @@ def test_rms_norm_matches_hf(dtype, d, dev):
     ulp = want.float().abs() * (2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10) + 1e-30
     assert (diff <= ulp).all()
     assert (diff == 0).float().mean() > 0.95
+
+
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 4096), (torch.float16, 4096), (torch.bfloat16, 520)])
+def test_add_rms_norm_matches_torch_and_hf(dtype, d, dev):
+    """bb_add_rms_norm: the sum is the 16-bit tensor add bit for bit, and the norm of it is bb_rms_norm's bit for bit
+    (so within one unit in the last place of transformers' LlamaRMSNorm, as bb_rms_norm)."""
+    from transformers.models.llama.modeling_llama import LlamaRMSNorm
+
+    from bigger_bird_amd.decode import add_rms_norm, rms_norm
+
+    g = torch.Generator().manual_seed(8)
+    norm = LlamaRMSNorm(d, eps=1e-5).to(dev, dtype)
+    with torch.no_grad():
+        norm.weight.copy_((1 + 0.1 * torch.randn(d, generator=g)).to(dtype))
+    x = (torch.randn(1, 3, d, generator=g) * 3).to(dtype).to(dev)
+    r = (torch.randn(1, 3, d, generator=g) * 2).to(dtype).to(dev)
+    total, got = add_rms_norm(x, r, norm.weight, norm.variance_epsilon)
+    assert torch.equal(total, x + r)
+    assert torch.equal(got, rms_norm(x + r, norm.weight, norm.variance_epsilon))
+    want = norm(x + r)
+    diff = (got.float() - want.float()).abs()
+    assert (diff <= want.float().abs() * (2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10) + 1e-30).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_silu_mul_matches_torch(dtype, dev):
+    """bb_silu_mul against F.silu(g) * u on the same 16-bit inputs (wide range, signed zeros, +-inf, large
+    negative gates): the same fp32 arithmetic, so the results are bitwise equal (NaNs compared as NaNs)."""
+    from bigger_bird_amd.decode import silu_mul
+
+    gen = torch.Generator().manual_seed(9)
+    n = 14336 * 2
+    g = (torch.randn(n, generator=gen) * torch.exp2(torch.randint(-8, 7, (n,), generator=gen).float()))
+    u = torch.randn(n, generator=gen) * 4
+    g[:8] = torch.tensor([0.0, -0.0, float("inf"), -float("inf"), -100.0, 100.0, 1e-30, -1e-30])
+    g, u = g.to(dtype).to(dev), u.to(dtype).to(dev)
+    y = torch.empty(2 * n, dtype=dtype, device=dev)  # g and u as the two halves of one projection's output
+    y[:n], y[n:] = g, u
+    got = silu_mul(y[:n], y[n:])
+    want = torch.nn.functional.silu(g) * u
+    assert torch.equal(got.isnan(), want.isnan())
+    ok = ~want.isnan()
+    assert torch.equal(got[ok], want[ok])
+
+
+def test_fused_mlp_engaged_and_close_to_module(dev):
+    """The decode step's MLP on a Llama layer takes the fused path (gate and up as one projection whose weights are
+    views of one buffer, run as two HIP GEMVs) and agrees with the HF module to bf16 rounding of the projections."""
+    model = _tiny(dev)
+    dec = StaticDecoder(model, 64)
+    plan = dec.plans[0]
+    mlp = plan.layer.mlp
+    assert plan.gate_up_w is not None and plan.inter == mlp.gate_proj.weight.shape[0]
+    assert mlp.gate_proj.weight.data_ptr() == plan.gate_up_w.data_ptr()
+    assert plan.mlp_vec and plan.qkv_vec and plan.o_vec
+    x = torch.randn(1, 1, 512, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(dev)
+    with torch.no_grad():
+        got, want = StaticDecoder._mlp(plan, x), mlp(x)
+    assert (got.float() - want.float()).abs().max().item() <= 2e-2 * want.float().abs().max().item()
+
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n,k,stride", [(6144, 4096, 4096), (4096, 14336, 14336), (1001, 520, 520),
+                                        (37, 1000, 1024), (3, 16384, 16384)])
+def test_linear_vec_matches_fp32(n, k, stride, dtype, dev):
+    """bb_gemv (one token through a linear layer) against the fp32 product of the same 16-bit operands: fp32
+    accumulation of exact products and one rounding, so within half a unit in the last place of the result plus the
+    accumulation's own error; ragged N and K, a row stride larger than K, and the largest K."""
+    from bigger_bird_amd.decode import linear_vec
+
+    g = torch.Generator().manual_seed(n + k)
+    wfull = (torch.randn(n, stride, generator=g) * 0.05).to(dtype).to(dev)
+    w = wfull[:, :k]
+    x = torch.randn(1, 1, k, generator=g).to(dtype).to(dev)
+    got = linear_vec(x, w).float()
+    ref = x.float() @ w.float().t()
+    mag = x.float().abs() @ w.float().abs().t()
+    half_ulp = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11  # relative, at most
+    assert ((got - ref).abs() <= ref.abs() * half_ulp * 1.01 + mag * 2.0 ** -16 + 1e-30).all()
+    assert ((got - ref).abs() <= ref.abs() * 2.0 ** -9).float().mean() > 0.5  # not a looser rounding
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n,k", [(14336, 4096), (100, 520), (3, 64)])
+def test_linear_vec_glu_matches_gate_up(n, k, dtype, dev):
+    """bb_gemv with the SiLU gate on a fused [gate; up] weight: a row's sum does not depend on which rows share its
+    wave, so the gated output is F.silu(gate) * up of the plain GEMV's gate and up outputs, bit for bit (the same
+    arithmetic as bb_silu_mul, `test_silu_mul_matches_torch`); odd N included."""
+    from bigger_bird_amd.decode import linear_vec
+
+    g = torch.Generator().manual_seed(n)
+    w = (torch.randn(2 * n, k, generator=g) * 0.05).to(dtype).to(dev)
+    x = torch.randn(1, 1, k, generator=g).to(dtype).to(dev)
+    got = linear_vec(x, w, glu=True)
+    both = linear_vec(x, w)  # the same rows without the gate
+    want = torch.nn.functional.silu(both[..., :n]) * both[..., n:]
+    assert torch.equal(got, want)

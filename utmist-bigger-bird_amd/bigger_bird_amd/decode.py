@@ -228,17 +228,87 @@ def argmax_index(x, out=None):
     return out
 
 
+def _matrix16(x, d):
+    """x as [rows, d] with 16-byte aligned rows (a copy only when x's layout does not allow it)."""
+    x2 = x.reshape(-1, d)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    return x2
+
+
 def rms_norm(x, weight, eps):
     """transformers' LlamaRMSNorm on a 16-bit GPU tensor [..., D] in one launch (fp32 mean of squares,
     rsqrt(mean + eps), round to x's dtype, times `weight`, round); D % 8 == 0, D <= 8192."""
     if not x.is_cuda or x.dtype not in (torch.bfloat16, torch.float16) or weight.dtype != x.dtype:
         raise ValueError("rms_norm needs bf16/fp16 GPU tensors of one dtype")
     d = x.shape[-1]
-    x2 = x.reshape(-1, d)
-    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
-        x2 = x2.contiguous()
+    x2 = _matrix16(x, d)
     w = weight.contiguous()
     out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
     _lib.check(_lib.lib().bb_rms_norm(_lib.ptr(x2), x2.stride(0), x2.shape[0], d, _lib.ptr(w), float(eps),
                                       int(x.dtype == torch.float16), _lib.ptr(out), d, _lib.stream_of(x)))
     return out
+
+
+def add_rms_norm(x, res, weight, eps):
+    """A decoder layer's residual add and the RMSNorm after it, in one launch: returns (x + res, rms_norm(x + res))
+    with the arithmetic of the 16-bit tensor add and of transformers' LlamaRMSNorm (as `rms_norm`)."""
+    if (not x.is_cuda or x.dtype not in (torch.bfloat16, torch.float16) or res.dtype != x.dtype
+            or weight.dtype != x.dtype):
+        raise ValueError("add_rms_norm needs bf16/fp16 GPU tensors of one dtype")
+    if res.shape != x.shape:
+        raise ValueError("add_rms_norm: x and res must have one shape")
+    d = x.shape[-1]
+    x2, r2 = _matrix16(x, d), _matrix16(res, d)
+    w = weight.contiguous()
+    total = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    _lib.check(_lib.lib().bb_add_rms_norm(_lib.ptr(x2), x2.stride(0), _lib.ptr(r2), r2.stride(0), x2.shape[0], d,
+                                          _lib.ptr(w), float(eps), int(x.dtype == torch.float16), _lib.ptr(total), d,
+                                          _lib.ptr(out), d, _lib.stream_of(x)))
+    return total, out
+
+
+def silu_mul(g, u):
+    """F.silu(g) * u on 16-bit GPU tensors of one shape in one launch, with the arithmetic of those two torch ops
+    (silu in fp32, rounded; the product in fp32, rounded): the gate of a Llama MLP."""
+    if not g.is_cuda or g.dtype not in (torch.bfloat16, torch.float16) or u.dtype != g.dtype or u.shape != g.shape:
+        raise ValueError("silu_mul needs bf16/fp16 GPU tensors of one dtype and shape")
+    g2, u2 = g.contiguous(), u.contiguous()
+    if g2.numel() % 8 or g2.data_ptr() % 16 or u2.data_ptr() % 16:
+        raise ValueError("silu_mul: the length must be a multiple of 8 (16-byte aligned buffers)")
+    out = torch.empty(g.shape, dtype=g.dtype, device=g.device)
+    _lib.check(_lib.lib().bb_silu_mul(_lib.ptr(g2), _lib.ptr(u2), g2.numel(), int(g.dtype == torch.float16),
+                                      _lib.ptr(out), _lib.stream_of(g)))
+    return out
+
+
+def gemv_ok(weight, x=None):
+    """Whether `linear_vec` can run this weight (16-bit [N, K], K % 8 == 0, K <= 16384, 16-byte aligned rows) and,
+    if given, this input's dtype."""
+    return (weight.is_cuda and weight.dtype in (torch.bfloat16, torch.float16) and weight.ndim == 2
+            and weight.stride(1) == 1 and weight.stride(0) % 8 == 0 and weight.data_ptr() % 16 == 0
+            and 0 < weight.shape[1] <= 16384 and weight.shape[1] % 8 == 0 and (x is None or x.dtype == weight.dtype))
+
+
+def linear_vec(x, weight, glu=False):
+    """One token through a bias-free linear layer, y = x W^T (x [..., K] holding K values in all; y [..., M] for W
+    [M, K]), as one HBM-streaming HIP launch. glu: W is a fused [gate; up] projection [2M, K] and y = silu(x gate^T) *
+    (x up^T) with the rounding of those torch ops on 16-bit tensors (`silu_mul`'s arithmetic): a Llama MLP's
+    activation input."""
+    m, k = weight.shape
+    if not gemv_ok(weight, x) or not x.is_cuda:
+        raise ValueError("linear_vec needs a 16-bit GPU weight [N, K] (K % 8 == 0, K <= 16384, aligned rows) "
+                         "and an input of its dtype")
+    if x.numel() != k:
+        raise ValueError("linear_vec takes one token: x must hold K values")
+    if glu and m % 2:
+        raise ValueError("linear_vec(glu=True) needs a [2N, K] gate / up weight")
+    n = m // 2 if glu else m
+    x1 = x.reshape(-1)
+    if x1.data_ptr() % 16:
+        x1 = x1.clone()
+    y = torch.empty(x.shape[:-1] + (n,), dtype=x.dtype, device=x.device)
+    _lib.check(_lib.lib().bb_gemv(_lib.ptr(weight), weight.stride(0), n, k, _lib.ptr(x1), int(glu),
+                                  int(x.dtype == torch.float16), _lib.ptr(y), _lib.stream_of(x)))
+    return y

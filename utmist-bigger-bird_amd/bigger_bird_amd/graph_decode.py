@@ -14,16 +14,21 @@ generate / EOS / rewind / feed protocol. The design is this package's own:
   shape and reads its varying values from device memory: the step is captured once and replayed per token.
 * Step (one token through the model): embedding; per layer RMSNorm -> one fused QKV projection (the q, k and v
   weights concatenated once at construction when they are plain bias-free Linear layers of one dtype) -> RoPE on q and
-  k in place -> attention, which also writes the new K and V row into the arena at `slot` = n - 1 -> o_proj,
-  residual -> RMSNorm -> MLP, residual; final norm, lm_head, greedy token by a one-workgroup HIP argmax written
-  straight into the control block.
+  k in place (one launch over both) -> attention, which also writes the new K and V row into the arena at `slot` =
+  n - 1 -> o_proj, residual + RMSNorm (one launch) -> MLP (gate and up as one fused projection whose launch also
+  applies SiLU(gate) * up, then down), residual + the next RMSNorm (one launch); final norm, lm_head, greedy token
+  by a one-workgroup HIP argmax written straight into the control block. The projections run as bb_gemv (one token:
+  a matrix-vector product streaming the weight once, faster at batch 1 than the vendor GEMM) where the weight is a
+  16-bit bias-free Linear with K <= 16384; 9 launches per layer on a Llama layer.
 * Attention per layer: one bb_decode_step. Dense layers run split-K flash decoding over the filled rows (front 0,
   window = capacity, no routes, length read on the GPU); `sparse_decode={"front", "window", "routed"}` switches the
   non-dense RDAttention layers to fused decode routing (pooled per KV head) + sparse decode. The first kernel that
   reads the cache takes the new row from the projection output and stores it in the arena, so the append needs no
   launch of its own (bit-identical to bb_kv_append followed by bigger_bird_decode / bigger_bird_route).
-* On bf16 / fp16 models the RMSNorms run as one bb_rms_norm launch each and RoPE as bb_rope_inplace (bit-identical to
-  HF apply_rotary_pos_emb): at batch 1 the HF modules' elementwise launches cost more than their arithmetic.
+* On bf16 / fp16 models the RMSNorms run as one bb_rms_norm launch each (bb_add_rms_norm with the residual add before
+  them), RoPE as bb_rope_inplace (bit-identical to HF apply_rotary_pos_emb) and the MLP's activation as bb_silu_mul:
+  at batch 1 the HF modules' elementwise launches cost more than their arithmetic. Modules of other types run as
+  they are.
 * A captured step holds no memset node and no multi-workgroup reduction of torch's (those have given wrong results
   on replays after the first on these boxes).
 * Not supported: the INT8 KV cache, batch > 1, sampling (as in the reference).
@@ -36,7 +41,7 @@ from transformers.cache_utils import DynamicLayer
 from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
 
 from .attention import rope_inplace
-from .decode import argmax_index, decode_step, rms_norm
+from .decode import add_rms_norm, argmax_index, decode_step, gemv_ok, linear_vec, rms_norm, silu_mul
 
 # Control block: slot indices and the per-step / per-token increments.
 N, POS, TOK, MADE, SLOT = range(5)
@@ -90,6 +95,23 @@ class _LayerPlan:
         if all(_plain_linear(p) for p in projs) and len({p.weight.dtype for p in projs}) == 1:
             with torch.inference_mode(False), torch.no_grad():
                 self.qkv_w = _fuse_rows([p.weight for p in projs])
+        # a Llama MLP (down(silu(gate(x)) * up(x)), plain 16-bit Linear layers): gate and up as one projection
+        mlp = layer.mlp
+        self.gate_up_w, self.inter = None, 0
+        lin = [getattr(mlp, n, None) for n in ("gate_proj", "up_proj", "down_proj")]
+        silu = type(getattr(mlp, "act_fn", None)).__name__ in ("SiLU", "SiLUActivation")  # torch's or HF's F.silu
+        if (silu and all(_plain_linear(m) for m in lin)
+                and len({m.weight.dtype for m in lin}) == 1 and lin[0].weight.dtype in (torch.bfloat16, torch.float16)
+                and lin[0].weight.shape == lin[1].weight.shape and lin[0].weight.shape[0] % 8 == 0):
+            with torch.inference_mode(False), torch.no_grad():
+                self.gate_up_w = _fuse_rows([lin[0].weight, lin[1].weight])
+            self.inter = lin[0].weight.shape[0]
+        # one-token projections on the HIP GEMV where the weight allows it (else nn.Linear / F.linear)
+        self.qkv_vec = self.qkv_w is not None and gemv_ok(self.qkv_w)
+        o = base.o_proj
+        self.o_vec = _plain_linear(o) and gemv_ok(o.weight)
+        self.mlp_vec = (self.gate_up_w is not None and gemv_ok(self.gate_up_w)
+                        and gemv_ok(layer.mlp.down_proj.weight))
 
 
 def _fuse_rows(weights):
@@ -191,26 +213,62 @@ class StaticDecoder:
         self.token.fill_(int(token))
 
     # ---- the step ----
-    def _norm(self, module, x):
-        """An RMSNorm module on x: one bb_rms_norm launch for the plain bf16/fp16 Llama module, else the module."""
+    @staticmethod
+    def _fast_norm(module, x):
+        """(weight, eps) of a plain bf16/fp16 Llama RMSNorm module that the HIP norm can run on x, else None."""
         w, eps = getattr(module, "weight", None), getattr(module, "variance_epsilon", None)
         fast = (type(module).__name__.endswith("RMSNorm") and w is not None and eps is not None
                 and w.dtype == x.dtype and x.dtype in (torch.bfloat16, torch.float16)
                 and x.shape[-1] % 8 == 0 and x.shape[-1] <= 8192)
-        return rms_norm(x, w, eps) if fast else module(x)
+        return (w, eps) if fast else None
+
+    def _norm(self, module, x):
+        """An RMSNorm module on x: one bb_rms_norm launch for the plain bf16/fp16 Llama module, else the module."""
+        f = self._fast_norm(module, x)
+        return rms_norm(x, *f) if f else module(x)
+
+    def _add_norm(self, module, hid, res):
+        """(hid + res, module(hid + res)); one bb_add_rms_norm launch where the module allows (res None: no add)."""
+        if res is None:
+            return hid, self._norm(module, hid)
+        f = self._fast_norm(module, hid)
+        if f and res.dtype == hid.dtype and res.shape == hid.shape:
+            return add_rms_norm(hid, res, *f)
+        hid = hid + res
+        return hid, module(hid)
+
+    @staticmethod
+    def _mlp(plan, x):
+        """The layer's MLP on the normed x: two HIP GEMVs (the fused gate / up projection with the SiLU gate, then
+        down) where the weights allow; else the fused projection, bb_silu_mul and down_proj; else the module."""
+        mlp = plan.layer.mlp
+        if plan.mlp_vec:
+            return linear_vec(linear_vec(x, plan.gate_up_w, glu=True), mlp.down_proj.weight)
+        if plan.gate_up_w is None:
+            return mlp(x)
+        y = torch.nn.functional.linear(x, plan.gate_up_w)
+        return mlp.down_proj(silu_mul(y[..., :plan.inter], y[..., plan.inter:]))
+
+    @staticmethod
+    def _o_proj(plan, o):
+        """o_proj on the attention output [H, d] of one token -> [1, 1, hidden]."""
+        o = o.reshape(1, 1, -1)
+        return linear_vec(o, plan.base.o_proj.weight) if plan.o_vec else plan.base.o_proj(o)
 
     def _qkv(self, plan, x):
         """Projections of the normed input x [1, 1, hidden]: q [1, H, 1, d], k and v [1, Hkv, 1, d], and, with the
-        fused projection, the [2, Hkv, 1, d] view of its K and V part (so RoPE on k in place also lands there)."""
+        fused projection, the [2, Hkv, 1, d] view of its K and V part (so RoPE on k in place also lands there) and the
+        [1, H + Hkv, 1, d] view of q and k together (one RoPE launch for both)."""
         h, hk, d = self.h, self.hk, self.d
         if plan.qkv_w is not None:
-            y = torch.nn.functional.linear(x, plan.qkv_w)[0, 0]
+            y = (linear_vec(x, plan.qkv_w) if plan.qkv_vec else torch.nn.functional.linear(x, plan.qkv_w))[0, 0]
             q, k, v = y.split((h * d, hk * d, hk * d))
             kv = y[h * d:].view(2, hk, 1, d)
+            qk = y[:(h + hk) * d].view(1, h + hk, 1, d)
         else:
             q, k, v = (p(x)[0, 0] for p in (plan.base.q_proj, plan.base.k_proj, plan.base.v_proj))
-            kv = None
-        return q.view(1, h, 1, d), k.view(1, hk, 1, d), v.view(1, hk, 1, d), kv
+            kv = qk = None
+        return q.view(1, h, 1, d), k.view(1, hk, 1, d), v.view(1, hk, 1, d), kv, qk
 
     def _attend(self, i, plan, q, kn, vn):
         """q [H, d] of the new token, its K / V rows kn / vn [Hkv, d] -> [H, d]. The rows become arena row
@@ -227,21 +285,27 @@ class StaticDecoder:
         hid = self.core.embed_tokens(self.token)
         cos, sin = self.core.rotary_emb(hid, self.position.view(1, 1))
         self.ctl.add_(self._claim)
+        pending = None  # the last MLP's output, added to hid together with the next norm
         for i, plan in enumerate(self.plans):
             layer = plan.layer
-            q, k, v, kv = self._qkv(plan, self._norm(layer.input_layernorm, hid))
+            hid, x = self._add_norm(layer.input_layernorm, hid, pending)
+            q, k, v, kv, qk = self._qkv(plan, x)
             if q.dtype == torch.bfloat16 and cos.dtype == torch.bfloat16:
-                rope_inplace(q, cos, sin)
-                rope_inplace(k, cos, sin)
+                if qk is not None:
+                    rope_inplace(qk, cos, sin)
+                else:
+                    rope_inplace(q, cos, sin)
+                    rope_inplace(k, cos, sin)
             else:
                 q, k = apply_rotary_pos_emb(q, k, cos, sin)
                 kv = None
             if kv is None:
                 kv = torch.stack((k[0], v[0]))
             o = self._attend(i, plan, q[0, :, 0], kv[0, :, 0], kv[1, :, 0])
-            hid = hid + plan.base.o_proj(o.reshape(1, 1, -1))
-            hid = hid + layer.mlp(self._norm(layer.post_attention_layernorm, hid))
-        self.logits = self.model.lm_head(self._norm(self.core.norm, hid))[0, -1]
+            hid, x = self._add_norm(layer.post_attention_layernorm, hid, self._o_proj(plan, o))
+            pending = self._mlp(plan, x)
+        hid, x = self._add_norm(self.core.norm, hid, pending)
+        self.logits = self.model.lm_head(x)[0, -1]
         argmax_index(self.logits, out=self._token_flat)
         self.out.index_copy_(0, self.step_i, self._token_flat)
         self.ctl.add_(self._advance)

@@ -782,10 +782,47 @@ int bb_rms_norm(const void* x, int64_t sx, int rows, int D, const void* w, float
   if (rows < 0 || D <= 0 || D % 8 || D > 8192) return fail("rms_norm: hidden size %d unsupported", D);
   if (!aligned(x, 16) || !aligned(w, 16) || !aligned(out, 16) || sx % 8 || so % 8)
     return fail("rms_norm: rows must be 16-byte aligned");
-  return hip_status(bb::launch_rms_norm(static_cast<const uint16_t*>(x), sx, rows, D, static_cast<const uint16_t*>(w),
-                                        eps, is_f16 ? 1 : 0, static_cast<uint16_t*>(out), so,
-                                        static_cast<hipStream_t>(stream)),
+  return hip_status(bb::launch_rms_norm(static_cast<const uint16_t*>(x), sx, nullptr, 0, rows, D,
+                                        static_cast<const uint16_t*>(w), eps, is_f16 ? 1 : 0,
+                                        static_cast<uint16_t*>(out), so, nullptr, 0, static_cast<hipStream_t>(stream)),
                     "bb_rms_norm");
+}
+
+int bb_add_rms_norm(const void* x, int64_t sx, const void* res, int64_t sr, int rows, int D, const void* w, float eps,
+                    int is_f16, void* sum, int64_t ssum, void* out, int64_t so, void* stream) {
+  g_err[0] = 0;
+  if (!x || !res || !w || !sum || !out) return fail("add_rms_norm: null argument");
+  if (rows < 0 || D <= 0 || D % 8 || D > 8192) return fail("add_rms_norm: hidden size %d unsupported", D);
+  if (!aligned(x, 16) || !aligned(res, 16) || !aligned(w, 16) || !aligned(sum, 16) || !aligned(out, 16) || sx % 8 ||
+      sr % 8 || ssum % 8 || so % 8)
+    return fail("add_rms_norm: rows must be 16-byte aligned");
+  return hip_status(bb::launch_rms_norm(static_cast<const uint16_t*>(x), sx, static_cast<const uint16_t*>(res), sr,
+                                        rows, D, static_cast<const uint16_t*>(w), eps, is_f16 ? 1 : 0,
+                                        static_cast<uint16_t*>(out), so, static_cast<uint16_t*>(sum), ssum,
+                                        static_cast<hipStream_t>(stream)),
+                    "bb_add_rms_norm");
+}
+
+int bb_gemv(const void* w, int64_t sw, int N, int K, const void* x, int glu, int is_f16, void* y, void* stream) {
+  g_err[0] = 0;
+  if (!w || !x || !y) return fail("gemv: null argument");
+  if (N < 0 || K <= 0 || K % 8 || K > 16384) return fail("gemv: K = %d must be a positive multiple of 8, at most 16384", K);
+  if (!aligned(w, 16) || !aligned(x, 16) || sw % 8 || sw < K || !aligned(y, 2))
+    return fail("gemv: W rows and x must be 16-byte aligned");
+  return hip_status(bb::launch_gemv(static_cast<const uint16_t*>(w), sw, N, K, static_cast<const uint16_t*>(x),
+                                    glu != 0, is_f16 ? 1 : 0, static_cast<uint16_t*>(y),
+                                    static_cast<hipStream_t>(stream)),
+                    "bb_gemv");
+}
+
+int bb_silu_mul(const void* g, const void* u, int64_t n, int is_f16, void* out, void* stream) {
+  g_err[0] = 0;
+  if (!g || !u || !out) return fail("silu_mul: null argument");
+  if (n < 0 || n % 8) return fail("silu_mul: length %lld must be a multiple of 8", (long long)n);
+  if (!aligned(g, 16) || !aligned(u, 16) || !aligned(out, 16)) return fail("silu_mul: buffers must be 16-byte aligned");
+  return hip_status(bb::launch_silu_mul(static_cast<const uint16_t*>(g), static_cast<const uint16_t*>(u), n,
+                                        is_f16 ? 1 : 0, static_cast<uint16_t*>(out), static_cast<hipStream_t>(stream)),
+                    "bb_silu_mul");
 }
 
 int bb_argmax(const void* x, int64_t n, int dtype, int64_t* out, void* stream) {

@@ -558,12 +558,15 @@ __global__ __launch_bounds__(kAmThreads) void argmax_kernel(const T* __restrict_
 // ---------------------------------------------------------------------------------------------------------------
 // RMSNorm of a decode step's hidden rows with the arithmetic of HF LlamaRMSNorm on a 16-bit model: x in fp32,
 // r = rsqrt(mean(x^2) + eps), y = round(x r) to the model dtype, out = round(w y). One 256-thread workgroup per
-// row, 8 values per 16-byte load (D % 8 == 0, D <= 8192).
+// row, 8 values per 16-byte load (D % 8 == 0, D <= 8192). RES: x is first replaced by round(x + res) (the residual
+// add of a decoder layer, as a 16-bit tensor add computes it), which is also written to sum.
 constexpr int kRnThreads = 256;
-template <bool F16>
+template <bool F16, bool RES>
 __global__ __launch_bounds__(kRnThreads) void rms_norm_kernel(const uint16_t* __restrict__ x, int64_t sx,
+                                                              const uint16_t* __restrict__ res, int64_t sr,
                                                               const uint16_t* __restrict__ w, int D, float eps,
-                                                              uint16_t* __restrict__ out, int64_t so) {
+                                                              uint16_t* __restrict__ out, int64_t so,
+                                                              uint16_t* __restrict__ sum, int64_t ssum) {
   __shared__ float red[kRnThreads / 64];
   const int row = blockIdx.x, tid = threadIdx.x;
   const uint16_t* xr = x + (int64_t)row * sx;
@@ -574,6 +577,21 @@ __global__ __launch_bounds__(kRnThreads) void rms_norm_kernel(const uint16_t* __
   for (int u = 0; u < kMaxUnits; ++u) {
     const int c = (u * kRnThreads + tid) * 8;
     xv[u] = c < D ? ld16(xr + c) : u32x4_t{0, 0, 0, 0};
+    if (RES && c < D) {
+      const u32x4_t rv = ld16(res + (int64_t)row * sr + c);
+#pragma unroll
+      for (int e2 = 0; e2 < 4; ++e2) {
+        uint32_t pair = 0;
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) {
+          const float a = elem_to_f32<F16>((uint16_t)(xv[u][e2] >> (16 * hb)));
+          const float b = elem_to_f32<F16>((uint16_t)(rv[e2] >> (16 * hb)));
+          pair |= (uint32_t)f32_to_elem<F16>(a + b) << (16 * hb);
+        }
+        xv[u][e2] = pair;
+      }
+      st16(sum + (int64_t)row * ssum + c, xv[u]);
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float f = elem_to_f32<F16>((uint16_t)(xv[u][e >> 1] >> (16 * (e & 1))));
@@ -605,6 +623,128 @@ __global__ __launch_bounds__(kRnThreads) void rms_norm_kernel(const uint16_t* __
       o[e2] = pair;
     }
     st16(out + (int64_t)row * so + c, o);
+  }
+}
+
+// out = round(round(silu(g)) u) elementwise over n values (n % 8 == 0, 16-byte aligned): the arithmetic of
+// F.silu(g) * u on 16-bit tensors (silu in fp32 as g / (1 + exp(-g)), rounded; the product in fp32, rounded), i.e.
+// the activation of a Llama MLP between its gate / up and down projections.
+template <bool F16>
+BB_DEV u32x4_t silu_mul8(u32x4_t gv, u32x4_t uv) {
+  u32x4_t o;
+#pragma unroll
+  for (int e2 = 0; e2 < 4; ++e2) {
+    uint32_t pair = 0;
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+      const float x = elem_to_f32<F16>((uint16_t)(gv[e2] >> (16 * hb)));
+      const float a = elem_to_f32<F16>(f32_to_elem<F16>(x / (1.0f + expf(-x))));
+      const float b = elem_to_f32<F16>((uint16_t)(uv[e2] >> (16 * hb)));
+      pair |= (uint32_t)f32_to_elem<F16>(a * b) << (16 * hb);
+    }
+    o[e2] = pair;
+  }
+  return o;
+}
+
+template <bool F16>
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u,
+                                                       int64_t n, uint16_t* __restrict__ out) {
+  const int64_t c = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (c >= n) return;
+  st16(out + c, silu_mul8<F16>(ld16(g + c), ld16(u + c)));
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// One token through a linear layer, y[N] = W[N, K] x[K] (16-bit W rows of stride sw; fp32 accumulation, y rounded
+// to the model dtype): the decode step's projections, HBM-bound on streaming W once. A workgroup is 4 waves; each
+// group of KS waves takes R rows, the KS waves of a group taking consecutive parts of K; lane l of a wave takes the
+// 16-byte chunks l, l + 64, ... of its part of the rows (512 values per step), with A steps of its R rows' loads in
+// flight, and x is staged once per workgroup in LDS (after the first steps' W loads are issued, so the staging hides
+// under their latency). Each lane sums its share of a row with v_dot2c_f32_{bf16,f16}, the wave sums the lanes, and
+// the KS waves' sums are added in LDS in wave order. GLU: W holds 2N rows, gate rows [0, N) above up rows [N, 2N) (a Llama MLP's fused
+// gate / up projection); a wave takes R / 2 outputs i with both their rows i and N + i, and writes
+// round(round(silu(g)) u) of the rounded g and u (silu_mul_kernel's arithmetic): the MLP's activation input.
+constexpr int kGvWaves = 4;
+constexpr int kGvMaxK = 16384;  // x staged in 32 KB of LDS
+template <bool F16, bool GLU, int R, int A, int KS>
+__global__ __launch_bounds__(64 * kGvWaves) void gemv_kernel(const uint16_t* __restrict__ w, int64_t sw, int N, int K,
+                                                              const uint16_t* __restrict__ x,
+                                                              uint16_t* __restrict__ y) {
+  static_assert(!GLU || R % 2 == 0, "GLU rows come in (gate, up) pairs");
+  static_assert(kGvWaves % KS == 0, "K parts split the workgroup's waves evenly");
+  constexpr int OUTS = GLU ? R / 2 : R;  // outputs per group of KS waves
+  __shared__ __attribute__((aligned(16))) uint16_t xs[kGvMaxK];
+  __shared__ float part[KS > 1 ? kGvWaves : 1][R];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int grp = wave / KS, kp = wave % KS;
+  const int out0 = (blockIdx.x * (kGvWaves / KS) + grp) * OUTS;
+  const int kc = K / 8, nsteps = (kc + 63) / 64;  // 16-byte chunks per row, 512-value steps
+  const int sbeg = nsteps * kp / KS, steps = nsteps * (kp + 1) / KS - sbeg;  // this wave's steps
+  const uint16_t* wr[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int o = out0 + (GLU ? r / 2 : r);
+    const int oc = o < N ? o : N - 1;  // rows past the end read the last row; their outputs are not stored
+    wr[r] = w + (int64_t)(GLU ? oc + (r & 1) * N : oc) * sw;
+  }
+  auto load = [&](int st, u32x4_t (&dst)[R]) {
+    const int c = (sbeg + st) * 64 + lane;
+#pragma unroll
+    for (int r = 0; r < R; ++r) dst[r] = c < kc ? ld16(wr[r] + 8 * c) : u32x4_t{0, 0, 0, 0};
+  };
+  u32x4_t buf[A][R];
+#pragma unroll
+  for (int a = 0; a < A; ++a)
+    if (a < steps) load(a, buf[a]);
+  for (int c = tid; c < nsteps * 64; c += 64 * kGvWaves)
+    *reinterpret_cast<u32x4_t*>(&xs[8 * c]) = c < kc ? ld16(x + 8 * c) : u32x4_t{0, 0, 0, 0};
+  __syncthreads();
+  float acc[R] = {};
+  for (int s0 = 0; s0 < steps; s0 += A) {
+#pragma unroll
+    for (int a = 0; a < A; ++a) {
+      const int st = s0 + a;
+      if (st < steps) {
+        const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(&xs[8 * ((sbeg + st) * 64 + lane)]);
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[r] = dot2<F16>(buf[a][r][e], xv[e], acc[r]);
+        if (st + A < steps) load(st + A, buf[a]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+  if constexpr (KS > 1) {
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) part[wave][r] = acc[r];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float t = part[grp * KS][r];
+#pragma unroll
+      for (int j = 1; j < KS; ++j) t += part[grp * KS + j][r];
+      acc[r] = t;
+    }
+    if (kp != 0) return;
+  }
+  if (lane < OUTS && out0 + lane < N) {
+    float v = acc[0];  // acc[lane] with a static index
+#pragma unroll
+    for (int r = 1; r < OUTS; ++r) v = lane == r ? acc[GLU ? 2 * r : r] : v;
+    if constexpr (GLU) {
+      float u = acc[1];
+#pragma unroll
+      for (int r = 1; r < OUTS; ++r) u = lane == r ? acc[2 * r + 1] : u;
+      const uint32_t gp = f32_to_elem<F16>(v), up = f32_to_elem<F16>(u);
+      y[out0 + lane] = (uint16_t)silu_mul8<F16>(u32x4_t{gp, 0, 0, 0}, u32x4_t{up, 0, 0, 0})[0];
+    } else {
+      y[out0 + lane] = f32_to_elem<F16>(v);
+    }
   }
 }
 
@@ -692,14 +832,61 @@ hipError_t launch_argmax(const void* x, int64_t n, int kind, bool vec16, int64_t
   return hipGetLastError();
 }
 
-hipError_t launch_rms_norm(const uint16_t* x, int64_t sx, int rows, int D, const uint16_t* w, float eps, int f16,
-                           uint16_t* out, int64_t so, hipStream_t stream) {
+hipError_t launch_rms_norm(const uint16_t* x, int64_t sx, const uint16_t* res, int64_t sr, int rows, int D,
+                           const uint16_t* w, float eps, int f16, uint16_t* out, int64_t so, uint16_t* sum,
+                           int64_t ssum, hipStream_t stream) {
   if (rows <= 0) return hipSuccess;
-  if (D <= 0 || D % 8 || D > 8192) return hipErrorInvalidValue;
-  if (f16)
-    hipLaunchKernelGGL(rms_norm_kernel<true>, dim3(rows), dim3(kRnThreads), 0, stream, x, sx, w, D, eps, out, so);
-  else
-    hipLaunchKernelGGL(rms_norm_kernel<false>, dim3(rows), dim3(kRnThreads), 0, stream, x, sx, w, D, eps, out, so);
+  if (D <= 0 || D % 8 || D > 8192 || (res != nullptr) != (sum != nullptr)) return hipErrorInvalidValue;
+  const dim3 grid(rows), block(kRnThreads);
+  if (res) {
+    if (f16)
+      hipLaunchKernelGGL((rms_norm_kernel<true, true>), grid, block, 0, stream, x, sx, res, sr, w, D, eps, out, so,
+                         sum, ssum);
+    else
+      hipLaunchKernelGGL((rms_norm_kernel<false, true>), grid, block, 0, stream, x, sx, res, sr, w, D, eps, out, so,
+                         sum, ssum);
+  } else if (f16) {
+    hipLaunchKernelGGL((rms_norm_kernel<true, false>), grid, block, 0, stream, x, sx, res, sr, w, D, eps, out, so,
+                       sum, ssum);
+  } else {
+    hipLaunchKernelGGL((rms_norm_kernel<false, false>), grid, block, 0, stream, x, sx, res, sr, w, D, eps, out, so,
+                       sum, ssum);
+  }
+  return hipGetLastError();
+}
+
+template <bool F16, bool GLU, int R, int A, int KS>
+hipError_t launch_gemv_t(const uint16_t* w, int64_t sw, int N, int K, const uint16_t* x, uint16_t* y,
+                         hipStream_t stream) {
+  constexpr int outs = (GLU ? R / 2 : R) * (kGvWaves / KS);  // outputs per workgroup
+  hipLaunchKernelGGL((gemv_kernel<F16, GLU, R, A, KS>), dim3((unsigned)((N + outs - 1) / outs)), dim3(64 * kGvWaves),
+                     0, stream, w, sw, N, K, x, y);
+  return hipGetLastError();
+}
+
+// Rows per group R = 2, A = 8 steps in flight, K in KS = 2 parts: the fastest of the (R, A, KS) shapes measured for
+// Llama-3-8B's decode projections (q/k/v 6144 x 4096, o 4096 x 4096, gate / up 28672 x 4096, down 4096 x 14336:
+// 12.2, 10.7, 40.3 and 23.3 us, against 12.0-14.1, 10.8-11.7, 42.3-50.4 and 24.0-31.0 us for (4, 4, 1), (2, 8, 1),
+// (4, 2, 4), (4, 4, 4), (2, 4, 4) and (4, 4, 2)).
+constexpr int kGvR = 2, kGvA = 8, kGvKS = 2;
+
+hipError_t launch_gemv(const uint16_t* w, int64_t sw, int N, int K, const uint16_t* x, bool glu, int f16, uint16_t* y,
+                       hipStream_t stream) {
+  if (N <= 0) return hipSuccess;
+  if (K <= 0 || K % 8 || K > kGvMaxK) return hipErrorInvalidValue;
+  if (f16) return glu ? launch_gemv_t<true, true, kGvR, kGvA, kGvKS>(w, sw, N, K, x, y, stream)
+                      : launch_gemv_t<true, false, kGvR, kGvA, kGvKS>(w, sw, N, K, x, y, stream);
+  return glu ? launch_gemv_t<false, true, kGvR, kGvA, kGvKS>(w, sw, N, K, x, y, stream)
+             : launch_gemv_t<false, false, kGvR, kGvA, kGvKS>(w, sw, N, K, x, y, stream);
+}
+
+hipError_t launch_silu_mul(const uint16_t* g, const uint16_t* u, int64_t n, int f16, uint16_t* out,
+                           hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  if (n % 8) return hipErrorInvalidValue;
+  const unsigned blocks = (unsigned)((n / 8 + 255) / 256);
+  if (f16) hipLaunchKernelGGL(silu_mul_kernel<true>, dim3(blocks), dim3(256), 0, stream, g, u, n, out);
+  else hipLaunchKernelGGL(silu_mul_kernel<false>, dim3(blocks), dim3(256), 0, stream, g, u, n, out);
   return hipGetLastError();
 }
 

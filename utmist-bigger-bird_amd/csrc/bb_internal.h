@@ -171,8 +171,17 @@ hipError_t launch_gather_rows(const uint16_t* src, int64_t ss0, int64_t ss1, int
                               const int64_t* idx, int64_t si0, int m, int D, uint16_t* dst, int64_t sd0, int64_t sd1,
                               hipStream_t stream);
 // HF LlamaRMSNorm arithmetic on rows of a 16-bit tensor (D % 8 == 0, D <= 8192).
-hipError_t launch_rms_norm(const uint16_t* x, int64_t sx, int rows, int D, const uint16_t* w, float eps, int f16,
-                           uint16_t* out, int64_t so, hipStream_t stream);
+// (res, sum both null, or both set: x + res is normalised and written to sum)
+hipError_t launch_rms_norm(const uint16_t* x, int64_t sx, const uint16_t* res, int64_t sr, int rows, int D,
+                           const uint16_t* w, float eps, int f16, uint16_t* out, int64_t so, uint16_t* sum,
+                           int64_t ssum, hipStream_t stream);
+// y[N] = W[N, K] x[K] for one token (16-bit, row stride sw; K % 8 == 0, K <= 16384; 16-byte aligned rows and x);
+// silu: x is [2K] and the product takes round(round(silu(x[:K])) x[K:]).
+hipError_t launch_gemv(const uint16_t* w, int64_t sw, int N, int K, const uint16_t* x, bool silu, int f16,
+                       uint16_t* y, hipStream_t stream);
+// out = round(round(silu(g)) u) over n values (n % 8 == 0, 16-byte aligned).
+hipError_t launch_silu_mul(const uint16_t* g, const uint16_t* u, int64_t n, int f16, uint16_t* out,
+                           hipStream_t stream);
 // Index of the largest element of x [n] (kind 0 fp32, 1 bf16, 2 fp16; vec16: 16-byte aligned), to out[0].
 // Decode-step cache append at a device-side length (advanced by n_inc afterwards).
 hipError_t launch_kv_append(uint16_t* k, int64_t sk0, int64_t sk1, uint16_t* v, int64_t sv0, int64_t sv1,
