@@ -34,7 +34,7 @@ extern "C" {
  *   202  bb_int8_quantize / bb_int8_quantize_pair take an element kind (0 bf16, 1 fp32, 2 fp16) where they took
  *        x_is_f32, and bb_int8_dequantize an output kind where it took out_is_f32 (the old values keep their
  *        meaning)
- *   203  bb_add_rms_norm, bb_silu_mul and bb_gemv added */
+ *   203  bb_add_rms_norm, bb_silu_mul, bb_gemv and bb_gemv_norm added */
 #define BB_ABI_VERSION 203
 int bb_version(void);
 
@@ -300,6 +300,16 @@ int bb_silu_mul(const void* g, const void* u, int64_t n, int is_f16, void* out, 
  * modal_rd/graph_decode.py:186-188,199-200); HBM-bound on streaming W once.
  */
 int bb_gemv(const void* w, int64_t sw, int N, int K, const void* x, int glu, int is_f16, void* y, void* stream);
+
+/*
+ * bb_gemv on the RMSNorm of a hidden row: y = W rms_norm(x + res) with norm weight norm_w [K] and eps, where sum =
+ * x + res is also written (res and sum both null: no add). Bit-identical to bb_add_rms_norm (or bb_rms_norm)
+ * followed by bb_gemv, in one launch (every workgroup normalises the row itself). K <= 8192; sum must not overlap x
+ * or res. Replaces a decoder layer's residual add, norm and following projection in the decode step
+ * (modal_rd/graph_decode.py:185-188,199-200).
+ */
+int bb_gemv_norm(const void* w, int64_t sw, int N, int K, const void* x, const void* res, const void* norm_w,
+                 float eps, int glu, int is_f16, void* sum, void* y, void* stream);
 
 /*
  * In-place RoPE on x [B, Hh, T, D] (strides sx[3]) with cos/sin [B, T, D] (strides sc[2]; 0 to broadcast), with

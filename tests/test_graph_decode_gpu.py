@@ -269,3 +269,26 @@ def test_linear_vec_glu_matches_gate_up(n, k, dtype, dev):
     both = linear_vec(x, w)  # the same rows without the gate
     want = torch.nn.functional.silu(both[..., :n]) * both[..., n:]
     assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n,k,glu,with_res", [(6144, 4096, False, True), (1000, 4096, True, True),
+                                              (37, 520, False, False), (64, 8192, True, False)])
+def test_linear_vec_norm_is_norm_then_gemv(n, k, glu, with_res, dtype, dev):
+    """bb_gemv_norm: every workgroup normalises the hidden row with bb_rms_norm's arithmetic, so (sum, y) equal
+    bb_add_rms_norm (or bb_rms_norm) followed by bb_gemv bit for bit."""
+    from bigger_bird_amd.decode import add_rms_norm, linear_vec, linear_vec_norm, rms_norm
+
+    g = torch.Generator().manual_seed(k + n)
+    w = (torch.randn(2 * n if glu else n, k, generator=g) * 0.05).to(dtype).to(dev)
+    nw = (1 + 0.1 * torch.randn(k, generator=g)).to(dtype).to(dev)
+    x = (torch.randn(1, 1, k, generator=g) * 3).to(dtype).to(dev)
+    r = (torch.randn(1, 1, k, generator=g) * 2).to(dtype).to(dev) if with_res else None
+    total, y = linear_vec_norm(x, r, nw, 1e-5, w, glu=glu)
+    if with_res:
+        want_total, xn = add_rms_norm(x, r, nw, 1e-5)
+        assert torch.equal(total, want_total)
+    else:
+        xn = rms_norm(x, nw, 1e-5)
+        assert total is x
+    assert torch.equal(y, linear_vec(xn, w, glu=glu))

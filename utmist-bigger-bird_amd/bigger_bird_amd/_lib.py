@@ -61,6 +61,7 @@ SIGNATURES = {
     "bb_add_rms_norm": (_i32, [_vp, _i64, _vp, _i64, _i32, _i32, _vp, _f32, _i32, _vp, _i64, _vp, _i64, _vp]),
     "bb_silu_mul": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp]),
     "bb_gemv": (_i32, [_vp, _i64, _i32, _i32, _vp, _i32, _i32, _vp, _vp]),
+    "bb_gemv_norm": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp, _vp, _f32, _i32, _i32, _vp, _vp, _vp]),
     "bb_stream_read": (_i32, [_vp, _sz, _vp, _i32, _vp]),
     "bb_int8_quantize_pair": (_i32, [_vp, _vp, _i32, _i64, _i64, _i32, _i64, _i32, _f32, _vp, _vp, _vp, _vp, _i32, _vp]),
 }

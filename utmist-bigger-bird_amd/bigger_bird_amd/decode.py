@@ -312,3 +312,31 @@ def linear_vec(x, weight, glu=False):
     _lib.check(_lib.lib().bb_gemv(_lib.ptr(weight), weight.stride(0), n, k, _lib.ptr(x1), int(glu),
                                   int(x.dtype == torch.float16), _lib.ptr(y), _lib.stream_of(x)))
     return y
+
+
+def linear_vec_norm(x, res, norm_weight, eps, weight, glu=False):
+    """`linear_vec` on the RMSNorm of one hidden row, in one launch: returns (x + res, linear_vec(rms_norm(x + res)))
+    (res None: (x, linear_vec(rms_norm(x)))), bit-identical to add_rms_norm / rms_norm followed by linear_vec."""
+    m, k = weight.shape
+    if not gemv_ok(weight, x) or not x.is_cuda or k > 8192 or norm_weight.dtype != x.dtype:
+        raise ValueError("linear_vec_norm needs a 16-bit GPU weight [N, K] (K % 8 == 0, K <= 8192, aligned rows), "
+                         "an input and a norm weight of its dtype")
+    if x.numel() != k or norm_weight.numel() != k or (res is not None and (res.numel() != k or res.dtype != x.dtype)):
+        raise ValueError("linear_vec_norm takes one token: x, res and the norm weight must hold K values")
+    if glu and m % 2:
+        raise ValueError("linear_vec_norm(glu=True) needs a [2N, K] gate / up weight")
+    n = m // 2 if glu else m
+
+    def flat(t):
+        t1 = t.reshape(-1)
+        return t1 if t1.data_ptr() % 16 == 0 else t1.clone()
+
+    x1, w1 = flat(x), flat(norm_weight)
+    r1 = flat(res) if res is not None else None
+    total = torch.empty_like(x) if res is not None else x
+    y = torch.empty(x.shape[:-1] + (n,), dtype=x.dtype, device=x.device)
+    _lib.check(_lib.lib().bb_gemv_norm(_lib.ptr(weight), weight.stride(0), n, k, _lib.ptr(x1),
+                                       _lib.ptr(r1) if r1 is not None else None, _lib.ptr(w1), float(eps), int(glu),
+                                       int(x.dtype == torch.float16), _lib.ptr(total) if r1 is not None else None,
+                                       _lib.ptr(y), _lib.stream_of(x)))
+    return total, y

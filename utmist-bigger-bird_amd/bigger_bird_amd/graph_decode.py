@@ -19,7 +19,8 @@ generate / EOS / rewind / feed protocol. The design is this package's own:
   applies SiLU(gate) * up, then down), residual + the next RMSNorm (one launch); final norm, lm_head, greedy token
   by a one-workgroup HIP argmax written straight into the control block. The projections run as bb_gemv (one token:
   a matrix-vector product streaming the weight once, faster at batch 1 than the vendor GEMM) where the weight is a
-  16-bit bias-free Linear with K <= 16384; 9 launches per layer on a Llama layer.
+  16-bit bias-free Linear with K <= 16384, and each residual add and RMSNorm rides in the launch of the projection
+  that follows it (bb_gemv_norm): 7 launches per Llama layer (q/k/v, RoPE, decode, merge, o, gate / up, down).
 * Attention per layer: one bb_decode_step. Dense layers run split-K flash decoding over the filled rows (front 0,
   window = capacity, no routes, length read on the GPU); `sparse_decode={"front", "window", "routed"}` switches the
   non-dense RDAttention layers to fused decode routing (pooled per KV head) + sparse decode. The first kernel that
@@ -41,7 +42,8 @@ from transformers.cache_utils import DynamicLayer
 from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
 
 from .attention import rope_inplace
-from .decode import add_rms_norm, argmax_index, decode_step, gemv_ok, linear_vec, rms_norm, silu_mul
+from .decode import (add_rms_norm, argmax_index, decode_step, gemv_ok, linear_vec, linear_vec_norm, rms_norm,
+                     silu_mul)
 
 # Control block: slot indices and the per-step / per-token increments.
 N, POS, TOK, MADE, SLOT = range(5)
@@ -255,20 +257,36 @@ class StaticDecoder:
         o = o.reshape(1, 1, -1)
         return linear_vec(o, plan.base.o_proj.weight) if plan.o_vec else plan.base.o_proj(o)
 
-    def _qkv(self, plan, x):
-        """Projections of the normed input x [1, 1, hidden]: q [1, H, 1, d], k and v [1, Hkv, 1, d], and, with the
+    def _norm_qkv(self, plan, module, hid, res):
+        """The layer's input: hid + res (res None: hid), its norm and the q/k/v projections, as one bb_gemv_norm
+        launch where the modules allow. Returns the new hid and q [1, H, 1, d], k and v [1, Hkv, 1, d], and, with the
         fused projection, the [2, Hkv, 1, d] view of its K and V part (so RoPE on k in place also lands there) and the
         [1, H + Hkv, 1, d] view of q and k together (one RoPE launch for both)."""
         h, hk, d = self.h, self.hk, self.d
-        if plan.qkv_w is not None:
-            y = (linear_vec(x, plan.qkv_w) if plan.qkv_vec else torch.nn.functional.linear(x, plan.qkv_w))[0, 0]
-            q, k, v = y.split((h * d, hk * d, hk * d))
-            kv = y[h * d:].view(2, hk, 1, d)
-            qk = y[:(h + hk) * d].view(1, h + hk, 1, d)
+        f = self._fast_norm(module, hid)
+        if plan.qkv_vec and f and hid.shape[-1] <= 8192 and (res is None or res.dtype == hid.dtype):
+            hid, y = linear_vec_norm(hid, res, *f, plan.qkv_w)
+            y = y[0, 0]
         else:
-            q, k, v = (p(x)[0, 0] for p in (plan.base.q_proj, plan.base.k_proj, plan.base.v_proj))
-            kv = qk = None
-        return q.view(1, h, 1, d), k.view(1, hk, 1, d), v.view(1, hk, 1, d), kv, qk
+            hid, x = self._add_norm(module, hid, res)
+            if plan.qkv_w is None:
+                q, k, v = (p(x)[0, 0] for p in (plan.base.q_proj, plan.base.k_proj, plan.base.v_proj))
+                return hid, q.view(1, h, 1, d), k.view(1, hk, 1, d), v.view(1, hk, 1, d), None, None
+            y = (linear_vec(x, plan.qkv_w) if plan.qkv_vec else torch.nn.functional.linear(x, plan.qkv_w))[0, 0]
+        q, k, v = y.split((h * d, hk * d, hk * d))
+        kv = y[h * d:].view(2, hk, 1, d)
+        qk = y[:(h + hk) * d].view(1, h + hk, 1, d)
+        return hid, q.view(1, h, 1, d), k.view(1, hk, 1, d), v.view(1, hk, 1, d), kv, qk
+
+    def _norm_mlp(self, plan, module, hid, res):
+        """hid + res, its norm and the MLP: returns the new hid and the MLP's output. With the HIP GEMVs the norm
+        rides in the gate / up launch (bb_gemv_norm with the SiLU gate), then the down GEMV: two launches."""
+        f = self._fast_norm(module, hid)
+        if plan.mlp_vec and f and hid.shape[-1] <= 8192 and res.dtype == hid.dtype and res.numel() == hid.numel():
+            hid, g = linear_vec_norm(hid, res, *f, plan.gate_up_w, glu=True)
+            return hid, linear_vec(g, plan.layer.mlp.down_proj.weight)
+        hid, x = self._add_norm(module, hid, res)
+        return hid, self._mlp(plan, x)
 
     def _attend(self, i, plan, q, kn, vn):
         """q [H, d] of the new token, its K / V rows kn / vn [Hkv, d] -> [H, d]. The rows become arena row
@@ -288,8 +306,7 @@ class StaticDecoder:
         pending = None  # the last MLP's output, added to hid together with the next norm
         for i, plan in enumerate(self.plans):
             layer = plan.layer
-            hid, x = self._add_norm(layer.input_layernorm, hid, pending)
-            q, k, v, kv, qk = self._qkv(plan, x)
+            hid, q, k, v, kv, qk = self._norm_qkv(plan, layer.input_layernorm, hid, pending)
             if q.dtype == torch.bfloat16 and cos.dtype == torch.bfloat16:
                 if qk is not None:
                     rope_inplace(qk, cos, sin)
@@ -302,8 +319,7 @@ class StaticDecoder:
             if kv is None:
                 kv = torch.stack((k[0], v[0]))
             o = self._attend(i, plan, q[0, :, 0], kv[0, :, 0], kv[1, :, 0])
-            hid, x = self._add_norm(layer.post_attention_layernorm, hid, self._o_proj(plan, o))
-            pending = self._mlp(plan, x)
+            hid, pending = self._norm_mlp(plan, layer.post_attention_layernorm, hid, self._o_proj(plan, o))
         hid, x = self._add_norm(self.core.norm, hid, pending)
         self.logits = self.model.lm_head(x)[0, -1]
         argmax_index(self.logits, out=self._token_flat)

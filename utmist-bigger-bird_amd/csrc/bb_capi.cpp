@@ -809,10 +809,27 @@ int bb_gemv(const void* w, int64_t sw, int N, int K, const void* x, int glu, int
   if (N < 0 || K <= 0 || K % 8 || K > 16384) return fail("gemv: K = %d must be a positive multiple of 8, at most 16384", K);
   if (!aligned(w, 16) || !aligned(x, 16) || sw % 8 || sw < K || !aligned(y, 2))
     return fail("gemv: W rows and x must be 16-byte aligned");
-  return hip_status(bb::launch_gemv(static_cast<const uint16_t*>(w), sw, N, K, static_cast<const uint16_t*>(x),
+  return hip_status(bb::launch_gemv(static_cast<const uint16_t*>(w), sw, N, K, static_cast<const uint16_t*>(x), nullptr,
                                     glu != 0, is_f16 ? 1 : 0, static_cast<uint16_t*>(y),
                                     static_cast<hipStream_t>(stream)),
                     "bb_gemv");
+}
+
+int bb_gemv_norm(const void* w, int64_t sw, int N, int K, const void* x, const void* res, const void* norm_w,
+                 float eps, int glu, int is_f16, void* sum, void* y, void* stream) {
+  g_err[0] = 0;
+  if (!w || !x || !norm_w || !y || (res != nullptr) != (sum != nullptr)) return fail("gemv_norm: null argument");
+  if (N < 0 || K <= 0 || K % 8 || K > 8192)
+    return fail("gemv_norm: K = %d must be a positive multiple of 8, at most 8192", K);
+  if (!aligned(w, 16) || !aligned(x, 16) || !aligned(norm_w, 16) || (res && (!aligned(res, 16) || !aligned(sum, 16))) ||
+      sw % 8 || sw < K || !aligned(y, 2))
+    return fail("gemv_norm: W rows, x, res, sum and the norm weight must be 16-byte aligned");
+  const bb::GemvNorm nm{static_cast<const uint16_t*>(res), static_cast<const uint16_t*>(norm_w), eps,
+                        static_cast<uint16_t*>(sum)};
+  return hip_status(bb::launch_gemv(static_cast<const uint16_t*>(w), sw, N, K, static_cast<const uint16_t*>(x), &nm,
+                                    glu != 0, is_f16 ? 1 : 0, static_cast<uint16_t*>(y),
+                                    static_cast<hipStream_t>(stream)),
+                    "bb_gemv_norm");
 }
 
 int bb_silu_mul(const void* g, const void* u, int64_t n, int is_f16, void* out, void* stream) {

@@ -561,16 +561,15 @@ __global__ __launch_bounds__(kAmThreads) void argmax_kernel(const T* __restrict_
 // row, 8 values per 16-byte load (D % 8 == 0, D <= 8192). RES: x is first replaced by round(x + res) (the residual
 // add of a decoder layer, as a 16-bit tensor add computes it), which is also written to sum.
 constexpr int kRnThreads = 256;
-template <bool F16, bool RES>
-__global__ __launch_bounds__(kRnThreads) void rms_norm_kernel(const uint16_t* __restrict__ x, int64_t sx,
-                                                              const uint16_t* __restrict__ res, int64_t sr,
-                                                              const uint16_t* __restrict__ w, int D, float eps,
-                                                              uint16_t* __restrict__ out, int64_t so,
-                                                              uint16_t* __restrict__ sum, int64_t ssum) {
-  __shared__ float red[kRnThreads / 64];
-  const int row = blockIdx.x, tid = threadIdx.x;
-  const uint16_t* xr = x + (int64_t)row * sx;
-  constexpr int kMaxUnits = 8192 / 8 / kRnThreads;  // 16-byte units per thread at D = 8192
+constexpr int kRnMaxD = 8192;
+// One row's arithmetic, shared by rms_norm_kernel and gemv_kernel's norm prologue: a 256-thread workgroup, thread t
+// holding the 16-byte units t, t + 256, ... of the row. sumr (may be null) receives round(x + res); emit(c, v) takes
+// the 8 normalised values at element c.
+template <bool F16, bool RES, typename Emit>
+BB_DEV void norm_row(const uint16_t* __restrict__ xr, const uint16_t* __restrict__ rr, const uint16_t* __restrict__ w,
+                     int D, float eps, float* red, uint16_t* __restrict__ sumr, Emit emit) {
+  const int tid = threadIdx.x;
+  constexpr int kMaxUnits = kRnMaxD / 8 / kRnThreads;  // 16-byte units per thread at D = 8192
   u32x4_t xv[kMaxUnits];
   float ss = 0.0f;
 #pragma unroll
@@ -578,7 +577,7 @@ __global__ __launch_bounds__(kRnThreads) void rms_norm_kernel(const uint16_t* __
     const int c = (u * kRnThreads + tid) * 8;
     xv[u] = c < D ? ld16(xr + c) : u32x4_t{0, 0, 0, 0};
     if (RES && c < D) {
-      const u32x4_t rv = ld16(res + (int64_t)row * sr + c);
+      const u32x4_t rv = ld16(rr + c);
 #pragma unroll
       for (int e2 = 0; e2 < 4; ++e2) {
         uint32_t pair = 0;
@@ -590,7 +589,7 @@ __global__ __launch_bounds__(kRnThreads) void rms_norm_kernel(const uint16_t* __
         }
         xv[u][e2] = pair;
       }
-      st16(sum + (int64_t)row * ssum + c, xv[u]);
+      if (sumr) st16(sumr + c, xv[u]);
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -622,8 +621,21 @@ __global__ __launch_bounds__(kRnThreads) void rms_norm_kernel(const uint16_t* __
       }
       o[e2] = pair;
     }
-    st16(out + (int64_t)row * so + c, o);
+    emit(c, o);
   }
+}
+
+template <bool F16, bool RES>
+__global__ __launch_bounds__(kRnThreads) void rms_norm_kernel(const uint16_t* __restrict__ x, int64_t sx,
+                                                              const uint16_t* __restrict__ res, int64_t sr,
+                                                              const uint16_t* __restrict__ w, int D, float eps,
+                                                              uint16_t* __restrict__ out, int64_t so,
+                                                              uint16_t* __restrict__ sum, int64_t ssum) {
+  __shared__ float red[kRnThreads / 64];
+  const int64_t row = blockIdx.x;
+  uint16_t* orow = out + row * so;
+  norm_row<F16, RES>(x + row * sx, RES ? res + row * sr : nullptr, w, D, eps, red, RES ? sum + row * ssum : nullptr,
+                     [&](int c, u32x4_t v) { st16(orow + c, v); });
 }
 
 // out = round(round(silu(g)) u) elementwise over n values (n % 8 == 0, 16-byte aligned): the arithmetic of
@@ -662,88 +674,114 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
 // 16-byte chunks l, l + 64, ... of its part of the rows (512 values per step), with A steps of its R rows' loads in
 // flight, and x is staged once per workgroup in LDS (after the first steps' W loads are issued, so the staging hides
 // under their latency). Each lane sums its share of a row with v_dot2c_f32_{bf16,f16}, the wave sums the lanes, and
-// the KS waves' sums are added in LDS in wave order. GLU: W holds 2N rows, gate rows [0, N) above up rows [N, 2N) (a Llama MLP's fused
+// the KS waves' sums are added in LDS in wave order. NORM: x is the RMSNorm of a hidden row (RES: of hid + res, the
+// sum also written to `sum` by workgroup 0), computed by every workgroup with rms_norm_kernel's arithmetic (so the
+// product is bit-identical to bb_add_rms_norm / bb_rms_norm followed by the plain GEMV). GLU: W holds 2N rows, gate rows [0, N) above up rows [N, 2N) (a Llama MLP's fused
 // gate / up projection); a wave takes R / 2 outputs i with both their rows i and N + i, and writes
 // round(round(silu(g)) u) of the rounded g and u (silu_mul_kernel's arithmetic): the MLP's activation input.
 constexpr int kGvWaves = 4;
 constexpr int kGvMaxK = 16384;  // x staged in 32 KB of LDS
-template <bool F16, bool GLU, int R, int A, int KS>
+template <bool F16, bool GLU, bool NORM, bool RES, int R, int A, int KS>
 __global__ __launch_bounds__(64 * kGvWaves) void gemv_kernel(const uint16_t* __restrict__ w, int64_t sw, int N, int K,
-                                                              const uint16_t* __restrict__ x,
-                                                              uint16_t* __restrict__ y) {
+                                                              const uint16_t* __restrict__ x, GemvNorm nm,
+                                                              uint16_t* __restrict__ y, int rounds) {
   static_assert(!GLU || R % 2 == 0, "GLU rows come in (gate, up) pairs");
   static_assert(kGvWaves % KS == 0, "K parts split the workgroup's waves evenly");
-  constexpr int OUTS = GLU ? R / 2 : R;  // outputs per group of KS waves
+  static_assert(!NORM || 64 * kGvWaves == kRnThreads, "the norm prologue runs on rms_norm_kernel's thread layout");
+  constexpr int OUTS = GLU ? R / 2 : R;   // outputs per group of KS waves and round
+  constexpr int GROUPS = kGvWaves / KS;   // wave groups per workgroup
+  __shared__ float red[kGvWaves];
   __shared__ __attribute__((aligned(16))) uint16_t xs[kGvMaxK];
-  __shared__ float part[KS > 1 ? kGvWaves : 1][R];
+  __shared__ float part[2][KS > 1 ? kGvWaves : 1][R];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int grp = wave / KS, kp = wave % KS;
-  const int out0 = (blockIdx.x * (kGvWaves / KS) + grp) * OUTS;
-  const int kc = K / 8, nsteps = (kc + 63) / 64;  // 16-byte chunks per row, 512-value steps
-  const int sbeg = nsteps * kp / KS, steps = nsteps * (kp + 1) / KS - sbeg;  // this wave's steps
-  const uint16_t* wr[R];
+  const int gid = blockIdx.x * GROUPS + grp, ngroups = gridDim.x * GROUPS;  // wave group, all wave groups
+  const int kc = K / 8;                                     // 16-byte chunks per row
+  const int steps = ((kc + 63) / 64 + KS - 1) / KS;         // 512-value steps per K part (every wave the same)
+  const int sbeg = kp * steps;
+  const int total = rounds * steps;                         // this wave's (round, step) sequence
+  // row r of round k: output group gid + k ngroups (rows past the end read the last row; their outputs are not
+  // stored)
+  auto row = [&](int k, int r) -> const uint16_t* {
+    const int o = (gid + k * ngroups) * OUTS + (GLU ? r / 2 : r);
+    const int oc = o < N ? o : N - 1;
+    return w + (int64_t)(GLU ? oc + (r & 1) * N : oc) * sw;
+  };
+  int lk = 0, lst = 0;  // next (round, step) to load
+  auto load = [&](u32x4_t (&dst)[R]) {
+    const int c = (sbeg + lst) * 64 + lane;
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int o = out0 + (GLU ? r / 2 : r);
-    const int oc = o < N ? o : N - 1;  // rows past the end read the last row; their outputs are not stored
-    wr[r] = w + (int64_t)(GLU ? oc + (r & 1) * N : oc) * sw;
-  }
-  auto load = [&](int st, u32x4_t (&dst)[R]) {
-    const int c = (sbeg + st) * 64 + lane;
-#pragma unroll
-    for (int r = 0; r < R; ++r) dst[r] = c < kc ? ld16(wr[r] + 8 * c) : u32x4_t{0, 0, 0, 0};
+    for (int r = 0; r < R; ++r) dst[r] = c < kc ? ld16(row(lk, r) + 8 * c) : u32x4_t{0, 0, 0, 0};
+    if (++lst == steps) {
+      lst = 0;
+      ++lk;
+    }
   };
   u32x4_t buf[A][R];
 #pragma unroll
   for (int a = 0; a < A; ++a)
-    if (a < steps) load(a, buf[a]);
-  for (int c = tid; c < nsteps * 64; c += 64 * kGvWaves)
-    *reinterpret_cast<u32x4_t*>(&xs[8 * c]) = c < kc ? ld16(x + 8 * c) : u32x4_t{0, 0, 0, 0};
+    if (a < total) load(buf[a]);
+  const int xchunks = KS * steps * 64;  // chunks of x the waves read (zero past K)
+  if constexpr (NORM) {
+    norm_row<F16, RES>(x, nm.res, nm.w, K, nm.eps, red, RES && blockIdx.x == 0 ? nm.sum : nullptr,
+                       [&](int c, u32x4_t v) { *reinterpret_cast<u32x4_t*>(&xs[c]) = v; });
+    for (int c = kc + tid; c < xchunks; c += 64 * kGvWaves)
+      *reinterpret_cast<u32x4_t*>(&xs[8 * c]) = u32x4_t{0, 0, 0, 0};
+  } else {
+    for (int c = tid; c < xchunks; c += 64 * kGvWaves)
+      *reinterpret_cast<u32x4_t*>(&xs[8 * c]) = c < kc ? ld16(x + 8 * c) : u32x4_t{0, 0, 0, 0};
+  }
   __syncthreads();
   float acc[R] = {};
-  for (int s0 = 0; s0 < steps; s0 += A) {
+  int ck = 0, cst = 0;  // (round, step) being summed
+  for (int t0 = 0; t0 < total; t0 += A) {
 #pragma unroll
     for (int a = 0; a < A; ++a) {
-      const int st = s0 + a;
-      if (st < steps) {
-        const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(&xs[8 * ((sbeg + st) * 64 + lane)]);
+      if (t0 + a < total) {
+        const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(&xs[8 * ((sbeg + cst) * 64 + lane)]);
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
           for (int e = 0; e < 4; ++e) acc[r] = dot2<F16>(buf[a][r][e], xv[e], acc[r]);
-        if (st + A < steps) load(st + A, buf[a]);
+        if (t0 + a + A < total) load(buf[a]);
+        if (++cst == steps) {  // round ck done: sum the lanes, then the K parts, and store its outputs
+#pragma unroll
+          for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+          if constexpr (KS > 1) {
+            if (lane == 0) {
+#pragma unroll
+              for (int r = 0; r < R; ++r) part[ck & 1][wave][r] = acc[r];
+            }
+            __syncthreads();
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+              float s2 = part[ck & 1][grp * KS][r];
+#pragma unroll
+              for (int j = 1; j < KS; ++j) s2 += part[ck & 1][grp * KS + j][r];
+              acc[r] = s2;
+            }
+          }
+          const int out0 = (gid + ck * ngroups) * OUTS;
+          if (kp == 0 && lane < OUTS && out0 + lane < N) {
+            float v = acc[0];  // acc[lane] with a static index
+#pragma unroll
+            for (int r = 1; r < OUTS; ++r) v = lane == r ? acc[GLU ? 2 * r : r] : v;
+            if constexpr (GLU) {
+              float u = acc[1];
+#pragma unroll
+              for (int r = 1; r < OUTS; ++r) u = lane == r ? acc[2 * r + 1] : u;
+              const uint32_t gp = f32_to_elem<F16>(v), up = f32_to_elem<F16>(u);
+              y[out0 + lane] = (uint16_t)silu_mul8<F16>(u32x4_t{gp, 0, 0, 0}, u32x4_t{up, 0, 0, 0})[0];
+            } else {
+              y[out0 + lane] = f32_to_elem<F16>(v);
+            }
+          }
+#pragma unroll
+          for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+          cst = 0;
+          ++ck;
+        }
       }
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
-  if constexpr (KS > 1) {
-    if (lane == 0) {
-#pragma unroll
-      for (int r = 0; r < R; ++r) part[wave][r] = acc[r];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      float t = part[grp * KS][r];
-#pragma unroll
-      for (int j = 1; j < KS; ++j) t += part[grp * KS + j][r];
-      acc[r] = t;
-    }
-    if (kp != 0) return;
-  }
-  if (lane < OUTS && out0 + lane < N) {
-    float v = acc[0];  // acc[lane] with a static index
-#pragma unroll
-    for (int r = 1; r < OUTS; ++r) v = lane == r ? acc[GLU ? 2 * r : r] : v;
-    if constexpr (GLU) {
-      float u = acc[1];
-#pragma unroll
-      for (int r = 1; r < OUTS; ++r) u = lane == r ? acc[2 * r + 1] : u;
-      const uint32_t gp = f32_to_elem<F16>(v), up = f32_to_elem<F16>(u);
-      y[out0 + lane] = (uint16_t)silu_mul8<F16>(u32x4_t{gp, 0, 0, 0}, u32x4_t{up, 0, 0, 0})[0];
-    } else {
-      y[out0 + lane] = f32_to_elem<F16>(v);
     }
   }
 }
@@ -855,29 +893,45 @@ hipError_t launch_rms_norm(const uint16_t* x, int64_t sx, const uint16_t* res, i
   return hipGetLastError();
 }
 
-template <bool F16, bool GLU, int R, int A, int KS>
-hipError_t launch_gemv_t(const uint16_t* w, int64_t sw, int N, int K, const uint16_t* x, uint16_t* y,
-                         hipStream_t stream) {
-  constexpr int outs = (GLU ? R / 2 : R) * (kGvWaves / KS);  // outputs per workgroup
-  hipLaunchKernelGGL((gemv_kernel<F16, GLU, R, A, KS>), dim3((unsigned)((N + outs - 1) / outs)), dim3(64 * kGvWaves),
-                     0, stream, w, sw, N, K, x, y);
-  return hipGetLastError();
-}
-
 // Rows per group R = 2, A = 8 steps in flight, K in KS = 2 parts: the fastest of the (R, A, KS) shapes measured for
 // Llama-3-8B's decode projections (q/k/v 6144 x 4096, o 4096 x 4096, gate / up 28672 x 4096, down 4096 x 14336:
 // 12.2, 10.7, 40.3 and 23.3 us, against 12.0-14.1, 10.8-11.7, 42.3-50.4 and 24.0-31.0 us for (4, 4, 1), (2, 8, 1),
 // (4, 2, 4), (4, 4, 4), (2, 4, 4) and (4, 4, 2)).
 constexpr int kGvR = 2, kGvA = 8, kGvKS = 2;
+constexpr int kGvMaxGroups = 1024;
 
-hipError_t launch_gemv(const uint16_t* w, int64_t sw, int N, int K, const uint16_t* x, bool glu, int f16, uint16_t* y,
-                       hipStream_t stream) {
+template <bool F16, bool GLU, bool NORM, bool RES>
+hipError_t launch_gemv_t(const uint16_t* w, int64_t sw, int N, int K, const uint16_t* x, const GemvNorm& nm,
+                         uint16_t* y, hipStream_t stream) {
+  // workgroups: at most kGvMaxGroups; each wave group takes `rounds` output groups, spread so that the last round
+  // is as full as the others
+  constexpr int outs = kGvWaves / kGvKS * (GLU ? kGvR / 2 : kGvR);  // outputs per workgroup and round
+  const int64_t wg_needed = (N + outs - 1) / outs;
+  int cap = kGvMaxGroups;
+  if (const char* e = getenv("BB_GEMV_CAP")) cap = atoi(e);
+  const int rounds = (int)((wg_needed + cap - 1) / cap);
+  const unsigned grid = (unsigned)((wg_needed + rounds - 1) / rounds);
+  hipLaunchKernelGGL((gemv_kernel<F16, GLU, NORM, RES, kGvR, kGvA, kGvKS>), dim3(grid), dim3(64 * kGvWaves), 0,
+                     stream, w, sw, N, K, x, nm, y, rounds);
+  return hipGetLastError();
+}
+
+template <bool F16, bool GLU>
+hipError_t launch_gemv_g(const uint16_t* w, int64_t sw, int N, int K, const uint16_t* x, const GemvNorm* nm,
+                         uint16_t* y, hipStream_t stream) {
+  if (!nm) return launch_gemv_t<F16, GLU, false, false>(w, sw, N, K, x, GemvNorm{}, y, stream);
+  if (nm->res) return launch_gemv_t<F16, GLU, true, true>(w, sw, N, K, x, *nm, y, stream);
+  return launch_gemv_t<F16, GLU, true, false>(w, sw, N, K, x, *nm, y, stream);
+}
+
+hipError_t launch_gemv(const uint16_t* w, int64_t sw, int N, int K, const uint16_t* x, const GemvNorm* nm, bool glu,
+                       int f16, uint16_t* y, hipStream_t stream) {
   if (N <= 0) return hipSuccess;
-  if (K <= 0 || K % 8 || K > kGvMaxK) return hipErrorInvalidValue;
-  if (f16) return glu ? launch_gemv_t<true, true, kGvR, kGvA, kGvKS>(w, sw, N, K, x, y, stream)
-                      : launch_gemv_t<true, false, kGvR, kGvA, kGvKS>(w, sw, N, K, x, y, stream);
-  return glu ? launch_gemv_t<false, true, kGvR, kGvA, kGvKS>(w, sw, N, K, x, y, stream)
-             : launch_gemv_t<false, false, kGvR, kGvA, kGvKS>(w, sw, N, K, x, y, stream);
+  if (K <= 0 || K % 8 || K > kGvMaxK || (nm && K > kRnMaxD)) return hipErrorInvalidValue;
+  if (f16) return glu ? launch_gemv_g<true, true>(w, sw, N, K, x, nm, y, stream)
+                      : launch_gemv_g<true, false>(w, sw, N, K, x, nm, y, stream);
+  return glu ? launch_gemv_g<false, true>(w, sw, N, K, x, nm, y, stream)
+             : launch_gemv_g<false, false>(w, sw, N, K, x, nm, y, stream);
 }
 
 hipError_t launch_silu_mul(const uint16_t* g, const uint16_t* u, int64_t n, int f16, uint16_t* out,

@@ -175,10 +175,17 @@ hipError_t launch_gather_rows(const uint16_t* src, int64_t ss0, int64_t ss1, int
 hipError_t launch_rms_norm(const uint16_t* x, int64_t sx, const uint16_t* res, int64_t sr, int rows, int D,
                            const uint16_t* w, float eps, int f16, uint16_t* out, int64_t so, uint16_t* sum,
                            int64_t ssum, hipStream_t stream);
+// The RMSNorm that a GEMV applies to its input row first (x + res when res is set; the sum goes to `sum`).
+struct GemvNorm {
+  const uint16_t* res;  // residual added before the norm, or null
+  const uint16_t* w;    // the norm's weight [K]
+  float eps;
+  uint16_t* sum;        // x + res [K] (with res; must not overlap x or res)
+};
 // y[N] = W[N, K] x[K] for one token (16-bit, row stride sw; K % 8 == 0, K <= 16384; 16-byte aligned rows and x);
-// silu: x is [2K] and the product takes round(round(silu(x[:K])) x[K:]).
-hipError_t launch_gemv(const uint16_t* w, int64_t sw, int N, int K, const uint16_t* x, bool silu, int f16,
-                       uint16_t* y, hipStream_t stream);
+// nm: x replaced by its RMSNorm (K <= 8192); glu: W has 2N rows (gate over up) and y = round(round(silu(g)) u).
+hipError_t launch_gemv(const uint16_t* w, int64_t sw, int N, int K, const uint16_t* x, const GemvNorm* nm, bool glu,
+                       int f16, uint16_t* y, hipStream_t stream);
 // out = round(round(silu(g)) u) over n values (n % 8 == 0, 16-byte aligned).
 hipError_t launch_silu_mul(const uint16_t* g, const uint16_t* u, int64_t n, int f16, uint16_t* out,
                            hipStream_t stream);
