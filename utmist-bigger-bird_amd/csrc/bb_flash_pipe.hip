@@ -61,9 +61,13 @@ typedef __attribute__((__vector_size__(4 * sizeof(int32_t)))) int32_t i32x4_t;
 // not change when a row moves by 8 (within those sets) or by 32, so a lane's fragment offsets are fixed per d chunk.
 BB_DEV int pk_swz(int r) { return (r & 7) | ((r >> 1) & 8); }
 BB_DEV int pk_off(int r, int c) { return r * PD + 8 * (c ^ pk_swz(r)); }
-// V^T tile: row d (0..127), 8-key unit u of the global V^T layout at element d * 64 + 8 ((u + pv_rot(d)) & 7). A
-// fragment read (16 rows 16 db + x at one unit) touches 16 distinct slots, and the rotation depends on d % 16 only,
-// so the d block is an immediate offset.
+// V^T tile: row d (0..127), 8-key unit u of the global V^T layout at element d * 64 + 8 ((u + pv_rot(d)) & 7). The
+// rotation depends on d % 16 only, so the d block of a fragment is an immediate offset. A ds_read_b128 serves its 64
+// lanes in four 16-lane groups (measured on gfx950: lanes 32 h + 4 q + 0..3 for the quads q whose three index bits
+// have the same parity), each group conflict-free when it hits 16 distinct 16-byte bank slots (address / 16 mod 16).
+// This rotation leaves the fragment reads 2-way conflicting (3.2 extra LDS cycles per read, measured); the
+// conflict-free rotation 2 ((d >> 1) & 3) measured 2.4% slower in the whole kernel (24.76 against 24.17 ms at 128K,
+// 1.866 against 1.829 ms at 32K, interleaved A/B, identical ISA otherwise), so the conflicting one stays.
 BB_DEV int pv_rot(int d) { return (d ^ ((d >> 3) & 1)) & 7; }
 BB_DEV int pv_off(int d, int u) { return d * kTileKeys + 8 * ((u + pv_rot(d)) & 7); }
 
@@ -285,9 +289,9 @@ BB_DEV void ping_pv(PingState& st, const uint16_t* vt, const FragOfs& fo) {
 }
 
 // MFMA phase of the window loop: O^T += V^T(t-1) P(t-1)^T, then S(t) = K(t) Q^T (64 MFMAs), with the 32 LDS fragment
-// reads software-pipelined four fragments ahead through a register ring (the LDS latency would otherwise idle the
-// matrix core between each read and the MFMAs that consume it).
-constexpr int kRing = 4;
+// reads software-pipelined six fragments ahead through a register ring (the LDS latency would otherwise idle the
+// matrix core between each read and the MFMAs that consume it; 4 and 8 ahead measured slower).
+constexpr int kRing = 6;
 
 template <bool F16>
 BB_DEV void ping_mfma_phase(PingState& st, uint32_t kl, uint32_t vt, const FragOfs& fo) {
