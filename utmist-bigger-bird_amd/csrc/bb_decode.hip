@@ -34,12 +34,21 @@ BB_DEV float dot2(uint32_t a, uint32_t b, float c) {
   else return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
-// q row slice of one lane as packed pairs (DPL 16-bit values, DPL / 2 words).
+// The decode kernels read each cached row with the 8 lanes of a key slot. Lane `sub` holds the 16-byte pieces
+// sub, sub + 8, ... of the row (element offset piece_off(sub, e0)), so that each load instruction of the slot covers
+// whole 128-byte spans of the row: the rows are read once per step, with non-temporal loads (global_load ... nt),
+// which stream at about 7.1 TB/s where plain loads reach 6.2-6.3 (16-byte reads over 4 GiB, measured) but which
+// fetch whole lines for every instruction, so a lane layout that left half-lines per instruction read them twice.
+constexpr int kSlotLanes = 8;
+BB_DEV int piece_off(int sub, int e0) { return 8 * (sub + kSlotLanes * e0); }
+BB_DEV u32x4_t ld16_nt(const uint16_t* p) { return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p)); }
+
+// q row of one lane's pieces as packed pairs (DPL 16-bit values, DPL / 2 words).
 template <int DPL>
-BB_DEV void load_q_pairs(const uint16_t* qr, uint32_t (&qw)[DPL / 2]) {
+BB_DEV void load_q_pairs(const uint16_t* qrow, int sub, uint32_t (&qw)[DPL / 2]) {
 #pragma unroll
   for (int e0 = 0; e0 < DPL / 8; ++e0) {
-    const u32x4_t w = ld16(qr + 8 * e0);
+    const u32x4_t w = ld16(qrow + piece_off(sub, e0));
 #pragma unroll
     for (int i = 0; i < 4; ++i) qw[4 * e0 + i] = w[i];
   }
@@ -57,15 +66,15 @@ BB_DEV int64_t appended_row(const RowAppend& a, int64_t n, const int64_t* n_dev,
   return a.knew && v >= 1 && v <= cap ? v - 1 : -1;
 }
 
-// The 16-byte units [DPL sub, DPL (sub + 1)) of the new K row of KV head kv (already loaded into kw) and of its V row
-// to cache row j: each of the 8 lanes of the key slot that read the row writes its own units.
+// The 16-byte pieces of lane `sub` (piece_off) of the new K row of KV head kv (already loaded into kw) and of its V row
+// to cache row j: each of the 8 lanes of the key slot that read the row writes its own pieces.
 template <int DPL>
 BB_DEV void store_appended(const RowAppend& a, int kv, int64_t j, int sub, const u32x4_t (&kw)[DPL / 8]) {
 #pragma unroll
   for (int e0 = 0; e0 < DPL / 8; ++e0) {
-    st16(a.k + (int64_t)kv * a.sk0 + j * a.sk1 + DPL * sub + 8 * e0, kw[e0]);
-    st16(a.v + (int64_t)kv * a.sv0 + j * a.sv1 + DPL * sub + 8 * e0,
-         ld16(a.vnew + (int64_t)kv * a.svn + DPL * sub + 8 * e0));
+    st16(a.k + (int64_t)kv * a.sk0 + j * a.sk1 + piece_off(sub, e0), kw[e0]);
+    st16(a.v + (int64_t)kv * a.sv0 + j * a.sv1 + piece_off(sub, e0),
+         ld16(a.vnew + (int64_t)kv * a.svn + piece_off(sub, e0)));
   }
 }
 
@@ -81,7 +90,7 @@ constexpr float kSdRescale = 8.0f;
 
 template <int D, int GR, bool F16>
 __global__ __launch_bounds__(kSdThreads) void sparse_decode_kernel(SparseDecodeParams p) {
-  constexpr int LPK = 8, DPL = D / LPK, KPW = 64 / LPK, SLOTS = kSdThreads / LPK, NW = kSdThreads / 64;
+  constexpr int LPK = kSlotLanes, DPL = D / LPK, KPW = 64 / LPK, SLOTS = kSdThreads / LPK, NW = kSdThreads / 64;
   __shared__ float part_m[NW][GR];
   __shared__ float part_l[NW][GR];
   __shared__ float part_o[NW][GR][D];
@@ -99,7 +108,7 @@ __global__ __launch_bounds__(kSdThreads) void sparse_decode_kernel(SparseDecodeP
 
   uint32_t qw[GR][DPL / 2];
 #pragma unroll
-  for (int h = 0; h < GR; ++h) load_q_pairs<DPL>(p.q + (int64_t)(r * GR + h) * p.sq + DPL * sub, qw[h]);
+  for (int h = 0; h < GR; ++h) load_q_pairs<DPL>(p.q + (int64_t)(r * GR + h) * p.sq, sub, qw[h]);
   float m[GR], l[GR], acc[GR][DPL];
 #pragma unroll
   for (int h = 0; h < GR; ++h) {
@@ -109,8 +118,8 @@ __global__ __launch_bounds__(kSdThreads) void sparse_decode_kernel(SparseDecodeP
     for (int e = 0; e < DPL; ++e) acc[h][e] = 0.0f;
   }
   const int32_t* irow = p.idx + (int64_t)r * p.si0;
-  const uint16_t* kbase = p.k + (int64_t)kv * p.sk0 + DPL * sub;
-  const uint16_t* vbase = p.v + (int64_t)kv * p.sv0 + DPL * sub;
+  const uint16_t* kbase = p.k + (int64_t)kv * p.sk0;
+  const uint16_t* vbase = p.v + (int64_t)kv * p.sv0;
   for (int64_t j0 = j_begin + slot; j0 < j_end; j0 += 2 * SLOTS) {
     int64_t pos[2];
     bool ok[2];
@@ -128,12 +137,12 @@ __global__ __launch_bounds__(kSdThreads) void sparse_decode_kernel(SparseDecodeP
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const bool fresh = ok[u] && pos[u] == jnew;
-      const uint16_t* ks = fresh ? p.app.knew + (int64_t)kv * p.app.skn + DPL * sub : kbase + pos[u] * p.sk1;
-      const uint16_t* vs = fresh ? p.app.vnew + (int64_t)kv * p.app.svn + DPL * sub : vbase + pos[u] * p.sv1;
+      const uint16_t* ks = fresh ? p.app.knew + (int64_t)kv * p.app.skn : kbase + pos[u] * p.sk1;
+      const uint16_t* vs = fresh ? p.app.vnew + (int64_t)kv * p.app.svn : vbase + pos[u] * p.sv1;
 #pragma unroll
       for (int e0 = 0; e0 < DPL / 8; ++e0) {
-        kw[u][e0] = ld16(ks + 8 * e0);
-        vw[u][e0] = ld16(vs + 8 * e0);
+        kw[u][e0] = ld16_nt(ks + piece_off(sub, e0));
+        vw[u][e0] = ld16_nt(vs + piece_off(sub, e0));
       }
     }
 #pragma unroll
@@ -191,7 +200,7 @@ __global__ __launch_bounds__(kSdThreads) void sparse_decode_kernel(SparseDecodeP
         part_l[wave][h] = l[h];
       }
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) part_o[wave][h][DPL * sub + e] = acc[h][e];
+      for (int e = 0; e < DPL; ++e) part_o[wave][h][piece_off(sub, e >> 3) + (e & 7)] = acc[h][e];
     }
   }
   __syncthreads();
@@ -279,7 +288,7 @@ __global__ __launch_bounds__(kSdMergeThreads) void sparse_merge_kernel(SparseDec
 constexpr int kRsKeysPerSlot = 4;
 template <int D, int G, bool F16>
 __global__ __launch_bounds__(kSdThreads) void route_scores_kernel(DecodeRouteParams p) {
-  constexpr int LPK = 8, DPL = D / LPK, KPW = 64 / LPK, SLOTS = kSdThreads / LPK;
+  constexpr int LPK = kSlotLanes, DPL = D / LPK, KPW = 64 / LPK, SLOTS = kSdThreads / LPK;
   __shared__ float part_m[SLOTS][G];
   __shared__ float part_l[SLOTS][G];
   const int split = blockIdx.x, kv = blockIdx.y;
@@ -296,7 +305,7 @@ __global__ __launch_bounds__(kSdThreads) void route_scores_kernel(DecodeRoutePar
   const int64_t j_end = j_begin + p.split_len < n ? j_begin + p.split_len : n;
   uint32_t qw[G][DPL / 2];
 #pragma unroll
-  for (int h = 0; h < G; ++h) load_q_pairs<DPL>(p.q + (int64_t)(kv * G + h) * p.sq + DPL * sub, qw[h]);
+  for (int h = 0; h < G; ++h) load_q_pairs<DPL>(p.q + (int64_t)(kv * G + h) * p.sq, sub, qw[h]);
   float m[G], l[G];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
@@ -304,15 +313,15 @@ __global__ __launch_bounds__(kSdThreads) void route_scores_kernel(DecodeRoutePar
     l[h] = 0.0f;
   }
   constexpr int U = kRsKeysPerSlot;
-  const uint16_t* kbase = p.k + (int64_t)kv * p.sk0 + DPL * sub;
+  const uint16_t* kbase = p.k + (int64_t)kv * p.sk0;
   for (int64_t j0 = j_begin + slot; j0 < j_end; j0 += U * SLOTS) {
     u32x4_t kw[U][DPL / 8];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t j = j0 + u * SLOTS < j_end ? j0 + u * SLOTS : j0;
-      const uint16_t* ks = j == jnew ? p.app.knew + (int64_t)kv * p.app.skn + DPL * sub : kbase + j * p.sk1;
+      const uint16_t* ks = j == jnew ? p.app.knew + (int64_t)kv * p.app.skn : kbase + j * p.sk1;
 #pragma unroll
-      for (int e0 = 0; e0 < DPL / 8; ++e0) kw[u][e0] = ld16(ks + 8 * e0);
+      for (int e0 = 0; e0 < DPL / 8; ++e0) kw[u][e0] = ld16_nt(ks + piece_off(sub, e0));
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -671,8 +680,9 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
 // One token through a linear layer, y[N] = W[N, K] x[K] (16-bit W rows of stride sw; fp32 accumulation, y rounded
 // to the model dtype): the decode step's projections, HBM-bound on streaming W once. A workgroup is 4 waves; each
 // group of KS waves takes R rows, the KS waves of a group taking consecutive parts of K; lane l of a wave takes the
-// 16-byte chunks l, l + 64, ... of its part of the rows (512 values per step), with A steps of its R rows' loads in
-// flight, and x is staged once per workgroup in LDS (after the first steps' W loads are issued, so the staging hides
+// 16-byte chunks l, l + 64, ... of its part of the rows (512 values per step; 1 KB of a row per load instruction,
+// non-temporal since W is read once per token: 5.6 against 5.2 TB/s over 8 layers' weights), with A steps of its R
+// rows' loads in flight, and x is staged once per workgroup in LDS (after the first steps' W loads are issued, so the staging hides
 // under their latency). Each lane sums its share of a row with v_dot2c_f32_{bf16,f16}, the wave sums the lanes, and
 // the KS waves' sums are added in LDS in wave order. NORM: x is the RMSNorm of a hidden row (RES: of hid + res, the
 // sum also written to `sum` by workgroup 0), computed by every workgroup with rms_norm_kernel's arithmetic (so the
@@ -711,7 +721,7 @@ __global__ __launch_bounds__(64 * kGvWaves) void gemv_kernel(const uint16_t* __r
   auto load = [&](u32x4_t (&dst)[R]) {
     const int c = (sbeg + lst) * 64 + lane;
 #pragma unroll
-    for (int r = 0; r < R; ++r) dst[r] = c < kc ? ld16(row(lk, r) + 8 * c) : u32x4_t{0, 0, 0, 0};
+    for (int r = 0; r < R; ++r) dst[r] = c < kc ? ld16_nt(row(lk, r) + 8 * c) : u32x4_t{0, 0, 0, 0};
     if (++lst == steps) {
       lst = 0;
       ++lk;
