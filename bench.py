@@ -16,7 +16,7 @@ HIP events around its launches on the stream it runs on; `cpu_baseline` = the CP
 PyTorch path (oracle.routes_reference_order + oracle.flash_ref) timed on a bounded sample and scaled to a layer.
 Also reported, next to the headline: `tail_roofline` (the exact 256-row tail, TFLOP/s and HBM GB/s), `decode`
 (INT8-KV decode: microseconds per step and HBM GB/s against 8 TB/s and against
-`hbm_read_ceiling`, the rate of a plain 16-byte streaming read over 4 GiB measured in the same run) and `short_arm`
+`hbm_read_ceiling`, the rate of a non-temporal 16-byte streaming read over 4 GiB measured in the same run) and `short_arm`
 (B=4 at T=32768: sparse prefill, with its stage split, against dense causal SDPA on the same
 inputs).
 """
@@ -100,9 +100,10 @@ def staged_prefill(attn, q, k, v, ev):
     return out.unflatten(0, (bsz, attn.num_heads)), idx if bsz == 1 else idx.view(bsz, attn.num_heads, -1)
 
 
-def hbm_read_ceiling(dev, gib=4, workgroups=16384, reps=10):
-    """HBM read rate of a plain 16-byte streaming read (bb_stream_read) over `gib` GiB, far past the 256 MB Infinity
-    Cache: the ceiling the decode kernels are reported against next to the published 8 TB/s. Best of `reps`."""
+def hbm_read_ceiling(dev, gib=4, workgroups=4096, reps=10):
+    """HBM read rate of a non-temporal 16-byte streaming read (bb_stream_read: one contiguous range per workgroup)
+    over `gib` GiB, far past the 256 MB Infinity Cache: the ceiling the decode kernels are reported against next to
+    the published 8 TB/s. Best of `reps`."""
     import torch
     from bigger_bird_amd import _lib
 
@@ -124,7 +125,8 @@ def hbm_read_ceiling(dev, gib=4, workgroups=16384, reps=10):
         best = min(best, a.elapsed_time(b))
     del buf
     return {"gbps": round(nbytes / (best * 1e-3) / 1e9, 1), "bytes": nbytes, "workgroups": workgroups,
-            "kernel": "stream_read_kernel (bb_stream_read): 16-byte loads, 4 in flight per thread"}
+            "kernel": "stream_read_kernel (bb_stream_read): non-temporal 16-byte loads, 8 in flight per thread, "
+                      "one contiguous range per workgroup"}
 
 
 def main_traffic():

@@ -321,8 +321,8 @@ int bb_rope_inplace(void* x, const int64_t* sx, int B, int Hh, int64_t T, int D,
 
 /*
  * Measurement helper (no reference counterpart): reads `bytes` (a multiple of 16, 16-byte aligned) of device memory
- * with plain 16-byte loads over `workgroups` workgroups of 256 threads and writes one XOR word per workgroup to
- * sink[workgroups]. Over a buffer far larger than the 256 MB Infinity Cache its rate is the HBM read ceiling the
+ * with non-temporal 16-byte loads, one contiguous range per each of `workgroups` workgroups of 256 threads, and
+ * writes one XOR word per workgroup to sink[workgroups]. Over a buffer far larger than the 256 MB Infinity Cache its rate is the HBM read ceiling the
  * decode kernels are reported against, next to the published 8 TB/s.
  */
 int bb_stream_read(const void* buf, size_t bytes, uint32_t* sink, int workgroups, void* stream);
