@@ -344,9 +344,11 @@ __global__ __launch_bounds__(kSdThreads) void route_scores_kernel(DecodeRoutePar
       for (int h = 0; h < G; ++h) {
         const float x = sc[h] * p.c;
         if (sub == h % LPK) p.scores[(int64_t)(kv * G + h) * p.cap + j] = x;
-        const float mn = fmaxf(m[h], x);
-        l[h] = l[h] * fast_exp2(m[h] - mn) + fast_exp2(x - mn);
-        m[h] = mn;
+        // l 2^(m - mn) + 2^(x - mn) with mn = max(m, x), on one exponential: one of the two factors is 2^0 = 1
+        const float dx = x - m[h];
+        const float e = fast_exp2(-fabsf(dx));
+        l[h] = dx <= 0.0f ? l[h] + e : fmaf(l[h], e, 1.0f);
+        m[h] = fmaxf(m[h], x);
       }
     }
   }
