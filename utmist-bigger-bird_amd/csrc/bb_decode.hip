@@ -41,6 +41,56 @@ BB_DEV float dot2(uint32_t a, uint32_t b, float c) {
 // fetch whole lines for every instruction, so a lane layout that left half-lines per instruction read them twice.
 constexpr int kSlotLanes = 8;
 BB_DEV int piece_off(int sub, int e0) { return 8 * (sub + kSlotLanes * e0); }
+// Sum over the kSlotLanes = 8 lanes of a key slot (lane bits 0..2), the same value in every lane of the slot, on DPP
+// lane moves inside the VALU: quad_perm [1, 0, 3, 2], quad_perm [2, 3, 0, 1], then row_half_mirror (lane i of an
+// 8-lane half row reads lane 7 - i, which lies in the other quad and holds that quad's sum). The additions pair the
+// same values as a butterfly over lane xor 1, 2, 4, and each lane adds the pair in either order, so every lane holds
+// the same bits. (__shfl_xor goes through the LDS crossbar, ds_bpermute, with a wait per round.)
+template <int CTRL>
+BB_DEV float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+BB_DEV float slot_sum8(float v) {
+  static_assert(kSlotLanes == 8, "the DPP pattern reduces 8-lane slots");
+  v += dpp_mov<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp_mov<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp_mov<0x141>(v);  // row_half_mirror
+  return v;
+}
+// One round of slot_reduce_scatter over the N heads still held in v[0..N): with N > 1 the lane keeps the upper or
+// the lower half (its lane bit for this round) and adds the partner's partials of that half; with N = 1 it adds the
+// partner's partial of the one head.
+template <int N, int CTRL>
+BB_DEV void rs_round(float (&v)[8], bool upper) {
+  if constexpr (N == 1) {
+    v[0] += dpp_mov<CTRL>(v[0]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+      const float keep = upper ? v[N / 2 + i] : v[i];
+      const float send = upper ? v[i] : v[N / 2 + i];
+      v[i] = keep + dpp_mov<CTRL>(send);
+    }
+  }
+}
+// Reduce-scatter of G per-lane partial sums (G = 1, 2, 4 or 8 heads) over the 8 lanes of a key slot: lane `sub` ends
+// with the slot's total for head sub >> (3 - log2 G), each head held by 8 / G lanes with the same bits. The rounds
+// pair lane sub with 7 - sub (row_half_mirror), sub ^ 2 and sub ^ 1; the first log2 G of them halve the heads a lane
+// holds by lane bit 4, 2 and 1. Every lane's partial of a head enters its total once: the union of sub's quad and
+// 7 - sub's quad is the whole slot.
+template <int G>
+BB_DEV float slot_reduce_scatter(const float (&p)[G], int sub) {
+  static_assert(G == 1 || G == 2 || G == 4 || G == 8, "1, 2, 4 or 8 heads per slot");
+  constexpr int G1 = G > 1 ? G / 2 : 1, G2 = G1 > 1 ? G1 / 2 : 1;
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < G; ++i) v[i] = p[i];
+  rs_round<G, 0x141>(v, (sub & 4) != 0);
+  rs_round<G1, 0x4E>(v, (sub & 2) != 0);
+  rs_round<G2, 0xB1>(v, (sub & 1) != 0);
+  return v[0];
+}
+constexpr int log2_heads(int g) { return g >= 8 ? 3 : g >= 4 ? 2 : g >= 2 ? 1 : 0; }
 BB_DEV u32x4_t ld16_nt(const uint16_t* p) { return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p)); }
 
 // q row of one lane's pieces as packed pairs (DPL 16-bit values, DPL / 2 words).
@@ -158,9 +208,7 @@ __global__ __launch_bounds__(kSdThreads) void sparse_decode_kernel(SparseDecodeP
         s[h] = t;
       }
 #pragma unroll
-      for (int off = 1; off < LPK; off <<= 1)
-#pragma unroll
-        for (int h = 0; h < GR; ++h) s[h] += __shfl_xor(s[h], off);
+      for (int h = 0; h < GR; ++h) s[h] = slot_sum8(s[h]);
 #pragma unroll
       for (int h = 0; h < GR; ++h) {
         const float x = s[h] * p.c;
@@ -282,8 +330,10 @@ __global__ __launch_bounds__(kSdMergeThreads) void sparse_merge_kernel(SparseDec
 
 // ---------------------------------------------------------------------------------------------------------------
 // Decode routing, pass 1 (kernels/bigger_bird_route.py:24-52): workgroup (split, KV head) scores its key range for
-// the G query heads (fp32, log2 units, to S [H, cap]) and keeps each head's running (max, sum) per key slot; the
-// slots combine into one (max, sum) per head and split. Each key slot takes four keys per step (all rows in flight).
+// the G query heads (fp32, log2 units, to S [H, cap]) and keeps each head's running (max, sum) per key slot: the
+// slot's 8 lanes reduce their partial dot products scatter-wise, so that each lane ends with one head's score and
+// keeps that head's state. The slots combine into one (max, sum) per head and split. Each key slot takes four keys
+// per step (all rows in flight).
 // Split 0 also clears the KV head's top-k histogram and counters, which the pool pass fills.
 constexpr int kRsKeysPerSlot = 4;
 template <int D, int G, bool F16>
@@ -306,14 +356,14 @@ __global__ __launch_bounds__(kSdThreads) void route_scores_kernel(DecodeRoutePar
   uint32_t qw[G][DPL / 2];
 #pragma unroll
   for (int h = 0; h < G; ++h) load_q_pairs<DPL>(p.q + (int64_t)(kv * G + h) * p.sq, sub, qw[h]);
-  float m[G], l[G];
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-    m[h] = -1.0e20f;
-    l[h] = 0.0f;
-  }
+  // after the slot reduction lane sub holds head myh's score; the first of the head's 8 / G lanes writes it
+  constexpr int HSH = 3 - log2_heads(G);
+  const int myh = sub >> HSH;
+  const bool writer = (sub & ((1 << HSH) - 1)) == 0;
+  float m = -1.0e20f, l = 0.0f;  // head myh's running (max, sum) over this slot's keys
   constexpr int U = kRsKeysPerSlot;
   const uint16_t* kbase = p.k + (int64_t)kv * p.sk0;
+  float* srow = p.scores + (int64_t)(kv * G + myh) * p.cap;
   for (int64_t j0 = j_begin + slot; j0 < j_end; j0 += U * SLOTS) {
     u32x4_t kw[U][DPL / 8];
 #pragma unroll
@@ -336,28 +386,18 @@ __global__ __launch_bounds__(kSdThreads) void route_scores_kernel(DecodeRoutePar
         for (int w = 0; w < DPL / 2; ++w) t = dot2<F16>(qw[h][w], kw[u][w >> 2][w & 3], t);
         sc[h] = t;
       }
-#pragma unroll
-      for (int off = 1; off < LPK; off <<= 1)
-#pragma unroll
-        for (int h = 0; h < G; ++h) sc[h] += __shfl_xor(sc[h], off);
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        const float x = sc[h] * p.c;
-        if (sub == h % LPK) p.scores[(int64_t)(kv * G + h) * p.cap + j] = x;
-        // l 2^(m - mn) + 2^(x - mn) with mn = max(m, x), on one exponential: one of the two factors is 2^0 = 1
-        const float dx = x - m[h];
-        const float e = fast_exp2(-fabsf(dx));
-        l[h] = dx <= 0.0f ? l[h] + e : fmaf(l[h], e, 1.0f);
-        m[h] = fmaxf(m[h], x);
-      }
+      const float x = slot_reduce_scatter<G>(sc, sub) * p.c;
+      if (writer) srow[j] = x;
+      // l 2^(m - mn) + 2^(x - mn) with mn = max(m, x), on one exponential: one of the two factors is 2^0 = 1
+      const float dx = x - m;
+      const float e = fast_exp2(-fabsf(dx));
+      l = dx <= 0.0f ? l + e : fmaf(l, e, 1.0f);
+      m = fmaxf(m, x);
     }
   }
-  if (sub == 0) {
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      part_m[slot][h] = m[h];
-      part_l[slot][h] = l[h];
-    }
+  if (writer) {
+    part_m[slot][myh] = m;
+    part_l[slot][myh] = l;
   }
   __syncthreads();
   if (tid < G) {
