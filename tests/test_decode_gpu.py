@@ -229,9 +229,11 @@ def test_kv_append_matches_index_copy(dtype, dev):
 def test_decode_step_matches_separate_launches(routed, dtype, d, hk, dev):
     """bb_decode_step (the new row appended by the first kernel that reads the cache, the length advanced by the
     last) against the same step as separate launches: kv_append at length - 1, then routing + sparse decode (or dense
-    decode over the cache), then the length add. Bitwise on the output, the routed indices, the whole cache buffer
-    (strided views) and the length, over consecutive steps up to and past the capacity (a length past it appends
-    nothing and stays)."""
+    decode over the cache), then the length add. Bitwise on the routed indices, the whole cache buffer (strided
+    views) and the length, over consecutive steps up to and past the capacity (a length past it appends nothing and
+    stays). The output is bitwise for the dense step; the routed step's decode takes its scores from the routing
+    pass (the same q.k in another fp32 summation order) instead of recomputing them, so there it may differ from the
+    separate launches by one unit in the last place of the output type."""
     print(f"case decode_step routed={routed} {dtype} d={d} hk={hk}", flush=True)
     from bigger_bird_amd.decode import decode_step
     h, cap = 32, 5000
@@ -262,7 +264,12 @@ def test_decode_step_matches_separate_launches(routed, dtype, d, hk, dev):
         if appended:
             lref.add_(1)
         torch.cuda.synchronize()
-        assert torch.equal(out, out_r), i
+        if routed:
+            ulp = 2.0 ** (-7 if dtype == torch.bfloat16 else -10)
+            err = (out.float() - out_r.float()).abs()
+            assert bool((err <= out_r.float().abs() * ulp + 1e-6).all()), (i, err.max().item())
+        else:
+            assert torch.equal(out, out_r), i
         assert torch.equal(arena, ref), i
         assert int(length.item()) == int(lref.item()), i
     assert int(length.item()) == cap + 1

@@ -707,9 +707,11 @@ int bb_decode_step(const void* q, int64_t sq, void* k, const int64_t* sk, void* 
   const size_t part_bytes = bb_sparse_decode_workspace(H, Hkv, D, Hkv, fr, win, routed, 0);
   float* part = reinterpret_cast<float*>(w);
   w += align256(part_bytes);
+  const float* route_scores = nullptr;
   if (routed > 0) {  // decode routing appends the row (its scores pass is the first to read the cache)
     float* probs = reinterpret_cast<float*>(w);
     w += align256((size_t)Hkv * cap * 4);
+    route_scores = reinterpret_cast<const float*>(w);  // route_impl's first workspace block: scores [H][cap]
     const size_t rws = bb_decode_route_workspace(cap, H, Hkv, 0, routed);
     int rc = route_impl(q, sq, k, sk, cap, n_dev, cap, H, Hkv, D, front, window, scale, 0, is_f16, probs, routed,
                         idx_out, w, rws, &app, st);
@@ -738,6 +740,8 @@ int bb_decode_step(const void* q, int64_t sq, void* k, const int64_t* sk, void* 
   if (routed == 0) p.app = app;  // dense: the decode kernel is the first to read the cache
   p.n_advance = advance > 0 ? n_dev : nullptr;
   p.advance = advance;
+  p.xs = route_scores;  // routed: the decode reuses the routing pass's scores and reads only V rows
+  p.xs_stride = cap;
   return hip_status(bb::launch_sparse_decode(p, st), "bb_decode_step");
 }
 

@@ -134,11 +134,13 @@ BB_DEV void store_appended(const RowAppend& a, int kv, int64_t j, int sub, const
 // for pooled routes [Hkv, R], 1 for per-head routes [H, R]) and reads KV head (r GR) / groups. Virtual key
 // j < front -> position j; j < front + window -> n - window + (j - front); otherwise the routed index; positions
 // outside [0, n) are skipped (kernels/bigger_bird_decode.py:38-47). The key slots of a wave combine through lane
-// shuffles, the four waves through LDS.
+// shuffles, the four waves through LDS. XS (the fused decode step after its routing pass): every key's score is
+// already in the routing workspace (p.xs, [H][xs_stride], log2 units, computed from the same q and K rows), so only
+// the V rows are read.
 constexpr int kSdThreads = 256;
 constexpr float kSdRescale = 8.0f;
 
-template <int D, int GR, bool F16>
+template <int D, int GR, bool F16, bool XS>
 __global__ __launch_bounds__(kSdThreads) void sparse_decode_kernel(SparseDecodeParams p) {
   constexpr int LPK = kSlotLanes, DPL = D / LPK, KPW = 64 / LPK, SLOTS = kSdThreads / LPK, NW = kSdThreads / 64;
   __shared__ float part_m[NW][GR];
@@ -157,8 +159,10 @@ __global__ __launch_bounds__(kSdThreads) void sparse_decode_kernel(SparseDecodeP
   const int64_t j_end = j_begin + p.split_len < total ? j_begin + p.split_len : total;
 
   uint32_t qw[GR][DPL / 2];
+  if constexpr (!XS) {
 #pragma unroll
-  for (int h = 0; h < GR; ++h) load_q_pairs<DPL>(p.q + (int64_t)(r * GR + h) * p.sq, sub, qw[h]);
+    for (int h = 0; h < GR; ++h) load_q_pairs<DPL>(p.q + (int64_t)(r * GR + h) * p.sq, sub, qw[h]);
+  }
   float m[GR], l[GR], acc[GR][DPL];
 #pragma unroll
   for (int h = 0; h < GR; ++h) {
@@ -184,6 +188,7 @@ __global__ __launch_bounds__(kSdThreads) void sparse_decode_kernel(SparseDecodeP
       pos[u] = ok[u] ? ps : 0;
     }
     u32x4_t kw[2][DPL / 8], vw[2][DPL / 8];
+    float xs[2][GR];  // XS: the keys' scores (log2 units) from the routing pass of the same step
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const bool fresh = ok[u] && pos[u] == jnew;
@@ -191,27 +196,35 @@ __global__ __launch_bounds__(kSdThreads) void sparse_decode_kernel(SparseDecodeP
       const uint16_t* vs = fresh ? p.app.vnew + (int64_t)kv * p.app.svn : vbase + pos[u] * p.sv1;
 #pragma unroll
       for (int e0 = 0; e0 < DPL / 8; ++e0) {
-        kw[u][e0] = ld16_nt(ks + piece_off(sub, e0));
+        if constexpr (!XS) kw[u][e0] = ld16_nt(ks + piece_off(sub, e0));
         vw[u][e0] = ld16_nt(vs + piece_off(sub, e0));
+      }
+      if constexpr (XS) {
+#pragma unroll
+        for (int h = 0; h < GR; ++h) xs[u][h] = p.xs[(int64_t)(r * GR + h) * p.xs_stride + pos[u]];
       }
     }
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       if (!ok[u]) continue;
-      if (pos[u] == jnew) store_appended<DPL>(p.app, kv, jnew, sub, kw[u]);
       float s[GR];
+      if constexpr (!XS) {
+        if (pos[u] == jnew) store_appended<DPL>(p.app, kv, jnew, sub, kw[u]);
 #pragma unroll
-      for (int h = 0; h < GR; ++h) {
-        float t = 0.0f;
+        for (int h = 0; h < GR; ++h) {
+          float t = 0.0f;
 #pragma unroll
-        for (int w = 0; w < DPL / 2; ++w) t = dot2<F16>(qw[h][w], kw[u][w >> 2][w & 3], t);
-        s[h] = t;
+          for (int w = 0; w < DPL / 2; ++w) t = dot2<F16>(qw[h][w], kw[u][w >> 2][w & 3], t);
+          s[h] = t;
+        }
+#pragma unroll
+        for (int h = 0; h < GR; ++h) s[h] = slot_sum8(s[h]);
       }
 #pragma unroll
-      for (int h = 0; h < GR; ++h) s[h] = slot_sum8(s[h]);
-#pragma unroll
       for (int h = 0; h < GR; ++h) {
-        const float x = s[h] * p.c;
+        float x;
+        if constexpr (XS) x = xs[u][h];
+        else x = s[h] * p.c;
         if (x > m[h] + kSdRescale) {
           const float alpha = fast_exp2(m[h] - x);
           m[h] = x;
@@ -332,10 +345,11 @@ __global__ __launch_bounds__(kSdMergeThreads) void sparse_merge_kernel(SparseDec
 // Decode routing, pass 1 (kernels/bigger_bird_route.py:24-52): workgroup (split, KV head) scores its key range for
 // the G query heads (fp32, log2 units, to S [H, cap]) and keeps each head's running (max, sum) per key slot: the
 // slot's 8 lanes reduce their partial dot products scatter-wise, so that each lane ends with one head's score and
-// keeps that head's state. The slots combine into one (max, sum) per head and split. Each key slot takes four keys
-// per step (all rows in flight).
+// keeps that head's state. The slots combine into one (max, sum) per head and split. Each key slot takes eight keys
+// per step (all rows in flight: 16 KB per wave; four keys measured 2 us slower per sparse step at 131072 tokens,
+// twelve or sixteen spill).
 // Split 0 also clears the KV head's top-k histogram and counters, which the pool pass fills.
-constexpr int kRsKeysPerSlot = 4;
+constexpr int kRsKeysPerSlot = 8;
 template <int D, int G, bool F16>
 __global__ __launch_bounds__(kSdThreads) void route_scores_kernel(DecodeRouteParams p) {
   constexpr int LPK = kSlotLanes, DPL = D / LPK, KPW = 64 / LPK, SLOTS = kSdThreads / LPK;
@@ -840,7 +854,11 @@ __global__ __launch_bounds__(64 * kGvWaves) void gemv_kernel(const uint16_t* __r
 
 template <int D, int GR, bool F16>
 hipError_t launch_sparse_decode_t(const SparseDecodeParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((sparse_decode_kernel<D, GR, F16>), dim3(p.n_splits, p.rows), dim3(kSdThreads), 0, stream, p);
+  if (p.xs)
+    hipLaunchKernelGGL((sparse_decode_kernel<D, GR, F16, true>), dim3(p.n_splits, p.rows), dim3(kSdThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((sparse_decode_kernel<D, GR, F16, false>), dim3(p.n_splits, p.rows), dim3(kSdThreads), 0, stream,
+                       p);
   hipLaunchKernelGGL((sparse_merge_kernel<D, F16>), dim3(p.H), dim3(kSdMergeThreads), 0, stream, p);
   return hipGetLastError();
 }

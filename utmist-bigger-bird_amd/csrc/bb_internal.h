@@ -133,6 +133,8 @@ struct SparseDecodeParams {
   RowAppend app;         // the step's new row (dense decode without routing), or app.knew = null
   int64_t* n_advance;    // after the merge: *n_advance += advance when the row was appended (n_advance = n_dev), or null
   int64_t advance;
+  const float* xs;       // scores of this query from decode routing ([H][xs_stride], scale * log2(e) applied), or null
+  int64_t xs_stride;
 };
 hipError_t launch_sparse_decode(const SparseDecodeParams& p, hipStream_t stream);
 
