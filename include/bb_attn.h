@@ -166,7 +166,7 @@ int bb_decode_append(const void* q, int64_t sq, int8_t* k8, void* ks, int8_t* v8
 
 /*
  * bb_decode without a workspace argument and without any allocation: the split partials go to a static device array
- * of bb_decode_noalloc_max_bytes() bytes (4 MiB) inside the library, one per GPU, held until the process ends. No
+ * of bb_decode_noalloc_max_bytes() bytes (2 MiB) inside the library, one per GPU, held until the process ends. No
  * counterpart in the reference: this is for callers that cannot allocate (code under HIP graph capture, serving
  * loops, harnesses that forbid hipMalloc). Same arguments, kernels and results as bb_decode; a call whose partials
  * (H * splits * (D + 2) * 4 bytes, see bb_decode_workspace) exceed the array returns BB_EINVAL. The array of the

@@ -29,7 +29,7 @@ def _cache(n, Hkv, d, seed, dev, f16):
 @pytest.mark.parametrize("H,Hkv,d,f16,sizes", [(32, 8, 128, True, (131072, 3000)), (16, 2, 64, False, (20000, 700))])
 def test_noalloc_matches_workspace_decode(H, Hkv, d, f16, sizes, dev):
     L = _lib.lib()
-    assert L.bb_decode_noalloc_max_bytes() == 4 << 20
+    assert L.bb_decode_noalloc_max_bytes() == 2 << 20
     for i, n in enumerate(sizes):
         print(f"case decode_noalloc call {i} n={n} H={H}/{Hkv} d={d} f16={f16}", flush=True)
         k8, ks, v8, vs = _cache(n, Hkv, d, 11 + i, dev, f16)
@@ -48,7 +48,7 @@ def test_noalloc_matches_workspace_decode(H, Hkv, d, f16, sizes, dev):
 
 
 def test_noalloc_rejects_partials_beyond_the_scratch(dev):
-    """16 query heads over 2 KV heads at 128K keys need 512 splits * 16 heads * 130 floats = 4.26 MB > 4 MiB."""
+    """16 query heads over 2 KV heads at 128K keys need 256 splits * 16 heads * 130 floats = 2.13 MB > 2 MiB."""
     print("case decode_noalloc size limit", flush=True)
     L = _lib.lib()
     H, Hkv, d, n = 16, 2, 128, 131072

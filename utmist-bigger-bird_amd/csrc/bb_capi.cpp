@@ -90,7 +90,7 @@ FlashSchedule flash_schedule(int BH, int64_t T, int64_t N, int num_heads, int kv
 // caller workspace. Every GPU the library runs on holds its own copy for the life of the process; calls that overlap
 // on one GPU share it and race. Host code never passes `decode_scratch_mem` itself (that name is a host-side
 // stand-in): its device address comes from hipGetSymbolAddress, looked up once per device with that device current.
-constexpr size_t kDecodeScratchBytes = (size_t)4 << 20;
+constexpr size_t kDecodeScratchBytes = (size_t)2 << 20;
 constexpr int kMaxDevices = 64;
 static __device__ __align__(256) unsigned char decode_scratch_mem[kDecodeScratchBytes];
 std::mutex g_scratch_mu;
@@ -392,11 +392,12 @@ int bb_int8_dequantize(const int8_t* q, const void* scale, int scale_is_f16, int
                     "bb_int8_dequantize");
 }
 
-// Keys per decode workgroup: four workgroups per CU of equal length (at least 256 keys). The length is not rounded:
-// the bytes per CU, not the 32-key chunks per wave, set the time of this HBM-bound kernel (rounding 131073 keys up
-// to 1152 per split left 912 workgroups, some CUs with a third more bytes than others).
+// Keys per decode workgroup: two workgroups per CU of equal length (at least 256 keys), i.e. every workgroup resident
+// at once (two fit a CU by LDS); four per CU ran as two rounds and measured 1.2 us slower per configs[4] step. The
+// length is not rounded: the bytes per CU, not the 32-key chunks per wave, set the time of this HBM-bound kernel
+// (rounding 131073 keys up to 1152 per split left 912 workgroups, some CUs with a third more bytes than others).
 static int64_t decode_split_len(int64_t n, int Hkv) {
-  int64_t len = cdiv(n, cdiv(4 * kCUs, Hkv));
+  int64_t len = cdiv(n, cdiv(2 * kCUs, Hkv));
   return len < 256 ? 256 : len;
 }
 static int decode_splits(int64_t n, int Hkv) { return (int)cdiv(n, decode_split_len(n, Hkv)); }
