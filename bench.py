@@ -308,7 +308,8 @@ def sparse_decode_leg(dev, seed, ceiling):
     buffers (in a model they come from the projections inside the same graph). Timed eagerly, as a captured HIP
     graph of one step replayed per step, and as a graph of 8 consecutive steps (the length advances on the device,
     so 8 steps need no host work between them; a replay has a fixed cost of about 5 us that 8 steps share); bytes =
-    the K rows the routing reads + its fp32 score round trip + the K/V rows the sparse decode reads."""
+    the K rows the routing reads + its fp32 score round trip + what the sparse decode reads: the V rows of its key
+    list and their scores (the fused step's decode takes the routing pass's scores instead of re-reading K rows)."""
     import torch
     from bigger_bird_amd.decode import decode_step
 
@@ -365,7 +366,8 @@ def sparse_decode_leg(dev, seed, ceiling):
             del graph
     n_mean = n0 + (steps + 1) / 2
     route_bytes = Hkv * n_mean * d * 2 + 2 * H * n_mean * 4          # K read once + fp32 scores written and read
-    decode_bytes = Hkv * (front + window + routed) * d * 2 * 2        # K and V rows of the sparse key list
+    n_list = front + window + routed
+    decode_bytes = Hkv * n_list * d * 2 + H * n_list * 4               # V rows of the key list + their fp32 scores
     res["bytes_per_step"] = int(route_bytes + decode_bytes)
     us = min(res["eager_us_per_step"], res["graph_us_per_step"], res["graph8_us_per_step"])
     res["achieved_gbps"] = round(res["bytes_per_step"] / (us * 1e-6) / 1e9, 1)
